@@ -1,0 +1,271 @@
+"""Benchmark of the product-key-memory lookup on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Prints ONE JSON line.  Metric: "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather
+HBM GB/s".
+  value          decode tok/s of config 3 at batch 64: the 21M LM (d=384, 6 layers, vocab 32000) with the B-16M
+                 memory (4096^2 = 16,777,216 x 384 bf16 values, 12.9 GB) replacing layer 3's FFN, 128-token
+                 prompts, then K greedy steps; each step is one replay of the captured whole-step HIP graph
+                 (embedding, 6 blocks, lm_head, argmax, KV write).  value = 64 * K / time of the K steps.
+  decode_bs1     the same at batch 1.
+  pkm_lookup     config 2 (B-4M, 8 x 2048 tokens): scoring + selection + value bag kernels, tokens / time.
+  gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out;
+                 algorithmic bytes 3,439,329,280 per call; plus a uniform-index control.
+  roofline       the config-4 gather kernel against HBM peak (8 TB/s), timed with HIP events on the stream it
+                 is launched on; roofline_score: the config-2 scoring kernel against the bf16 MFMA peak.
+  cpu_baseline   the reference's PyTorch path on the host CPU (oracle/torch_path.py), config 3 at batch 64,
+                 a bounded sample of decode steps.
+All inputs are seeded synthetic data; weights are random N(0, 0.02).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "sparse-memory-lm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def lm_config(n_keys, max_seq_len):
+    from smlm_hip.model import ModelConfig
+    return ModelConfig(vocab_size=32000, d_model=384, n_layers=6, n_heads=6, ffn_hidden=1024,
+                       max_seq_len=max_seq_len, mem_layers=[3], mem_n_keys=n_keys, mem_heads=4, mem_knn=32,
+                       mem_k_dim=512)
+
+
+def build_lm(cfg, dev, seed=0):
+    """The LM with every weight matrix, the sub-keys and the value table drawn from N(0, 0.02), in bf16 on the
+    GPU (norm weights 1, BatchNorm at its initial statistics)."""
+    import torch
+    from smlm_hip.model import Transformer
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = Transformer(cfg)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() >= 2 or name.endswith("keys"):
+                p.normal_(0.0, 0.02)
+    model = model.to(torch.bfloat16).eval()
+    torch.cuda.empty_cache()
+    model.set_memory_inference_table("bf16")
+    return model
+
+
+def time_decode(model, B, steps, warmup, dev, seed=1):
+    """Prefill B uniform 128-token prompts, run `warmup` graph steps, then time `steps` graph replays."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    prompt = torch.randint(0, model.cfg.vocab_size, (B, 128), generator=g, device=dev)
+    with torch.no_grad():
+        dec = model._decoder(B, 128 + warmup + steps + 1, dev)
+        dec._capture()
+        logits = model(prompt, kv_caches=dec.caches, pos0=0)
+        dec.hist[:, :128] = prompt
+        dec.hist[:, 128] = logits[:, -1].argmax(-1)
+        dec.tok.copy_(dec.hist[:, 128:129])
+        dec.pos.fill_(128)
+        for _ in range(warmup):
+            dec.graph.replay()
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dec.graph.replay()
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+    return B * steps / dt, 1000.0 * dt / steps
+
+
+def event_time_ms(fn, reps, warm=3):
+    """Average device time of fn() in ms, from HIP events recorded on torch's current stream (the stream the
+    kernels are launched on)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def zipf_rows(n, rows, s, g, dev):
+    """n draws of Zipf(s) ranks over [0, rows) by inverse CDF, mapped through a seeded row permutation."""
+    import torch
+    cdf = torch.cumsum(torch.arange(1, rows + 1, device=dev, dtype=torch.float64).pow_(-s), 0)
+    cdf /= cdf[-1].clone()
+    u = torch.rand(n, generator=g, device=dev, dtype=torch.float64)
+    ranks = torch.searchsorted(cdf, u).clamp_(max=rows - 1)
+    del cdf, u
+    perm = torch.randperm(rows, generator=g, device=dev)
+    return perm[ranks]
+
+
+def gather_stress(dev, reps):
+    """Config 4: int8 B-16M table (per-row fp16 scales), 65,536 x 128 Zipf(1.1) lookups, fp32 out."""
+    import torch
+    from smlm_hip import kernels as K
+    rows, D, N, Kl = 4096 * 4096, 384, 65536, 128
+    g = torch.Generator(device=dev).manual_seed(0)
+    codes = torch.empty(rows, D, dtype=torch.int8, device=dev)
+    scales = torch.empty(rows, dtype=torch.float16, device=dev)
+    chunk = 1 << 21
+    for a in range(0, rows, chunk):
+        src = torch.empty(min(chunk, rows - a), D, device=dev).normal_(0.0, 0.02, generator=g)
+        c, s = K.quantize_int8(src)
+        codes[a:a + len(src)] = c
+        scales[a:a + len(src)] = s
+        del src, c, s
+    idx = zipf_rows(N * Kl, rows, 1.1, g, dev).view(N, Kl)
+    w = torch.softmax(torch.randn(N, 4, 32, generator=g, device=dev), -1).view(N, Kl)
+    uni = torch.randint(0, rows, (N, Kl), generator=g, device=dev)
+    alg_bytes = N * Kl * (D + 2 + 8 + 4) + N * D * 4          # 3,439,329,280
+    ms_zipf = event_time_ms(lambda: K.bag_infer(idx, w, codes, scales), reps)
+    ms_uni = event_time_ms(lambda: K.bag_infer(uni, w, codes, scales), reps)
+    top1k = None
+    res = {"tokens": N, "lookups_per_token": Kl, "table": "16,777,216 x 384 int8 + fp16 row scales",
+           "alg_bytes_per_call": alg_bytes, "ms_zipf": ms_zipf, "ms_uniform": ms_uni,
+           "alg_GBps_zipf": alg_bytes / ms_zipf / 1e6, "alg_GBps_uniform": alg_bytes / ms_uni / 1e6,
+           "top1000_share": top1k}
+    del codes, scales, idx, w, uni
+    torch.cuda.empty_cache()
+    return res
+
+
+def lookup_prefill(dev, reps):
+    """Config 2 PKM lookup: 8 x 2048 tokens, 4 heads x 2 halves x 2048 sub-keys of 256, top-32, 4M x 384 bf16
+    table; scoring, selection and bag kernels timed separately with HIP events."""
+    import torch
+    from smlm_hip import kernels as K
+    N, H, kd, NK, D = 8 * 2048, 4, 512, 2048, 384
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(N, H, kd, generator=g, device=dev).to(torch.bfloat16)
+    keys = (torch.randn(H, 2, NK, kd // 2, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    table = torch.empty(NK * NK, D, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=g)
+    pre = torch.randn(N, D, generator=g, device=dev).to(torch.bfloat16)
+    s1, s2 = K.pk_scores(q, keys)
+    sc, idx, w = K.pk_select(s1, s2, 32)
+    ms_score = event_time_ms(lambda: K.pk_scores(q, keys), reps)
+    ms_select = event_time_ms(lambda: K.pk_select(s1, s2, 32), reps)
+    ms_bag = event_time_ms(lambda: K.bag_infer(idx.view(N, -1), w.view(N, -1), table, pre=pre, out_bf16=True),
+                           reps)
+    flops = 2.0 * N * H * 2 * NK * (kd // 2)
+    total = ms_score + ms_select + ms_bag
+    res = {"tokens": N, "ms_score": ms_score, "ms_select": ms_select, "ms_bag": ms_bag,
+           "tok_s": N / total * 1e3, "score_TFLOPs": flops / ms_score / 1e9,
+           "bag_alg_GBps": N * 128 * (2 * D + 12) / ms_bag / 1e6}
+    del q, keys, table, pre, s1, s2, sc, idx, w
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(model, B, max_steps, budget_s):
+    """The reference's torch path (oracle/torch_path.py) on the host cores: config 3 at batch B, 128-token
+    prompts, then greedy decode steps (fp32 weights, the bf16 table read by row gather), timed until
+    `budget_s` seconds or `max_steps` steps."""
+    import torch
+    import oracle.torch_path as TP
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    sd = {}
+    for k, v in model.state_dict().items():
+        sd[k] = v.cpu() if k.endswith("values.weight") else v.float().cpu()
+    cfg = model.cfg.to_dict()
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, 128), generator=g)
+    with torch.no_grad():
+        caches = [dict() for _ in range(cfg["n_layers"])]
+        t0 = time.perf_counter()
+        nxt = TP.lm_forward(sd, cfg, prompt, caches, 0, last_only=True).argmax(-1)
+        t_prefill = time.perf_counter() - t0
+        steps = 0
+        t0 = time.perf_counter()
+        while steps < max_steps and (steps < 2 or time.perf_counter() - t0 < budget_s):
+            nxt = TP.lm_forward(sd, cfg, nxt, caches, 128 + steps).argmax(-1)
+            steps += 1
+        dt = time.perf_counter() - t0
+    del sd
+    return {"value": B * steps / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"config 3 decode at batch {B}: 128-token prompt prefill ({t_prefill:.1f} s, untimed), then "
+                      f"{steps} timed greedy steps ({dt:.1f} s) of the reference torch path (fp32 weights, "
+                      f"bf16 table)", "cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--reps", type=int, default=20, help="timed launches per kernel measurement")
+    ap.add_argument("--cpu-steps", type=int, default=64, help="most CPU-baseline decode steps")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from smlm_hip import _lib
+    dev = torch.device("cuda:0")
+    log(f"{_lib.version()} on {torch.cuda.get_device_name(dev)}")
+
+    cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
+    t0 = time.perf_counter()
+    model = build_lm(cfg, dev)
+    log(f"B-16M LM built in {time.perf_counter() - t0:.1f} s")
+    tok_s64, ms64 = time_decode(model, 64, args.steps, args.warmup, dev)
+    log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
+    tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
+    log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
+
+    lk = lookup_prefill(dev, args.reps)
+    log(f"lookup config 2: {lk}")
+    ga = gather_stress(dev, args.reps)
+    log(f"gather config 4: {ga}")
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(model, 64, args.cpu_steps, args.cpu_seconds)
+        log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f} s)")
+
+    achieved = ga["alg_GBps_zipf"]
+    line = {
+        "metric": "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather HBM GB/s",
+        "value": tok_s64, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms64, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded uniform prompt ids, random N(0,0.02) weights; Zipf(1.1) gather indices",
+        "config": {"workload": "config 3: 21M LM (d384, 6 layers, vocab 32000) + B-16M PKM at layer 3 "
+                               "(16,777,216 x 384 bf16 values), greedy decode at batch 64, 128-token prompts, "
+                               "whole-step hipGraph", "global_batch": 64, "prompt_len": 128,
+                   "new_tokens": args.steps},
+        "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
+        "pkm_lookup_config2": lk, "gather_config4": ga,
+        "roofline": {"kernel": "bag_rows_kernel<int8> (config 4 gather)", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "uniform_control_achieved": ga["alg_GBps_uniform"],
+                     "uniform_control_frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS},
+        "roofline_score": {"kernel": "score_kernel<bf16> (config 2 scoring)", "bound": "mfma",
+                           "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,108 @@
+/*
+ * smlm_pkm.h -- C ABI of the MI355X (gfx950) product-key-memory lookup.
+ *
+ * These entry points replace the forward GPU kernels of re133/sparse-memory-lm (smlm/kernels.py, Triton) and
+ * the torch einsum that feeds them (smlm/pkm.py).  Every function:
+ *   - takes plain device pointers and sizes (no framework types), plus the HIP stream to launch on
+ *     (`hipStream_t` passed as `void*`; NULL = the null stream);
+ *   - never allocates, frees, synchronises or reads device memory from the host, so a call can be recorded
+ *     into a hipGraph by stream capture;
+ *   - returns SMLM_OK (0) or a negative smlm_status; the message of the last failure on the calling thread is
+ *     returned by smlm_pkm_last_error().
+ * Buffers are caller-owned, dense and row-major.  Shapes use the reference's names: N tokens, H heads, NK
+ * sub-keys per half (table rows = NK^2), knn lookups per head, K = H*knn lookups per token, D value width.
+ */
+#ifndef SMLM_PKM_H
+#define SMLM_PKM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum smlm_status {
+  SMLM_OK = 0,
+  SMLM_EINVAL = -1,       /* bad argument: null pointer, shape, dtype or stride */
+  SMLM_EUNSUPPORTED = -2, /* valid request outside what the kernels implement */
+  SMLM_EHIP = -3          /* the HIP runtime reported an error at launch */
+} smlm_status;
+
+typedef enum smlm_dtype {
+  SMLM_F32 = 0,
+  SMLM_BF16 = 1,
+  SMLM_F16 = 2,
+  SMLM_I8 = 3,   /* int8 row-quantised table: codes (rows, D) int8 + (rows,) fp16 scales */
+  SMLM_Q4 = 4,   /* 4-bit row-quantised table: (rows, D/2) bytes + (rows,) fp16 scales */
+  SMLM_I32 = 5,
+  SMLM_I64 = 6
+} smlm_dtype;
+
+/* Library version string, e.g. "smlm_pkm 0.1.0 gfx950". */
+const char *smlm_pkm_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *smlm_pkm_last_error(void);
+
+/*
+ * Sub-key scores.  Replaces ProductKeyMemory.subkey_scores (smlm/pkm.py:117-123), the two
+ *   s1 = einsum("nhd,hkd->nhk", q[..., :half], keys[:, 0]);  s2 = einsum(..., q[..., half:], keys[:, 1])
+ * calls that feed pk_select (smlm/pkm.py:197).
+ *   q     (N, H, 2*half) of `dtype`, row n starting at q + n*q_row_stride elements (q_row_stride >= H*2*half)
+ *   keys  (H, 2, NK, half) of `dtype`, dense
+ *   s1,s2 (N, H, NK) of `dtype` (bf16: fp32 accumulation rounded to nearest even)
+ * dtype: SMLM_BF16 (MFMA bf16) or SMLM_F32 (MFMA fp32).  half % 8 == 0 (bf16) / half % 4 == 0 (fp32).
+ */
+int smlm_pkm_score(const void *q, int64_t q_row_stride, const void *keys, int dtype, int64_t N, int H, int NK,
+                   int half, void *s1, void *s2, void *stream);
+
+/*
+ * Product-key selection.  Replaces pk_select (smlm/kernels.py:214-226, kernel _pk_select_kernel 146-177) and
+ * the torch get_indices + softmax path (smlm/pkm.py:125-136, 205-208):
+ *   per (n, h): top-knn of s1[n,h,:] and of s2[n,h,:] (ties -> lower sub-key index), candidates (i, j) with
+ *   (i+1)(j+1) <= knn scored as dtype(v1[i] + v2[j]), top-knn of those (ties -> lower table index
+ *   i1*NK + i2), softmax in fp32.
+ *   s1,s2   (N, H, NK) of `dtype` (SMLM_BF16 or SMLM_F32)
+ *   scores  (N, H, knn) of `dtype`, descending
+ *   idx     (N, H, knn) int64 table rows in [0, NK^2)
+ *   w       (N, H, knn) fp32 softmax weights
+ * NK a power of two in [knn, 65536]; knn a power of two in [1, 64].
+ */
+int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_t N, int H, int NK, int knn, void *scores,
+                    int64_t *idx, float *w, void *stream);
+
+/*
+ * Weighted value bag.  Replaces bag_forward (smlm/kernels.py:229-237) and bag_infer (smlm/kernels.py:364-378):
+ *   out[n, :] = sum_{j<K} w[n, j] * row(idx[n, j])        (fp32 accumulation)
+ * with row() = table row for SMLM_F32 / SMLM_BF16 tables and scale[r] * code[r, :] for SMLM_I8 / SMLM_Q4 tables
+ * (the lookup weight is multiplied by the row scale first, as kernels.py:328-335 does for q4).
+ *   idx     (N, K) of idx_dtype (SMLM_I64 or SMLM_I32), rows in [0, rows)
+ *   w       (N, K) fp32
+ *   table   (rows, D) f32/bf16, (rows, D) int8 codes, or (rows, D/2) q4 bytes (byte i: column i in the low
+ *           nibble, column i + D/2 in the high nibble, each stored as code + 8)
+ *   scales  (rows,) fp16 bits for SMLM_I8 / SMLM_Q4, else NULL
+ *   pre     (N, D) bf16 bits or NULL; if given, out *= bf16(silu(pre)) (smlm/pkm.py:213-224 swilu epilogue)
+ *   out     (N, D) of out_dtype (SMLM_F32, or SMLM_BF16 rounded to nearest even)
+ * An index outside [0, rows) does not fault: that token's whole output row is written as NaN.
+ */
+int smlm_pkm_bag(const void *idx, int idx_dtype, const float *w, int64_t N, int K, const void *table,
+                 int table_dtype, int64_t rows, int D, const uint16_t *scales, const uint16_t *pre, void *out,
+                 int out_dtype, void *stream);
+
+/*
+ * Row quantisation of a value table for the inference bag.  Replaces quantize_q4 (smlm/kernels.py:280-300)
+ * and gives the int8 scheme of scripts/quantize_table_eval.py:55-61 a device implementation:
+ *   m = the row's value of largest magnitude (first on ties); d = fp16(m / lo) (1 if that is 0);
+ *   code = clamp(round_half_even(w / d), lo, hi), with (lo, hi) = (-128, 127) for SMLM_I8, (-8, 7) for SMLM_Q4.
+ *   src     (rows, D) of src_dtype (SMLM_F32 or SMLM_BF16)
+ *   codes   (rows, D) int8 for SMLM_I8; (rows, D/2) bytes for SMLM_Q4 (D even)
+ *   scales  (rows,) fp16 bits
+ */
+int smlm_pkm_quantize(const void *src, int src_dtype, int64_t rows, int D, int kind, void *codes,
+                      uint16_t *scales, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SMLM_PKM_H */

@@ -1,0 +1,128 @@
+"""Reference PyTorch path on the CPU -- TEST INFRASTRUCTURE ONLY (the LM-level checker and the timed CPU
+baseline of bench.py; the product path never calls it).
+
+A functional restatement of the reference's torch implementation, driven by a state_dict with the
+reference's key names:
+  pkm_forward     smlm/pkm.py:117-148, 186-228 with impl="torch": query_proj, BatchNorm (eval), two einsums,
+                  topk per half, Cartesian topk over all knn^2 sums, softmax, F.embedding_bag, swilu
+  lm_forward      smlm/model.py:63-118, 156-163, 266-293: RMSNorm, RoPE, causal attention with a dict KV cache,
+                  SwiGLU, tied lm_head
+  greedy_decode   the decode loop of smlm/train.py:283-301 (prefill, then one token per step, argmax)
+Everything runs in the dtype of the given weights (fp32 or fp64).  torch.topk breaks ties in an unspecified
+order, exactly like the reference's torch path; on tie-free scores it selects what pk_select selects.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def rms_norm(x, w, eps):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+def rope(x, pos0, theta):
+    hd = x.shape[-1]
+    T = x.shape[-2]
+    inv = 1.0 / (theta ** (torch.arange(0, hd, 2, dtype=torch.float32) / hd))
+    ang = torch.outer(torch.arange(pos0, pos0 + T, dtype=torch.float32), inv)
+    cos, sin = ang.cos().to(x.dtype), ang.sin().to(x.dtype)
+    a, b = x[..., :hd // 2], x[..., hd // 2:]
+    return torch.cat([a * cos - b * sin, a * sin + b * cos], dim=-1)
+
+
+def attention(sd, p, x, cfg, cache, pos0):
+    B, T, C = x.shape
+    H = cfg["n_heads"]
+    hd = C // H
+    qkv = (x @ sd[p + "wqkv.weight"].T).view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4)
+    q, k, v = rope(qkv[0], pos0, cfg["rope_theta"]), rope(qkv[1], pos0, cfg["rope_theta"]), qkv[2]
+    if cache is not None:
+        if "k" in cache:
+            k = torch.cat([cache["k"], k], 2)
+            v = torch.cat([cache["v"], v], 2)
+        cache["k"], cache["v"] = k, v
+    S = k.shape[2]
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(hd)
+    if T > 1:
+        mask = torch.ones(T, S, dtype=torch.bool).tril(S - T)
+        s = s.masked_fill(~mask, float("-inf"))
+    y = torch.softmax(s, -1) @ v
+    return y.transpose(1, 2).reshape(B, T, C) @ sd[p + "wo.weight"].T
+
+
+def pkm_select_torch(s1, s2, knn):
+    """get_indices of smlm/pkm.py:125-136 on given sub-key scores (N, H, NK)."""
+    N, H, NK = s1.shape
+    a1, i1 = s1.topk(knn, -1)
+    a2, i2 = s2.topk(knn, -1)
+    alls = (a1.unsqueeze(-1) + a2.unsqueeze(-2)).reshape(N, H, knn * knn)
+    alli = (i1.unsqueeze(-1) * NK + i2.unsqueeze(-2)).reshape(N, H, knn * knn)
+    sc, best = alls.topk(knn, -1)
+    return sc, alli.gather(-1, best)
+
+
+def pkm_forward(sd, p, x, mcfg, table=None):
+    """One memory layer: x (N, d_in) -> (N, d_out).  mcfg: heads, knn, k_dim, n_keys, query_norm, swilu, eps.
+    `table` overrides the value table (e.g. a dequantised inference table)."""
+    N = x.shape[0]
+    H, knn, k_dim = mcfg["heads"], mcfg["knn"], mcfg["k_dim"]
+    q = x @ sd[p + "query_proj.weight"].T + sd[p + "query_proj.bias"]
+    if mcfg["query_norm"] == "batchnorm":
+        q = (q - sd[p + "query_norm.running_mean"]) / torch.sqrt(sd[p + "query_norm.running_var"] + 1e-5)
+        q = q * sd[p + "query_norm.weight"] + sd[p + "query_norm.bias"]
+    q = q.view(N, H, k_dim)
+    keys = sd[p + "keys"]
+    half = k_dim // 2
+    s1 = torch.einsum("nhd,hkd->nhk", q[..., :half], keys[:, 0])
+    s2 = torch.einsum("nhd,hkd->nhk", q[..., half:], keys[:, 1])
+    scores, idx = pkm_select_torch(s1, s2, knn)
+    w = torch.softmax(scores, -1)
+    values = sd[p + "values.weight"] if table is None else table
+    if values.dtype == x.dtype:
+        out = F.embedding_bag(idx.view(N, -1), values, per_sample_weights=w.view(N, -1), mode="sum")
+    else:
+        # a table stored in another dtype (bf16): the reference's value_impl="gather" form (smlm/pkm.py:147-148)
+        out = torch.einsum("nj,njd->nd", w.view(N, -1), F.embedding(idx.view(N, -1), values).to(x.dtype))
+    if mcfg["swilu"]:
+        pre = x @ sd[p + "swilu_proj.weight"].T + sd[p + "swilu_proj.bias"]
+        out = (out * F.silu(pre)) @ sd[p + "value_proj.weight"].T + sd[p + "value_proj.bias"]
+    return out
+
+
+def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False):
+    """Logits (B, T, vocab) of the decoder with the memory layers cfg["mem_layers"] (only the last position's,
+    (B, 1, vocab), with last_only)."""
+    x = sd["tok_emb.weight"][idx]
+    mcfg = dict(heads=cfg["mem_heads"], knn=cfg["mem_knn"], k_dim=cfg["mem_k_dim"], n_keys=cfg["mem_n_keys"],
+                query_norm=cfg["mem_query_norm"], swilu=cfg["mem_swilu"])
+    eps = cfg["norm_eps"]
+    for i in range(cfg["n_layers"]):
+        p = f"layers.{i}."
+        x = x + attention(sd, p + "attn.", rms_norm(x, sd[p + "attn_norm.weight"], eps), cfg,
+                          None if caches is None else caches[i], pos0)
+        h = rms_norm(x, sd[p + "ffn_norm.weight"], eps)
+        if i in cfg["mem_layers"]:
+            B, T, C = h.shape
+            t = None if tables is None else tables.get(i)
+            x = x + pkm_forward(sd, p + "ffn.", h.reshape(B * T, C), mcfg, t).view(B, T, -1)
+        else:
+            a, b = (h @ sd[p + "ffn.w13.weight"].T).chunk(2, -1)
+            x = x + (F.silu(a) * b) @ sd[p + "ffn.w2.weight"].T
+    if last_only:
+        x = x[:, -1:]
+    return rms_norm(x, sd["norm.weight"], eps) @ sd["tok_emb.weight"].T
+
+
+def greedy_decode(sd, cfg, prompt, new_tokens):
+    """Prefill + new_tokens greedy steps with a dict KV cache -> generated ids (B, new_tokens + 1)."""
+    caches = [dict() for _ in range(cfg["n_layers"])]
+    logits = lm_forward(sd, cfg, prompt, caches, 0)
+    nxt = logits[:, -1:].argmax(-1)
+    out = [nxt]
+    P = prompt.shape[1]
+    for i in range(new_tokens):
+        logits = lm_forward(sd, cfg, nxt, caches, P + i)
+        nxt = logits[:, -1:].argmax(-1)
+        out.append(nxt)
+    return torch.cat(out, 1)

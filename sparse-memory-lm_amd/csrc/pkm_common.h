@@ -1,0 +1,62 @@
+// Shared helpers of the gfx950 product-key-memory kernels: bit-exact bf16 rounding, order-preserving score
+// codes, wavefront primitives and the error state of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "smlm_pkm.h"
+
+namespace smlm {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---- error state (one message per host thread) -------------------------------------------------------------
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int launch_status(const char *what);  // hipGetLastError() after a launch -> SMLM_OK / SMLM_EHIP
+void clear_error();
+
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// ---- number formats ------------------------------------------------------------------------------------------
+// fp32 -> bf16 bit pattern, round to nearest even, done on the integer bits so that every device and the CPU
+// oracle round identically (the convention of smlm/kernels.py:106-112).
+__device__ __forceinline__ uint32_t bf16_bits_rtne(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = u + 0x7FFFu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float round_bf16(float x) { return bf16_bits_to_f32(bf16_bits_rtne(x)); }
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+// fp32 -> fp16 bit pattern, round to nearest even (v_cvt_f16_f32)
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+
+// Order-preserving unsigned codes: a > b as floats  <=>  code(a) > code(b) as unsigned integers, with -0 ranked
+// just below +0 (the convention of smlm/kernels.py:114-126).
+__device__ __forceinline__ uint32_t order16(uint32_t b) { return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u); }
+__device__ __forceinline__ uint32_t unorder16(uint32_t o) { return (o & 0x8000u) ? (o ^ 0x8000u) : (~o & 0xFFFFu); }
+__device__ __forceinline__ uint32_t order32(uint32_t u) { return (u & 0x80000000u) ? ~u : (u | 0x80000000u); }
+__device__ __forceinline__ uint32_t unorder32(uint32_t o) { return (o & 0x80000000u) ? (o ^ 0x80000000u) : ~o; }
+
+// ---- wavefront primitives --------------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+// number of set bits of `mask` below this lane
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+}
+// Orders this wave's LDS accesses for the compiler; the LDS itself executes one wave's instructions in order.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+}  // namespace smlm

@@ -1,0 +1,73 @@
+"""ctypes binding of the C ABI in include/smlm_pkm.h (libsmlm_pkm.so, built by smlm_hip.build).
+
+torch is imported first on purpose: torch's ROCm wheel ships its own libamdhip64.so.7, and loading it before
+libsmlm_pkm.so makes the library bind to that same HIP runtime, so the stream handles torch hands out are
+valid in our launches.  There is no fallback: if the library is missing, every op raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (see module docstring)
+
+LIB_NAME = "libsmlm_pkm.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+# smlm_dtype / smlm_status values of include/smlm_pkm.h
+F32, BF16, F16, I8, Q4, I32, I64 = range(7)
+OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
+
+_p, _i, _i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+
+# name -> (restype, argtypes); every function declared in include/smlm_pkm.h
+EXPORTS = {
+    "smlm_pkm_version": (ctypes.c_char_p, []),
+    "smlm_pkm_last_error": (ctypes.c_char_p, []),
+    "smlm_pkm_score": (_i, [_p, _i64, _p, _i, _i64, _i, _i, _i, _p, _p, _p]),
+    "smlm_pkm_select": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
+    "smlm_pkm_bag": (_i, [_p, _i, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p]),
+    "smlm_pkm_quantize": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
+}
+
+_lib = None
+
+
+class SmlmError(RuntimeError):
+    """A C-ABI call returned an error code."""
+
+    def __init__(self, what, code, message):
+        super().__init__(f"{what} failed with status {code}: {message}")
+        self.code = code
+
+
+def lib():
+    """The loaded library (loaded once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run `python -m smlm_hip.build` in sparse-memory-lm_amd/ "
+                               "or __graft_entry__.build()); the HIP kernels have no fallback")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in EXPORTS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def version():
+    return lib().smlm_pkm_version().decode()
+
+
+def last_error():
+    return lib().smlm_pkm_last_error().decode()
+
+
+def check(rc, what):
+    if rc != OK:
+        raise SmlmError(what, rc, last_error())
+
+
+def stream_handle(device):
+    """hipStream_t (as int) of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream

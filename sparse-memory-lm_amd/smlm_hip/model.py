@@ -1,0 +1,371 @@
+"""Llama-style decoder with product-key memory layers: the entry points of smlm/model.py (ModelConfig,
+Transformer.forward(idx, targets, kv_caches, pos0), set_memory_decode_graphs, set_memory_inference_table),
+with the memory layers on the gfx950 lookup of smlm_hip.pkm, plus a whole-decode-step HIP graph
+(Transformer.generate) over a static KV cache.
+
+The dense parts (RMSNorm, RoPE, SDPA attention, SwiGLU, tied lm_head) are PyTorch ops with the reference's
+arithmetic; state_dict keys are the reference's, so a reference checkpoint of a supported config loads as is.
+"""
+import math
+from dataclasses import asdict, dataclass, field
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import kernels
+from .pkm import ProductKeyMemory
+
+
+@dataclass
+class ModelConfig:
+    """Fields and defaults of smlm/model.py:13-60 (mem_impl defaults to "hip")."""
+    vocab_size: int = 50304
+    d_model: int = 384
+    n_layers: int = 12
+    n_heads: int = 6
+    ffn_hidden: int = 1024
+    max_seq_len: int = 1024
+    rope_theta: float = 10000.0
+    norm_eps: float = 1e-5
+    init_std: float = 0.02
+    mem_layers: list = field(default_factory=list)
+    mem_n_keys: int = 512
+    mem_heads: int = 4
+    mem_knn: int = 32
+    mem_k_dim: int = 256
+    mem_v_dim: int = -1
+    mem_query_norm: str = "batchnorm"
+    mem_swilu: bool = True
+    mem_value_impl: str = "embedding_bag"
+    mem_keys_weight_decay: bool = True
+    mem_score_scale: str = "none"
+    mem_score_scale_init: float = 1.0
+    mem_share_values: bool = False
+    mem_round_layers: list = field(default_factory=list)
+    mem_value_grad: str = "dense"
+    mem_impl: str = "hip"
+    eng_layers: list = field(default_factory=list)
+    eng_orders: list = field(default_factory=lambda: [2, 3])
+    eng_heads: int = 8
+    eng_head_dim: int = 24
+    eng_rows: int = 524287
+    eng_conv_kernel: int = 4
+    eng_hash_seed: int = 0
+    eng_impl: str = "triton"
+    eng_value_grad: str = "row_sparse"
+
+    def to_dict(self):
+        return asdict(self)
+
+
+class RotaryEmbedding(nn.Module):
+    """RoPE on the two halves of each head (smlm/model.py:63-78).  pos0 is an int, or a 0-d / 1-element
+    device tensor (single-token decode inside a captured graph)."""
+
+    def __init__(self, head_dim, max_seq_len, theta):
+        super().__init__()
+        inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+        ang = torch.outer(torch.arange(max_seq_len).float(), inv)
+        self.register_buffer("cos", ang.cos(), persistent=False)
+        self.register_buffer("sin", ang.sin(), persistent=False)
+
+    def forward(self, x, pos0=0):
+        if torch.is_tensor(pos0):
+            cos = self.cos.index_select(0, pos0.view(1)).to(x.dtype)
+            sin = self.sin.index_select(0, pos0.view(1)).to(x.dtype)
+        else:
+            T = x.shape[-2]
+            cos = self.cos[pos0:pos0 + T].to(x.dtype)
+            sin = self.sin[pos0:pos0 + T].to(x.dtype)
+        a, b = x.chunk(2, dim=-1)
+        return torch.cat([a * cos - b * sin, a * sin + b * cos], dim=-1)
+
+
+class StaticKVCache:
+    """Preallocated (B, heads, max_len, head_dim) key/value buffers of one attention layer, written in place, so
+    a decode step has fixed shapes and addresses and can be captured in a HIP graph."""
+
+    def __init__(self, B, n_heads, max_len, head_dim, dtype, device):
+        self.k = torch.zeros(B, n_heads, max_len, head_dim, dtype=dtype, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.slots = torch.arange(max_len, device=device)
+        self.max_len = max_len
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.n_heads = cfg.n_heads
+        self.head_dim = cfg.d_model // cfg.n_heads
+        self.wqkv = nn.Linear(cfg.d_model, 3 * cfg.d_model, bias=False)
+        self.wo = nn.Linear(cfg.d_model, cfg.d_model, bias=False)
+        self.rope = RotaryEmbedding(self.head_dim, cfg.max_seq_len, cfg.rope_theta)
+
+    def forward(self, x, kv_cache=None, pos0=0):
+        B, T, C = x.shape
+        q, k, v = self.wqkv(x).view(B, T, 3, self.n_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        q, k = self.rope(q, pos0), self.rope(k, pos0)
+        if isinstance(kv_cache, StaticKVCache):
+            y = self._static(q, k, v, kv_cache, pos0)
+        else:
+            if kv_cache is not None:
+                if kv_cache.get("k") is not None:
+                    k = torch.cat([kv_cache["k"], k], dim=2)
+                    v = torch.cat([kv_cache["v"], v], dim=2)
+                kv_cache["k"], kv_cache["v"] = k, v
+            y = _attention(q, k, v, _causal_mask(q.shape[2], k.shape[2], q.device))
+        return self.wo(y.transpose(1, 2).reshape(B, T, C))
+
+    def _static(self, q, k, v, cache, pos0):
+        T = q.shape[2]
+        if torch.is_tensor(pos0):
+            # one token at a device-side position: write the slot, attend over the filled prefix
+            if T != 1:
+                raise ValueError("a device-side position is for single-token decode steps")
+            cache.k.index_copy_(2, pos0.view(1), k)
+            cache.v.index_copy_(2, pos0.view(1), v)
+            return _attention(q, cache.k, cache.v, (cache.slots <= pos0).view(1, 1, 1, -1))
+        cache.k[:, :, pos0:pos0 + T] = k
+        cache.v[:, :, pos0:pos0 + T] = v
+        S = pos0 + T
+        return _attention(q, cache.k[:, :, :S], cache.v[:, :, :S], _causal_mask(T, S, q.device))
+
+
+def _causal_mask(T, S, device):
+    """Token i of T new tokens after S - T cached ones sees keys 0 .. S - T + i (None: sees everything)."""
+    if T == 1:
+        return None
+    return torch.ones(T, S, dtype=torch.bool, device=device).tril(S - T)
+
+
+def _attention(q, k, v, mask):
+    """softmax(q k^T / sqrt(head_dim), masked) v for q (B, H, T, hd), k, v (B, H, S, hd); softmax in fp32.
+    Both products are bmm calls whose right operand is contiguous (single-token steps compute k q, so the
+    cache is never transposed)."""
+    B, H, T, hd = q.shape
+    S = k.shape[2]
+    if T == 1:
+        s = torch.bmm(k.reshape(B * H, S, hd), q.reshape(B * H, hd, 1)).view(B, H, 1, S)
+    else:
+        kt = k.reshape(B * H, S, hd).transpose(1, 2).contiguous()
+        s = torch.bmm(q.reshape(B * H, T, hd), kt).view(B, H, T, S)
+    s = s.float() * (hd ** -0.5)
+    if mask is not None:
+        s = s.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(s, dim=-1).to(v.dtype)
+    y = torch.bmm(p.view(B * H, T, S), v.reshape(B * H, S, hd).contiguous())
+    return y.view(B, H, T, hd)
+
+
+class SwiGLU(nn.Module):
+    def __init__(self, d, hidden):
+        super().__init__()
+        self.w13 = nn.Linear(d, 2 * hidden, bias=False)
+        self.w2 = nn.Linear(hidden, d, bias=False)
+
+    def forward(self, x):
+        a, b = self.w13(x).chunk(2, dim=-1)
+        return self.w2(F.silu(a) * b)
+
+
+def _memory(cfg, shared):
+    return ProductKeyMemory(
+        cfg.d_model, cfg.d_model, n_keys=cfg.mem_n_keys, heads=cfg.mem_heads, knn=cfg.mem_knn, k_dim=cfg.mem_k_dim,
+        v_dim=cfg.mem_v_dim, query_norm=cfg.mem_query_norm, swilu=cfg.mem_swilu, value_impl=cfg.mem_value_impl,
+        keys_weight_decay=cfg.mem_keys_weight_decay, score_scale=cfg.mem_score_scale,
+        score_scale_init=cfg.mem_score_scale_init, shared_values=shared, value_grad=cfg.mem_value_grad,
+        impl=cfg.mem_impl)
+
+
+class Block(nn.Module):
+    def __init__(self, cfg, layer_id, shared_values=None):
+        super().__init__()
+        self.attn_norm = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
+        self.attn = Attention(cfg)
+        self.ffn_norm = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
+        self.is_memory = layer_id in cfg.mem_layers
+        self.ffn = _memory(cfg, shared_values) if self.is_memory else SwiGLU(cfg.d_model, cfg.ffn_hidden)
+        self.ffn_r2 = None
+        if layer_id in cfg.mem_round_layers:
+            if not (self.is_memory and shared_values is not None):
+                raise ValueError("a second read needs a memory layer with a shared value table")
+            self.ffn_norm_r2 = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
+            self.ffn_r2 = _memory(cfg, shared_values)
+
+    def forward(self, x, kv_cache=None, pos0=0):
+        x = x + self.attn(self.attn_norm(x), kv_cache, pos0)
+        x = x + self.ffn(self.ffn_norm(x))
+        if self.ffn_r2 is not None:
+            x = x + self.ffn_r2(self.ffn_norm_r2(x))
+        return x
+
+
+class Transformer(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        if cfg.eng_layers:
+            raise NotImplementedError("Engram layers are not part of the product-key lookup build")
+        self.cfg = cfg
+        self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        shared = None
+        if cfg.mem_share_values and cfg.mem_layers:
+            shared = nn.Embedding(cfg.mem_n_keys ** 2, cfg.mem_v_dim if cfg.mem_v_dim > 0 else cfg.d_model)
+        self.layers = nn.ModuleList([Block(cfg, i, shared) for i in range(cfg.n_layers)])
+        self.norm = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
+        self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
+        self.lm_head.weight = self.tok_emb.weight
+        self._decoders = {}
+        self._init_weights()
+
+    @torch.no_grad()
+    def _init_weights(self):
+        """The reference's initialisation (smlm/model.py:196-206); memory layers keep their own."""
+        std = self.cfg.init_std
+        out_std = std / math.sqrt(2 * self.cfg.n_layers)
+        self.tok_emb.weight.normal_(0.0, std)
+        for blk in self.layers:
+            blk.attn.wqkv.weight.normal_(0.0, std)
+            blk.attn.wo.weight.normal_(0.0, out_std)
+            if not blk.is_memory:
+                blk.ffn.w13.weight.normal_(0.0, std)
+                blk.ffn.w2.weight.normal_(0.0, out_std)
+
+    def memory_layers(self):
+        """All product-key reads in forward order (a second read follows its layer's first)."""
+        out = []
+        for b in self.layers:
+            if b.is_memory:
+                out.append(b.ffn)
+                if b.ffn_r2 is not None:
+                    out.append(b.ffn_r2)
+        return out
+
+    def memory_sites(self):
+        out = []
+        for i, b in enumerate(self.layers):
+            if b.is_memory:
+                out.append(f"L{i}")
+                if b.ffn_r2 is not None:
+                    out.append(f"L{i}r2")
+        return out
+
+    def set_memory_decode_graphs(self, enabled=True):
+        """No-grad forwards of the memory layers replay a captured HIP graph per input shape."""
+        for m in self.memory_layers():
+            m.decode_graph = enabled
+            m._graph = None
+
+    @torch.no_grad()
+    def set_memory_inference_table(self, kind="fp32"):
+        """Inference copy of the value table(s) read by the fused bf16 bag: "fp32" (the weights themselves),
+        "bf16", "q4" (4 bit + fp16 row scale) or "int8" (8 bit + fp16 row scale).  Call again after the weights
+        change; captured graphs are dropped."""
+        seen = set()
+        for m in self.memory_layers():
+            m._graph = None
+            v = m.values
+            if id(v) in seen:
+                continue
+            seen.add(id(v))
+            w = v.weight.detach()
+            if kind == "fp32":
+                v.infer_table = None
+            elif kind == "bf16":
+                v.infer_table = (w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16), None)
+            elif kind == "q4":
+                v.infer_table = kernels.quantize_q4(w)
+            elif kind == "int8":
+                v.infer_table = kernels.quantize_int8(w)
+            else:
+                raise ValueError(kind)
+        self._decoders.clear()
+
+    def forward(self, idx, targets=None, kv_caches=None, pos0=0):
+        """Logits (B, T, vocab), or (logits, loss) with targets (smlm/model.py:266-293)."""
+        x = self.tok_emb(idx)
+        for i, blk in enumerate(self.layers):
+            x = blk(x, None if kv_caches is None else kv_caches[i], pos0)
+        logits = self.lm_head(self.norm(x))
+        if targets is None:
+            return logits
+        loss = F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.reshape(-1))
+        return logits, loss
+
+    # ---- whole-step graph decode -------------------------------------------------------------------------
+    @torch.no_grad()
+    def generate(self, prompt, new_tokens, use_graph=True, sync_every_step=False):
+        """Greedy decoding: prefill `prompt` (B, P) into a static KV cache, then `new_tokens` single-token
+        steps, each one forward + argmax (the loop of smlm/train.py:283-301).  With use_graph the whole step
+        (embedding, every block, lm_head, argmax, cache write, position update) is one HIP graph replay.
+        Returns the generated ids (B, new_tokens + 1): the prompt's next token, then one per step."""
+        B, P = prompt.shape
+        dec = self._decoder(B, P + new_tokens + 1, prompt.device)
+        tokens = dec.run(prompt, new_tokens, use_graph, sync_every_step)
+        return tokens
+
+    def _decoder(self, B, max_len, device):
+        key = (B, max_len, str(device), torch.is_autocast_enabled("cuda"), torch.get_autocast_dtype("cuda"))
+        if key not in self._decoders:
+            self._decoders[key] = _StepDecoder(self, B, max_len, device)
+        return self._decoders[key]
+
+
+class _StepDecoder:
+    """Static buffers and the captured graph of one decode step for batch B, sequences up to max_len."""
+
+    def __init__(self, model, B, max_len, device):
+        cfg = model.cfg
+        if max_len > cfg.max_seq_len:
+            raise ValueError(f"prompt + new tokens = {max_len} exceed max_seq_len = {cfg.max_seq_len}")
+        self.model, self.B, self.max_len = model, B, max_len
+        dtype = model.tok_emb.weight.dtype
+        if torch.is_autocast_enabled("cuda"):
+            dtype = torch.get_autocast_dtype("cuda")
+        hd = cfg.d_model // cfg.n_heads
+        self.caches = [StaticKVCache(B, cfg.n_heads, max_len, hd, dtype, device) for _ in range(cfg.n_layers)]
+        self.tok = torch.zeros(B, 1, dtype=torch.long, device=device)
+        self.pos = torch.zeros((), dtype=torch.long, device=device)
+        self.hist = torch.zeros(B, max_len, dtype=torch.long, device=device)
+        self.graph = None
+
+    def _step(self):
+        logits = self.model(self.tok, kv_caches=self.caches, pos0=self.pos)
+        nxt = logits[:, -1].argmax(-1, keepdim=True)
+        self.hist.index_copy_(1, (self.pos + 1).view(1), nxt)
+        self.tok.copy_(nxt)
+        self.pos.add_(1)
+
+    def _capture(self):
+        ac = torch.is_autocast_enabled("cuda")
+        ctx = (torch.autocast("cuda", dtype=torch.get_autocast_dtype("cuda"), cache_enabled=False) if ac
+               else torch.autocast("cuda", enabled=False))
+        self.pos.fill_(0)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), ctx:
+            for _ in range(2):                      # warm-up: library loads, cached casts, allocator
+                self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph), ctx:
+            self._step()
+        self.graph = graph
+
+    def run(self, prompt, new_tokens, use_graph, sync_every_step):
+        B, P = prompt.shape
+        if use_graph and self.graph is None:
+            self._capture()
+        logits = self.model(prompt, kv_caches=self.caches, pos0=0)
+        self.hist[:, :P] = prompt
+        self.hist[:, P] = logits[:, -1].argmax(-1)
+        self.tok.copy_(self.hist[:, P:P + 1])
+        self.pos.fill_(P)
+        for _ in range(new_tokens):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self._step()
+            if sync_every_step:
+                torch.cuda.current_stream().synchronize()
+        return self.hist[:, P:P + new_tokens + 1].clone()

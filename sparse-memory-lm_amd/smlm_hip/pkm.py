@@ -1,0 +1,227 @@
+"""Product-key memory layer with the module API of smlm/pkm.py (constructor, parameters and state_dict keys,
+forward, get_indices, subkey_scores, read_values, score_scale, macs_per_token, record / last_* and the decode
+graph switch), whose lookup runs on the gfx950 kernels of smlm_hip.kernels:
+
+    query_proj -> BatchNorm (fp32, eval statistics) -> pk_scores (MFMA) -> pk_select -> softmax
+    -> bag_infer (value gather, swilu epilogue, bf16 out) -> value_proj
+
+impl="hip" is the only implementation here; the reference's "torch" and "triton" implementations stay in the
+reference package.  The module is inference-only: a forward that autograd would record raises.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import kernels
+
+
+def _pow2(n):
+    return n > 0 and n & (n - 1) == 0
+
+
+def _autocast_bf16(x):
+    return x.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+
+
+class ProductKeyMemory(nn.Module):
+    """Same constructor as smlm/pkm.py:33-92 (impl defaults to "hip")."""
+
+    def __init__(self, d_in, d_out, n_keys=512, heads=4, knn=32, k_dim=256, v_dim=-1,
+                 query_norm="batchnorm", swilu=True, value_impl="embedding_bag",
+                 keys_weight_decay=True, score_scale="none", score_scale_init=1.0, shared_values=None,
+                 value_grad="dense", impl="hip"):
+        super().__init__()
+        if k_dim % 2 or knn > n_keys:
+            raise ValueError(f"k_dim must be even and knn <= n_keys, got k_dim={k_dim}, knn={knn}, n_keys={n_keys}")
+        if impl != "hip":
+            raise ValueError(f"smlm_hip runs mem_impl='hip' only, got {impl!r}; the 'torch' and 'triton' "
+                             "implementations are the reference package's")
+        if not (_pow2(n_keys) and n_keys <= 65536 and _pow2(knn) and knn <= 64):
+            # the selection kernel packs sub-key indices into 16 bits and keeps one selected entry per lane
+            raise ValueError(f"mem_impl='hip' needs n_keys and knn to be powers of two, n_keys <= 65536 and "
+                             f"knn <= 64, got n_keys={n_keys}, knn={knn}.")
+        if value_grad not in ("dense", "row_sparse"):
+            raise ValueError(value_grad)
+        self.d_in, self.d_out = d_in, d_out
+        self.n_keys, self.heads, self.knn, self.k_dim = n_keys, heads, knn, k_dim
+        self.size = n_keys ** 2
+        self.v_dim = v_dim if v_dim > 0 else d_out
+        self.swilu = swilu
+        self.value_impl = value_impl
+        self.value_grad = value_grad
+        self.impl = impl
+        self.score_scale_init = score_scale_init
+
+        self.keys = nn.Parameter(torch.empty(heads, 2, n_keys, k_dim // 2))
+        if not keys_weight_decay:
+            self.keys.no_weight_decay = True
+        if score_scale == "learned":
+            if score_scale_init <= 0:
+                raise ValueError("score_scale_init must be > 0")
+            self.log_score_scale = nn.Parameter(torch.empty(heads))
+        elif score_scale == "none":
+            self.log_score_scale = None
+        else:
+            raise ValueError(score_scale)
+        self.query_proj = nn.Linear(d_in, heads * k_dim, bias=True)
+        if query_norm == "batchnorm":
+            self.query_norm = nn.BatchNorm1d(heads * k_dim)
+        elif query_norm == "none":
+            self.query_norm = None
+        else:
+            raise ValueError(query_norm)
+        if shared_values is not None:
+            if tuple(shared_values.weight.shape) != (self.size, self.v_dim):
+                raise ValueError(f"shared value table must be ({self.size}, {self.v_dim}), got "
+                                 f"{tuple(shared_values.weight.shape)}")
+            self.values = shared_values
+        else:
+            self.values = nn.Embedding(self.size, self.v_dim)
+        if swilu:
+            self.swilu_proj = nn.Linear(d_in, self.v_dim)
+            self.value_proj = nn.Linear(self.v_dim, d_out)
+        elif self.v_dim != d_out:
+            raise ValueError("without swilu the value width must equal d_out")
+        self.record = False
+        self.last_indices = None
+        self.last_scores = None
+        self.last_weights = None
+        self.decode_graph = False
+        self._graph = None
+        self._keys_cache = None
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        """The reference's initialisation (smlm/pkm.py:94-109)."""
+        lim = 1.0 / math.sqrt(self.k_dim)
+        self.keys.uniform_(-lim, lim)
+        self.values.weight.normal_(0.0, self.v_dim ** -0.5)
+        nn.init.xavier_uniform_(self.query_proj.weight)
+        self.query_proj.bias.zero_()
+        if self.swilu:
+            std = self.d_out ** -0.5
+            self.swilu_proj.weight.normal_(0.0, std)
+            self.value_proj.weight.normal_(0.0, std)
+            self.swilu_proj.bias.zero_()
+            self.value_proj.bias.zero_()
+        if self.log_score_scale is not None:
+            self.log_score_scale.fill_(math.log(self.score_scale_init))
+        self.values.weight.pk_value_param = True
+
+    def score_scale(self):
+        """Per-head multiplier of the selected scores before the softmax (ones if disabled)."""
+        if self.log_score_scale is None:
+            return torch.ones(self.heads, device=self.keys.device)
+        return self.log_score_scale.exp()
+
+    # ---- lookup pieces -----------------------------------------------------------------------------------
+    def _keys_as(self, dtype):
+        """The sub-keys in the scoring dtype; a cast copy is cached until the parameter changes."""
+        k = self.keys
+        if k.dtype == dtype:
+            return k.detach()
+        tag = (k.data_ptr(), k._version, dtype)
+        if self._keys_cache is None or self._keys_cache[0] != tag:
+            self._keys_cache = (tag, k.detach().to(dtype).contiguous())
+        return self._keys_cache[1]
+
+    def subkey_scores(self, query):
+        """query (N, heads, k_dim) -> scores against both sub-key sets, each (N, heads, n_keys)."""
+        return kernels.pk_scores(query, self._keys_as(query.dtype))
+
+    def get_indices(self, query):
+        """query (N, heads, k_dim) -> scores, indices (N, heads, knn): exact top-knn over all n_keys^2 keys."""
+        s1, s2 = self.subkey_scores(query)
+        scores, indices, _ = kernels.pk_select(s1, s2, self.knn)
+        return scores, indices
+
+    def read_values(self, indices, weights):
+        """indices, weights (N, heads*knn) -> (N, v_dim) = sum_j weights[:, j] * values[indices[:, j]]"""
+        table = self.values.weight.detach()
+        return kernels.bag_forward(indices, weights, table).to(table.dtype)
+
+    # ---- forward -------------------------------------------------------------------------------------------
+    def forward(self, x):
+        shape = x.shape
+        x = x.reshape(-1, self.d_in)
+        if (self.decode_graph and not self.record and not torch.is_grad_enabled() and x.is_cuda
+                and not torch.cuda.is_current_stream_capturing()):
+            return self._graph_forward(x).view(*shape[:-1], self.d_out)
+        return self._forward(x).view(*shape[:-1], self.d_out)
+
+    def _graph_forward(self, x):
+        """Replay a HIP graph of _forward captured for this input shape (any token count): the same kernels as
+        the eager path without the per-op launch cost.  Re-captured when the shape, dtype, autocast state or
+        inference table changes."""
+        ac = torch.is_autocast_enabled("cuda")
+        tag = (tuple(x.shape), x.dtype, ac, torch.get_autocast_dtype("cuda") if ac else None,
+               id(getattr(self.values, "infer_table", None)))
+        if self._graph is None or self._graph[0] != tag:
+            static_x = x.clone()
+            ctx = (torch.autocast("cuda", dtype=tag[3], cache_enabled=False) if ac
+                   else torch.autocast("cuda", enabled=False))
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side), ctx:
+                for _ in range(2):
+                    self._forward(static_x)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph), ctx:
+                static_out = self._forward(static_x)
+            self._graph = (tag, graph, static_x, static_out)
+        _, graph, static_x, static_out = self._graph
+        static_x.copy_(x)
+        graph.replay()
+        return static_out.clone()
+
+    def _query(self, x):
+        q = self.query_proj(x)
+        bn = self.query_norm
+        if bn is not None:
+            if bn.training:
+                raise NotImplementedError("smlm_hip is inference-only: put the model in eval() mode")
+            # BatchNorm in fp32 with the running statistics, whatever the parameter dtype
+            q = F.batch_norm(q.float(), bn.running_mean.float(), bn.running_var.float(), bn.weight.float(),
+                             bn.bias.float(), False, 0.0, bn.eps)
+        return q
+
+    def _forward(self, x):
+        if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
+            raise NotImplementedError("smlm_hip implements the inference lookup only: run the forward under "
+                                      "torch.no_grad() / torch.inference_mode()")
+        N = x.shape[0]
+        bf16 = _autocast_bf16(x) or x.dtype == torch.bfloat16
+        sdt = torch.bfloat16 if (bf16 or self.keys.dtype == torch.bfloat16) else torch.float32
+        q = self._query(x).to(sdt).view(N, self.heads, self.k_dim)
+        s1, s2 = kernels.pk_scores(q, self._keys_as(sdt))
+        scores, indices, weights = kernels.pk_select(s1, s2, self.knn)
+        if self.log_score_scale is not None:
+            # a positive per-head scale keeps the selection; only the softmax sharpness changes
+            scale = self.log_score_scale.detach().float().exp().view(1, self.heads, 1)
+            weights = torch.softmax(scores.float() * scale, dim=-1)
+        if self.record:
+            self.last_indices, self.last_scores, self.last_weights = indices, scores, weights
+        idx, w = indices.view(N, -1), weights.view(N, -1)
+        if self.swilu and bf16:
+            # fused inference bag: value rows (bf16 / fp32 / int8 / q4 table) * bf16(silu(pre)), bf16 out
+            pre = self.swilu_proj(x).to(torch.bfloat16)
+            table, scales = getattr(self.values, "infer_table", None) or (self.values.weight.detach(), None)
+            out = kernels.bag_infer(idx, w, table, scales, pre=pre, out_bf16=True)
+            return self.value_proj(out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
+        out = self.read_values(idx, w)
+        if self.swilu:
+            out = self.value_proj(out * F.silu(self.swilu_proj(x)).to(out.dtype))
+        return out
+
+    def macs_per_token(self):
+        """Multiply-accumulates per token (analytic): query, sub-key scoring, value bag, swilu."""
+        m = self.d_in * self.heads * self.k_dim
+        m += self.heads * 2 * self.n_keys * (self.k_dim // 2)
+        m += self.heads * self.knn * self.v_dim
+        if self.swilu:
+            m += self.d_in * self.v_dim + self.v_dim * self.d_out + self.v_dim
+        return m

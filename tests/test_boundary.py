@@ -1,0 +1,98 @@
+"""The drop-in boundary, without a GPU: libsmlm_pkm.so loads, exports every function include/smlm_pkm.h
+declares, and its argument checks return the documented status codes before anything is launched; the Python
+host layer rejects unsupported shapes the way the reference does (tests/test_pkm.py:130-136)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from smlm_hip import _lib
+from smlm_hip.pkm import ProductKeyMemory
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "smlm_pkm.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(smlm_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert ctypes.cast(getattr(raw, name), ctypes.c_void_p).value
+
+
+def test_version():
+    assert _lib.version().startswith("smlm_pkm ") and "gfx950" in _lib.version()
+
+
+def test_argument_checks_return_status_codes():
+    """Invalid calls are refused before any HIP call (safe without a GPU)."""
+    lib = _lib.lib()
+    fake = 256                                           # never dereferenced: the checks fail first
+    assert lib.smlm_pkm_bag(None, _lib.I64, fake, 1, 1, fake, _lib.F32, 1, 4, None, None, fake, _lib.F32,
+                            None) == _lib.EINVAL
+    assert "null" in _lib.last_error()
+    assert lib.smlm_pkm_bag(fake, 99, fake, 1, 1, fake, _lib.F32, 1, 4, None, None, fake, _lib.F32,
+                            None) == _lib.EINVAL
+    assert lib.smlm_pkm_bag(fake, _lib.I64, fake, 1, 1, fake, _lib.I8, 1, 4, None, None, fake, _lib.F32,
+                            None) == _lib.EINVAL                                 # i8 table without scales
+    assert "scales" in _lib.last_error()
+    assert lib.smlm_pkm_bag(fake, _lib.I64, fake, 1, 1, fake, _lib.Q4, 1, 5, fake, None, fake, _lib.F32,
+                            None) == _lib.EINVAL                                 # odd D for q4
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 1024, 48, fake, fake, fake, None) == _lib.EUNSUPPORTED
+    assert "knn" in _lib.last_error()
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 1000, 32, fake, fake, fake, None) == _lib.EUNSUPPORTED
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 131072, 32, fake, fake, fake, None) == _lib.EUNSUPPORTED
+    assert lib.smlm_pkm_select(fake, fake, _lib.I8, 1, 4, 1024, 32, fake, fake, fake, None) == _lib.EINVAL
+    assert lib.smlm_pkm_score(fake, 512, fake, _lib.BF16, 1, 1, 64, 12, fake, fake, None) == _lib.EUNSUPPORTED
+    assert lib.smlm_pkm_score(fake, 100, fake, _lib.BF16, 1, 1, 64, 256, fake, fake, None) == _lib.EINVAL
+    assert lib.smlm_pkm_score(fake + 2, 512, fake, _lib.BF16, 1, 1, 64, 256, fake, fake, None) == _lib.EINVAL
+    assert "aligned" in _lib.last_error()
+    assert lib.smlm_pkm_quantize(fake, _lib.F32, 4, 5, _lib.Q4, fake, fake, None) == _lib.EINVAL
+    assert lib.smlm_pkm_quantize(fake, _lib.F32, 4, 8, _lib.BF16, fake, fake, None) == _lib.EINVAL
+    # zero tokens is a valid no-op
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 0, 4, 1024, 32, fake, fake, fake, None) == _lib.OK
+
+
+def test_status_becomes_python_exception():
+    with pytest.raises(_lib.SmlmError, match="status -1"):
+        _lib.check(_lib.lib().smlm_pkm_quantize(None, _lib.F32, 1, 8, _lib.I8, None, None, None),
+                   "smlm_pkm_quantize")
+
+
+def test_rejects_unsupported_shapes():
+    """As the reference's Triton path: non-power-of-two n_keys or knn fail at construction with a clear
+    message (and, here, knn > 64 and the other implementations)."""
+    for n_keys, knn in ((24, 4), (16, 5), (256, 128)):
+        with pytest.raises(ValueError, match="powers of two"):
+            ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16)
+    with pytest.raises(ValueError, match="mem_impl='hip' only"):
+        ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16, impl="torch")
+    m = ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16)
+    assert m.keys.shape == (4, 2, 16, 8) and m.values.weight.shape == (256, 32)
+
+
+def test_state_dict_keys_are_the_reference_names():
+    m = ProductKeyMemory(24, 24, n_keys=16, heads=2, knn=4, k_dim=16)
+    keys = set(m.state_dict())
+    assert {"keys", "query_proj.weight", "query_proj.bias", "query_norm.weight", "query_norm.bias",
+            "query_norm.running_mean", "query_norm.running_var", "values.weight", "swilu_proj.weight",
+            "swilu_proj.bias", "value_proj.weight", "value_proj.bias"} <= keys
+
+
+def test_kernels_refuse_cpu_tensors():
+    from smlm_hip import kernels
+    s = torch.zeros(1, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP"):
+        kernels.pk_select(s, s, 8)

@@ -1,0 +1,327 @@
+"""HIP kernels against the CPU oracle (oracle/pkm_oracle.py), through the C ABI (smlm_hip.kernels).
+
+Bars: selection (indices, scores, order) bit-exact on the same sub-key scores; softmax weights within 1e-6;
+bf16 scores within 1 bf16 ulp of the fp64 scores (fp32 within 1e-5 of their scale); fp32 bag outputs within
+rtol = atol = 1e-5 relative to max|reference| (the reference's close(), tests/test_kernels.py:48-53); bf16 bag
+outputs within 1 bf16 ulp; quantised tables bit-exact.  Shapes follow the reference's tests
+(tests/test_kernels.py:123-125, 29-35, 220-242, 323-360) and BASELINE's configs.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.pkm_oracle as O
+from smlm_hip import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def bits_of(t):
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def bf16_from_bits(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------------------------------------ selection
+SELECT_SHAPES = [(4096, 4, 512, 32), (4096, 4, 1024, 32), (4096, 4, 2048, 32), (4096, 4, 4096, 32),
+                 (1, 4, 1024, 32), (64, 2, 16, 4), (96, 4, 64, 8), (33, 3, 256, 64), (5, 2, 65536, 32),
+                 (7, 1, 8, 1)]
+
+
+def check_select(s1, s2, knn, sc, idx, w):
+    rs, ri, rw = O.pk_select(s1, s2, knn)
+    got_sc = bits_of(sc) if s1.dtype == np.uint16 else sc.cpu().numpy()
+    assert np.array_equal(idx.cpu().numpy(), ri)
+    assert np.array_equal(got_sc.view(np.uint16 if s1.dtype == np.uint16 else np.uint32),
+                          rs.view(np.uint16 if s1.dtype == np.uint16 else np.uint32))
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("N,H,NK,knn", SELECT_SHAPES)
+def test_pk_select_bf16_bit_exact(N, H, NK, knn):
+    note(f"pk_select bf16 N={N} H={H} NK={NK} knn={knn}")
+    rng = np.random.default_rng(N + NK)
+    s1 = O.bf16_bits_rtne(rng.standard_normal((N, H, NK)).astype(np.float32))
+    s2 = O.bf16_bits_rtne(rng.standard_normal((N, H, NK)).astype(np.float32))
+    sc, idx, w = K.pk_select(bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV), knn)
+    torch.cuda.synchronize()
+    check_select(s1, s2, knn, sc, idx, w)
+    # the reference test's invariants (tests/test_kernels.py:146-151)
+    t1, t2 = bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV)
+    own = (t1.gather(-1, idx // NK).float() + t2.gather(-1, idx % NK).float()).to(torch.bfloat16)
+    assert torch.equal(own, sc)
+    srt = idx.view(-1, knn).sort(-1).values
+    assert bool((srt[:, 1:] != srt[:, :-1]).all())
+
+
+@pytest.mark.parametrize("N,H,NK,knn", [(512, 4, 1024, 32), (64, 4, 4096, 32), (40, 3, 64, 8), (9, 2, 16, 16)])
+def test_pk_select_bf16_ties(N, H, NK, knn):
+    """Scores from a handful of values (both signed zeros): almost every comparison is a tie."""
+    note(f"pk_select ties N={N} NK={NK} knn={knn}")
+    rng = np.random.default_rng(11)
+    vals = np.array([0x3F80, 0x3F00, 0x0000, 0x8000, 0xBF00, 0x3F40, 0x4000, 0xBF80], np.uint16)
+    s1 = vals[rng.integers(0, len(vals), (N, H, NK))]
+    s2 = vals[rng.integers(0, len(vals), (N, H, NK))]
+    sc, idx, w = K.pk_select(bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV), knn)
+    torch.cuda.synchronize()
+    check_select(s1, s2, knn, sc, idx, w)
+
+
+@pytest.mark.parametrize("N,H,NK,knn", [(2048, 4, 1024, 32), (3, 2, 4096, 64), (50, 2, 16, 8)])
+def test_pk_select_fp32_bit_exact(N, H, NK, knn):
+    note(f"pk_select fp32 N={N} NK={NK} knn={knn}")
+    rng = np.random.default_rng(N * 3 + NK)
+    s1 = rng.standard_normal((N, H, NK)).astype(np.float32)
+    s2 = rng.standard_normal((N, H, NK)).astype(np.float32)
+    sc, idx, w = K.pk_select(torch.from_numpy(s1).to(DEV), torch.from_numpy(s2).to(DEV), knn)
+    torch.cuda.synchronize()
+    check_select(s1, s2, knn, sc, idx, w)
+
+
+def test_pk_select_many_candidates_path():
+    """Rows built so that more than 1024 elements reach the lane-maxima threshold: the kernel must take its
+    exact path over the whole row.  Lane l of the 64-lane stride holds elements l, l+64, ...; lanes 0..31 get
+    maxima 8 - l/32 (bf16-exact) at their first element, lanes 0..15 carry 7.5 elsewhere (above the 32nd lane
+    maximum 7.03125 but below their own maximum), the rest 0."""
+    note("pk_select adversarial candidate overflow")
+    NK, knn = 4096, 32
+    row = np.zeros(NK, np.float32)
+    k = np.arange(NK)
+    lane = k % 64
+    row[(lane < 16) & (k >= 64)] = 7.5
+    row[:32] = 8.0 - np.arange(32) / 32.0
+    s1 = O.bf16_bits_rtne(np.stack([row, row[::-1].copy()]).reshape(2, 1, NK))
+    rng = np.random.default_rng(12)
+    s2 = O.bf16_bits_rtne(rng.standard_normal((2, 1, NK)).astype(np.float32))
+    assert np.sum(O.bf16_to_f32(s1[0, 0]) >= 7.03125) > 1024
+    sc, idx, w = K.pk_select(bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV), knn)
+    torch.cuda.synchronize()
+    check_select(s1, s2, knn, sc, idx, w)
+
+
+def test_pk_select_golden():
+    with open(os.path.join(GOLDEN, "select_known.json")) as f:
+        cases = json.load(f)["cases"]
+    for c in cases:
+        s1 = np.array(c["s1"], np.uint16).reshape(1, 1, -1)
+        s2 = np.array(c["s2"], np.uint16).reshape(1, 1, -1)
+        sc, idx, w = K.pk_select(bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV), c["knn"])
+        assert idx[0, 0].tolist() == c["idx"], c["name"]
+        if "score_bits" in c:
+            assert bits_of(sc)[0, 0].tolist() == c["score_bits"], c["name"]
+
+
+# ------------------------------------------------------------------------------------------------ scoring
+SCORE_SHAPES = [(1, 4, 4096, 256), (64, 4, 4096, 256), (2048, 4, 1024, 256), (100, 4, 2048, 256),
+                (5, 2, 16, 8), (17, 3, 64, 32), (300, 1, 512, 64)]
+
+
+def _score_inputs(N, H, NK, half, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(N, H, 2 * half, generator=g)
+    keys = torch.randn(H, 2, NK, half, generator=g) / 16
+    return q, keys
+
+
+@pytest.mark.parametrize("N,H,NK,half", SCORE_SHAPES)
+def test_pk_scores_bf16_within_one_ulp(N, H, NK, half):
+    note(f"pk_scores bf16 N={N} H={H} NK={NK} half={half}")
+    q, keys = _score_inputs(N, H, NK, half, N + NK)
+    qb, kb = q.to(torch.bfloat16), keys.to(torch.bfloat16)
+    s1, s2 = K.pk_scores(qb.to(DEV), kb.to(DEV))
+    r1, r2 = O.subkey_scores(qb.float().numpy(), kb.float().numpy())
+    absdot1 = np.einsum("nhd,hkd->nhk", np.abs(qb.float().numpy()[..., :half]), np.abs(kb.float().numpy()[:, 0]))
+    for got, ref, mag in ((s1, r1, absdot1), (s2, r2, None)):
+        g = got.float().cpu().numpy().astype(np.float64)
+        # one bf16 ulp (2^-7 relative) plus fp32-accumulation slack on cancellation
+        slack = 1e-5 * (mag if mag is not None else np.abs(ref).max())
+        assert np.all(np.abs(g - ref) <= 2 ** -7 * np.abs(ref) + slack)
+    # the result is the bf16 rounding of an fp32 sum: at most one ulp from the rounded fp64 value
+    assert got.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("N,H,NK,half", SCORE_SHAPES[:4] + [(5, 2, 16, 8)])
+def test_pk_scores_fp32(N, H, NK, half):
+    note(f"pk_scores fp32 N={N} NK={NK}")
+    q, keys = _score_inputs(N, H, NK, half, 7 * N + NK)
+    s1, s2 = K.pk_scores(q.to(DEV), keys.to(DEV))
+    r1, r2 = O.subkey_scores(q.numpy(), keys.numpy())
+    mag = np.einsum("nhd,hkd->nhk", np.abs(q.numpy()[..., :half]).astype(np.float64),
+                    np.abs(keys.numpy()[:, 0]).astype(np.float64))
+    np.testing.assert_array_less(np.abs(s1.cpu().numpy() - r1), 1e-5 * mag + 1e-30)
+    np.testing.assert_allclose(s2.cpu().numpy(), r2, rtol=1e-5, atol=1e-5 * np.abs(r2).max())
+
+
+def test_pk_scores_rejects_mismatch():
+    q = torch.zeros(2, 4, 512, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        K.pk_scores(q, torch.zeros(4, 2, 64, 128, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(ValueError):
+        K.pk_scores(q, torch.zeros(4, 2, 64, 256, dtype=torch.float32, device=DEV))
+
+
+# ------------------------------------------------------------------------------------------------ value bag
+def skewed_indices(rows, N, K_, rng):
+    """Uniform rows plus a few hot rows (the reference's skewed_indices, tests/test_kernels.py:55-61)."""
+    idx = rng.integers(0, rows, (N, K_))
+    hot = rng.integers(0, rows, 8)
+    m = rng.random((N, K_)) < 0.2
+    idx[m] = hot[rng.integers(0, 8, int(m.sum()))]
+    return idx
+
+
+_TABLES = {}
+
+
+def make_table(kind, rows, D, rng):
+    """(device-ready torch table, torch scales, numpy table, numpy scales); cached per (kind, rows, D)."""
+    key = (kind, rows, D)
+    if key not in _TABLES:
+        _TABLES.clear()
+        _TABLES[key] = _make_table(kind, rows, D, np.random.default_rng(rows * 7 + D))
+    return _TABLES[key]
+
+
+def _make_table(kind, rows, D, rng):
+    t32 = rng.standard_normal((rows, D), dtype=np.float32) * np.float32(D ** -0.5)
+    if kind == "f32":
+        return torch.from_numpy(t32), None, t32, None
+    if kind == "bf16":
+        b = O.bf16_bits_rtne(t32)
+        return bf16_from_bits(b), None, b, None
+    codes, sc = O.quantize_rows(t32, kind)
+    tt = torch.from_numpy(codes)
+    return tt, torch.from_numpy(sc), codes, sc
+
+
+def close(a, b):
+    scale = max(1.0, float(np.abs(b).max()))
+    np.testing.assert_allclose(a / scale, b / scale, rtol=1e-5, atol=1e-5)
+
+
+BAG_CASES = [("f32", 1 << 20, 384, 512, 128), ("bf16", 1 << 20, 384, 512, 128), ("i8", 1 << 20, 384, 512, 128),
+             ("q4", 1 << 20, 384, 512, 128), ("bf16", 4096, 64, 32, 96), ("f32", 4096, 64, 32, 48),
+             ("q4", 4096, 64, 32, 40), ("i8", 4096, 64, 32, 40), ("i8", 1000, 24, 16, 12), ("bf16", 1000, 24, 9, 7),
+             ("f32", 2048, 96, 64, 128), ("bf16", 300, 384, 3, 1), ("bf16", 1 << 16, 384, 2, 600)]
+
+
+@pytest.mark.parametrize("kind,rows,D,N,K_", BAG_CASES)
+@pytest.mark.parametrize("idx32", [False, True])
+def test_bag_matches_oracle(kind, rows, D, N, K_, idx32):
+    note(f"bag {kind} rows={rows} D={D} N={N} K={K_} idx32={idx32}")
+    rng = np.random.default_rng(rows + D + K_)
+    t, sc, tn, scn = make_table(kind, rows, D, rng)
+    idx = skewed_indices(rows, N, K_, rng)
+    w = rng.random((N, K_)).astype(np.float32)
+    pre = O.bf16_bits_rtne(rng.standard_normal((N, D)).astype(np.float32))
+    ti = torch.from_numpy(idx.astype(np.int32 if idx32 else np.int64)).to(DEV)
+    tw = torch.from_numpy(w).to(DEV)
+    td, tsc = t.to(DEV), (sc.to(DEV) if sc is not None else None)
+    ref = O.bag(idx, w, tn, kind, scn)
+    close(K.bag_infer(ti, tw, td, tsc).cpu().numpy(), ref)
+    if kind in ("f32", "bf16"):
+        close(K.bag_forward(ti, tw, td).cpu().numpy(), ref)
+    ref2 = O.bag(idx, w, tn, kind, scn, pre=pre)
+    tpre = bf16_from_bits(pre).to(DEV)
+    close(K.bag_infer(ti, tw, td, tsc, pre=tpre).cpu().numpy(), ref2)
+    out = K.bag_infer(ti, tw, td, tsc, pre=tpre, out_bf16=True)
+    assert out.dtype == torch.bfloat16
+    refb = O.bf16_to_f32(O.bag(idx, w, tn, kind, scn, pre=pre, out_bf16=True)).astype(np.float64)
+    scale = float(np.abs(ref2).max())
+    np.testing.assert_allclose(out.float().cpu().numpy(), refb, rtol=2 ** -7, atol=2 ** -8 * scale)
+
+
+def test_bag_out_of_range_index_gives_nan_row():
+    rng = np.random.default_rng(13)
+    t = torch.randn(100, 64, device=DEV)
+    idx = torch.from_numpy(rng.integers(0, 100, (4, 8))).to(DEV)
+    idx[2, 3] = 100
+    idx[3, 0] = -1
+    w = torch.rand(4, 8, device=DEV)
+    out = K.bag_forward(idx, w, t)
+    assert torch.isnan(out[2:]).all() and torch.isfinite(out[:2]).all()
+    ref = O.bag(idx[:2].cpu().numpy(), w[:2].cpu().numpy(), t.cpu().numpy(), "f32")
+    close(out[:2].cpu().numpy(), ref)
+
+
+def test_bag_table_beyond_2_31_elements():
+    """Row offsets past 2^31 elements (and 2^32 bytes): 6M x 384 bf16 (tests/test_kernels.py:323-360)."""
+    note("bag large table 6M x 384 bf16")
+    rows, D = 6 * 1024 * 1024, 384
+    t = torch.empty(rows, D, dtype=torch.bfloat16, device=DEV).normal_(0, 0.05)
+    rng = np.random.default_rng(14)
+    idx = rng.integers(rows - 200000, rows, (64, 128))
+    idx[:, 0] = rows - 1
+    w = rng.random((64, 128)).astype(np.float32)
+    ti = torch.from_numpy(idx).to(DEV)
+    used = np.unique(idx)
+    sub = bits_of(t[torch.from_numpy(used).to(DEV)])
+    remap = np.searchsorted(used, idx)
+    ref = O.bag(remap, w, sub, "bf16")
+    close(K.bag_infer(ti, torch.from_numpy(w).to(DEV), t).cpu().numpy(), ref)
+    del t
+    torch.cuda.empty_cache()
+
+
+def test_bag_zipf_int8_gather_sample():
+    """A 2048-token sample of the config-4 stress gather: int8 table with fp16 row scales, 128 Zipf(1.1)
+    lookups per token through a seeded row permutation, per-head softmax weights, fp32 out."""
+    note("bag zipf int8 sample")
+    rows, D, N = 1 << 20, 384, 2048
+    rng = np.random.default_rng(15)
+    t32 = (rng.standard_normal((rows, D)) * 0.02).astype(np.float32)
+    codes, sc = O.quantize_rows(t32, "i8")
+    p = 1.0 / np.arange(1, rows + 1) ** 1.1
+    cdf = np.cumsum(p) / p.sum()
+    ranks = np.minimum(np.searchsorted(cdf, rng.random((N, 128))), rows - 1)
+    idx = rng.permutation(rows)[ranks]
+    w = np.concatenate([O.softmax_f32(rng.standard_normal((N, 32)).astype(np.float32)) for _ in range(4)], 1)
+    out = K.bag_infer(torch.from_numpy(idx).to(DEV), torch.from_numpy(w).to(DEV), torch.from_numpy(codes).to(DEV),
+                      torch.from_numpy(sc).to(DEV))
+    close(out.cpu().numpy(), O.bag(idx, w, codes, "i8", sc))
+
+
+# ------------------------------------------------------------------------------------------------ quantisation
+@pytest.mark.parametrize("kind", ["i8", "q4"])
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_quantize_bit_exact(kind, src):
+    rng = np.random.default_rng(16)
+    t32 = (rng.standard_normal((5000, 384)) * 0.02).astype(np.float32)
+    t32[7] = 0.0                                           # zero row -> scale 1
+    t32[8, 3], t32[8, 5] = 0.5, -0.5                       # tied largest magnitude
+    if src == "bf16":
+        bits = O.bf16_bits_rtne(t32)
+        tt, t_np = bf16_from_bits(bits), O.bf16_to_f32(bits)
+    else:
+        tt, t_np = torch.from_numpy(t32), t32
+    fn = K.quantize_int8 if kind == "i8" else K.quantize_q4
+    codes, sc = fn(tt.to(DEV))
+    rc, rs = O.quantize_rows(t_np, kind)
+    assert np.array_equal(codes.cpu().numpy(), rc)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    deq = (K.dequantize_int8 if kind == "i8" else K.dequantize_q4)(codes, sc).cpu().numpy()
+    np.testing.assert_array_equal(deq, O.dequantize(rc, rs, kind).astype(np.float32))
+
+
+def test_quantize_golden():
+    with open(os.path.join(GOLDEN, "quant_known.json")) as f:
+        g = json.load(f)
+    for case in g["i8"]:
+        codes, sc = K.quantize_int8(torch.tensor([case["row"]], dtype=torch.float32, device=DEV))
+        assert codes[0].tolist() == case["codes"]
+        assert int(sc.cpu().view(torch.int16)[0]) & 0xFFFF == case["scale_f16_bits"]
+    for case in g["q4"]:
+        codes, sc = K.quantize_q4(torch.tensor([case["row"]], dtype=torch.float32, device=DEV))
+        assert codes[0].tolist() == case["packed"]
+        assert int(sc.cpu().view(torch.int16)[0]) & 0xFFFF == case["scale_f16_bits"]
