@@ -185,11 +185,13 @@ def cpu_baseline(model, B, max_steps, budget_s):
     cfg = model.cfg.to_dict()
     g = torch.Generator().manual_seed(1)
     prompt = torch.randint(0, cfg["vocab_size"], (B, 128), generator=g)
+    log(f"cpu baseline: weights on the host, prefill of {B} x 128 tokens on {torch.get_num_threads()} threads")
     with torch.no_grad():
         caches = [dict() for _ in range(cfg["n_layers"])]
         t0 = time.perf_counter()
         nxt = TP.lm_forward(sd, cfg, prompt, caches, 0, last_only=True).argmax(-1)
         t_prefill = time.perf_counter() - t0
+        log(f"cpu baseline: prefill {t_prefill:.1f} s, timing decode steps")
         steps = 0
         t0 = time.perf_counter()
         while steps < max_steps and (steps < 2 or time.perf_counter() - t0 < budget_s):

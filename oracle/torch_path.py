@@ -62,22 +62,27 @@ def pkm_select_torch(s1, s2, knn):
     return sc, alli.gather(-1, best)
 
 
-def pkm_forward(sd, p, x, mcfg, table=None):
-    """One memory layer: x (N, d_in) -> (N, d_out).  mcfg: heads, knn, k_dim, n_keys, query_norm, swilu, eps.
-    `table` overrides the value table (e.g. a dequantised inference table)."""
+def pkm_forward(sd, p, x, mcfg, table=None, selection=None):
+    """One memory layer: x (N, d_in) -> (N, d_out).  mcfg: heads, knn, k_dim, n_keys, query_norm, swilu.
+    `table` overrides the value table (e.g. a dequantised inference table); `selection` = (indices, weights),
+    each (N, heads, knn), replaces the scoring and selection (to check everything downstream of a given
+    selection)."""
     N = x.shape[0]
     H, knn, k_dim = mcfg["heads"], mcfg["knn"], mcfg["k_dim"]
-    q = x @ sd[p + "query_proj.weight"].T + sd[p + "query_proj.bias"]
-    if mcfg["query_norm"] == "batchnorm":
-        q = (q - sd[p + "query_norm.running_mean"]) / torch.sqrt(sd[p + "query_norm.running_var"] + 1e-5)
-        q = q * sd[p + "query_norm.weight"] + sd[p + "query_norm.bias"]
-    q = q.view(N, H, k_dim)
-    keys = sd[p + "keys"]
-    half = k_dim // 2
-    s1 = torch.einsum("nhd,hkd->nhk", q[..., :half], keys[:, 0])
-    s2 = torch.einsum("nhd,hkd->nhk", q[..., half:], keys[:, 1])
-    scores, idx = pkm_select_torch(s1, s2, knn)
-    w = torch.softmax(scores, -1)
+    if selection is None:
+        q = x @ sd[p + "query_proj.weight"].T + sd[p + "query_proj.bias"]
+        if mcfg["query_norm"] == "batchnorm":
+            q = (q - sd[p + "query_norm.running_mean"]) / torch.sqrt(sd[p + "query_norm.running_var"] + 1e-5)
+            q = q * sd[p + "query_norm.weight"] + sd[p + "query_norm.bias"]
+        q = q.view(N, H, k_dim)
+        keys = sd[p + "keys"]
+        half = k_dim // 2
+        s1 = torch.einsum("nhd,hkd->nhk", q[..., :half], keys[:, 0])
+        s2 = torch.einsum("nhd,hkd->nhk", q[..., half:], keys[:, 1])
+        scores, idx = pkm_select_torch(s1, s2, knn)
+        w = torch.softmax(scores, -1)
+    else:
+        idx, w = selection[0], selection[1].to(x.dtype)
     values = sd[p + "values.weight"] if table is None else table
     if values.dtype == x.dtype:
         out = F.embedding_bag(idx.view(N, -1), values, per_sample_weights=w.view(N, -1), mode="sum")
@@ -90,9 +95,9 @@ def pkm_forward(sd, p, x, mcfg, table=None):
     return out
 
 
-def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False):
+def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False, selections=None):
     """Logits (B, T, vocab) of the decoder with the memory layers cfg["mem_layers"] (only the last position's,
-    (B, 1, vocab), with last_only)."""
+    (B, 1, vocab), with last_only).  selections: {layer: (indices, weights)} given to pkm_forward."""
     x = sd["tok_emb.weight"][idx]
     mcfg = dict(heads=cfg["mem_heads"], knn=cfg["mem_knn"], k_dim=cfg["mem_k_dim"], n_keys=cfg["mem_n_keys"],
                 query_norm=cfg["mem_query_norm"], swilu=cfg["mem_swilu"])
@@ -105,7 +110,8 @@ def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False):
         if i in cfg["mem_layers"]:
             B, T, C = h.shape
             t = None if tables is None else tables.get(i)
-            x = x + pkm_forward(sd, p + "ffn.", h.reshape(B * T, C), mcfg, t).view(B, T, -1)
+            sel = None if selections is None else selections.get(i)
+            x = x + pkm_forward(sd, p + "ffn.", h.reshape(B * T, C), mcfg, t, sel).view(B, T, -1)
         else:
             a, b = (h @ sd[p + "ffn.w13.weight"].T).chunk(2, -1)
             x = x + (F.silu(a) * b) @ sd[p + "ffn.w2.weight"].T

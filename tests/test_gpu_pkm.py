@@ -207,15 +207,27 @@ def test_lm_logits_fp32_match_torch_path():
 
 @torch.no_grad()
 def test_lm_logits_bf16_within_1e2():
-    """bf16 LM logits against the fp32 torch path with the same (bf16-valued) weights: within 1e-2 of the
-    logits' scale."""
+    """bf16 LM: the memory layer's selection is bit-exact against the oracle on the layer's own bf16 sub-key
+    scores, and the logits are within 1e-2 of their scale of the fp32 torch path given that selection.
+    (bf16 scores legitimately select other rows than fp32 scores wherever candidates lie within a bf16
+    rounding step, so the logits are compared on one selection.)"""
     cfg = ModelConfig(vocab_size=512, d_model=128, n_layers=3, n_heads=2, ffn_hidden=256, max_seq_len=64,
                       mem_layers=[1], mem_n_keys=64, mem_heads=4, mem_knn=16, mem_k_dim=64)
     torch.manual_seed(6)
     m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
     x = torch.randint(0, 512, (2, 32), generator=torch.Generator().manual_seed(6))
+    mem = m.layers[1].ffn
+    mem.record = True
+    seen = {}
+    hook = mem.register_forward_hook(lambda mod, inp, out: seen.__setitem__("x", inp[0].detach().clone()))
     got = m(x.to(DEV)).float().cpu()
+    hook.remove()
+    q = mem._query(seen["x"].reshape(-1, cfg.d_model)).to(torch.bfloat16).view(-1, 4, 64)
+    s1, s2 = K.pk_scores(q, mem.keys.detach())
+    _, oi, ow = O.pk_select(bits_of(s1), bits_of(s2), 16)
+    assert np.array_equal(mem.last_indices.cpu().numpy(), oi)
+    np.testing.assert_allclose(mem.last_weights.cpu().numpy(), ow, rtol=0, atol=1e-6)
     sd = {k: v.float().cpu() for k, v in m.state_dict().items()}
-    ref = TP.lm_forward(sd, cfg.to_dict(), x)
+    ref = TP.lm_forward(sd, cfg.to_dict(), x, selections={1: (mem.last_indices.cpu(), mem.last_weights.cpu())})
     err = (got - ref).abs().max() / ref.abs().max()
     assert float(err) < 1e-2, float(err)
