@@ -135,11 +135,9 @@ def gather_stress(dev, reps):
     alg_bytes = N * Kl * (D + 2 + 8 + 4) + N * D * 4          # 3,439,329,280
     ms_zipf = event_time_ms(lambda: K.bag_infer(idx, w, codes, scales), reps)
     ms_uni = event_time_ms(lambda: K.bag_infer(uni, w, codes, scales), reps)
-    top1k = None
     res = {"tokens": N, "lookups_per_token": Kl, "table": "16,777,216 x 384 int8 + fp16 row scales",
            "alg_bytes_per_call": alg_bytes, "ms_zipf": ms_zipf, "ms_uniform": ms_uni,
-           "alg_GBps_zipf": alg_bytes / ms_zipf / 1e6, "alg_GBps_uniform": alg_bytes / ms_uni / 1e6,
-           "top1000_share": top1k}
+           "alg_GBps_zipf": alg_bytes / ms_zipf / 1e6, "alg_GBps_uniform": alg_bytes / ms_uni / 1e6}
     del codes, scales, idx, w, uni
     torch.cuda.empty_cache()
     return res
@@ -205,47 +203,97 @@ def cpu_baseline(model, B, max_steps, budget_s):
                       f"bf16 table)", "cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
 
 
+def read_traffic():
+    """HBM bytes per launch of the config-4 gather from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE, calibrated on a plain copy kernel), or None if there is none."""
+    path = os.path.join(REPO, "profiles", "gather_config4_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch_zipf:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def calibration_copy(dev, nbytes=1 << 30):
+    """A plain device copy of known size (reads and writes nbytes): the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters in the PMC runs."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--reps", type=int, default=20, help="timed launches per kernel measurement")
-    ap.add_argument("--cpu-steps", type=int, default=64, help="most CPU-baseline decode steps")
+    ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--phases", default="decode,lookup,gather,cpu",
+                    help="subset of decode,lookup,gather,cpu,calibrate (profiling runs); the JSON line is "
+                         "complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    phases = set(args.phases.split(","))
+    if args.no_cpu:
+        phases.discard("cpu")
 
     import torch
     from smlm_hip import _lib
     dev = torch.device("cuda:0")
     log(f"{_lib.version()} on {torch.cuda.get_device_name(dev)}")
 
-    cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
-    t0 = time.perf_counter()
-    model = build_lm(cfg, dev)
-    log(f"B-16M LM built in {time.perf_counter() - t0:.1f} s")
-    tok_s64, ms64 = time_decode(model, 64, args.steps, args.warmup, dev)
-    log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
-    tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
-    log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
-
-    lk = lookup_prefill(dev, args.reps)
-    log(f"lookup config 2: {lk}")
-    ga = gather_stress(dev, args.reps)
-    log(f"gather config 4: {ga}")
-
-    cpu = None
-    if not args.no_cpu:
+    if "calibrate" in phases:
+        calibration_copy(dev)
+        log("calibration copy of 1 GiB done")
+    model = None
+    tok_s64 = ms64 = tok_s1 = ms1 = None
+    if "decode" in phases or "cpu" in phases:
+        cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
+        t0 = time.perf_counter()
+        model = build_lm(cfg, dev)
+        log(f"B-16M LM built in {time.perf_counter() - t0:.1f} s")
+    if "decode" in phases:
+        tok_s64, ms64 = time_decode(model, 64, args.steps, args.warmup, dev)
+        log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
+        tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
+        log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
+    lk = ga = cpu = None
+    if "lookup" in phases:
+        lk = lookup_prefill(dev, args.reps)
+        log(f"lookup config 2: {lk}")
+    if "gather" in phases:
+        ga = gather_stress(dev, args.reps)
+        log(f"gather config 4: {ga}")
+    if "cpu" in phases:
         t0 = time.perf_counter()
         cpu = cpu_baseline(model, 64, args.cpu_steps, args.cpu_seconds)
         log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f} s)")
 
-    achieved = ga["alg_GBps_zipf"]
+    roofline = roofline_score = None
+    if ga is not None:
+        achieved = ga["alg_GBps_zipf"]
+        traffic = read_traffic()
+        roofline = {"kernel": "bag_rows_kernel<int8> (config 4 gather)", "bound": "hbm", "achieved": achieved,
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                    "uniform_control_achieved": ga["alg_GBps_uniform"],
+                    "uniform_control_frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS}
+        if traffic:
+            roofline["physical_GBps_zipf"] = traffic / ga["ms_zipf"] / 1e6
+    if lk is not None:
+        roofline_score = {"kernel": "score_kernel<bf16> (config 2 scoring)", "bound": "mfma",
+                          "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS}
     line = {
         "metric": "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather HBM GB/s",
         "value": tok_s64, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -257,14 +305,7 @@ def main():
                    "new_tokens": args.steps},
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
         "pkm_lookup_config2": lk, "gather_config4": ga,
-        "roofline": {"kernel": "bag_rows_kernel<int8> (config 4 gather)", "bound": "hbm", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "uniform_control_achieved": ga["alg_GBps_uniform"],
-                     "uniform_control_frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS},
-        "roofline_score": {"kernel": "score_kernel<bf16> (config 2 scoring)", "bound": "mfma",
-                           "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                           "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS},
-        "cpu_baseline": cpu,
+        "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 

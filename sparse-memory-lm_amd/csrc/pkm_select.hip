@@ -2,43 +2,70 @@
 // top-knn of the (i+1)(j+1) <= knn Cartesian candidates and the fp32 softmax.  Replaces pk_select /
 // _pk_select_kernel (smlm/kernels.py:128-177, 200-226) with the same deterministic semantics, and extends them
 // to fp32 scores (smlm/pkm.py:125-136 for the fp32 path):
-//   - a half's element k gets the key (order(score) << kIdxBits) | (idxmax - k): larger key = larger score,
-//     ties -> smaller k.  bf16: 16-bit code + 16-bit index in a u32; fp32: 32 + 32 bits in a u64.
+//   - a half's element k gets the key (code(score) << B) | (2^B - 1 - k) with code() order-preserving (B = 16
+//     for bf16 in a u32, B = 32 for fp32 in a u64): larger key = larger score, ties -> smaller k;
 //   - candidate (i, j) is scored as dtype(v1[i] + v2[j]) (bf16: fp32 add, rounded to nearest even) with key
-//     (order(score) << 32) | (0xFFFFFFFF - (i1*NK + i2)), so ties -> smaller table index.
+//     (code(score) << 32) | (0xFFFFFFFF - (i1*NK + i2)), so ties -> smaller table index;
 //   - all keys are distinct, so "the knn largest keys" is one exact set.
 //
-// One workgroup = two wavefronts per (token, head) row; wavefront 0 selects in s1, wavefront 1 in s2, then
-// wavefront 0 does the Cartesian step.  A wavefront's half top-k:
-//   1. every lane takes the maximum key of its strided share of the row; the knn-th largest of the 64 lane
-//      maxima is a threshold t0 that at least knn elements reach (the knn largest lane maxima are distinct
-//      elements), found by a bitwise search over ballot() counts;
-//   2. the elements >= t0 (typically a few dozen) are compacted into LDS with ballot/mbcnt;
-//   3. the exact knn-th largest key t1 among them is found by the same bitwise search, the knn keys >= t1 are
-//      compacted and put in descending order by counting ranks.
-// If more than kCap elements reach t0 (adversarial rows), step 3 runs directly on the row instead.
+// One workgroup = two wavefronts per (token, head) row: wavefront 0 selects in s1, wavefront 1 in s2, then
+// wavefront 0 does the Cartesian step.  Half top-k of a wavefront (row of NK <= 4096 bf16 / 2048 fp32 scores):
+//   1. the row is loaded into registers with 16-byte loads, all in flight at once (lane l holds chunks
+//      l, l+64, ...), and turned into order codes (packed 16-bit ops for bf16);
+//   2. each lane's maximum code; the knn-th largest of the 64 lane maxima, code0, is reached by at least knn
+//      elements (the top knn lanes each hold one), found by a bitwise search over ballot() counts;
+//   3. the elements with code >= code0 (typically a few dozen) are compacted into LDS via a lane prefix sum;
+//   4. the exact knn-th largest key t1 among them is found by the same bitwise search with the candidates held
+//      in registers; the knn keys >= t1 are compacted and put in descending order by counting ranks.
+// Rows outside the register shapes, or with more than kCap elements at or above code0 (adversarial ties),
+// take the streaming path, which searches the row in global memory directly.
 #include "pkm_common.h"
 
 namespace smlm {
 namespace {
 
 constexpr int kCap = 1024;       // LDS candidates per half
+constexpr int kRegCand = 4;      // candidates per lane held in registers for the exact search (C <= 256)
 constexpr int kMaxKnn = 64;
-constexpr int kMaxPairs = 288;   // (i, j) with (i+1)(j+1) <= 64: sum_{i=1..64} floor(64/i) = 280
+
+// ---- the Cartesian pair list, built at compile time: for knn = 2^lg, pairs [off[lg], off[lg+1]) ------------
+struct PairTable {
+  uint16_t off[8];
+  uint8_t i[512];
+  uint8_t j[512];
+};
+constexpr PairTable make_pairs() {
+  PairTable t{};
+  int n = 0;
+  for (int lg = 0; lg <= 6; ++lg) {
+    const int knn = 1 << lg;
+    t.off[lg] = (uint16_t)n;
+    for (int i = 0; i < knn; ++i)
+      for (int j = 0; (i + 1) * (j + 1) <= knn; ++j) {
+        t.i[n] = (uint8_t)i;
+        t.j[n] = (uint8_t)j;
+        ++n;
+      }
+  }
+  t.off[7] = (uint16_t)n;  // 1 + 3 + 8 + 20 + 50 + 119 + 280 = 481
+  return t;
+}
+__constant__ PairTable kPairs = make_pairs();
+constexpr int kMaxPairSlots = 5;  // ceil(280 / 64)
 
 template <bool F32> struct SelKey;
 template <> struct SelKey<false> { using T = uint32_t; };
 template <> struct SelKey<true> { using T = uint64_t; };
 
 template <bool F32>
+__device__ __forceinline__ typename SelKey<F32>::T make_key(uint32_t code, uint32_t k) {
+  if constexpr (F32) return ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - k);
+  else return (code << 16) | (0xFFFFu - k);
+}
+template <bool F32>
 __device__ __forceinline__ typename SelKey<F32>::T half_key(const void *row, int k) {
-  if constexpr (F32) {
-    const uint32_t u = ((const uint32_t *)row)[k];
-    return ((uint64_t)order32(u) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)k);
-  } else {
-    const uint32_t b = ((const uint16_t *)row)[k];
-    return (order16(b) << 16) | (0xFFFFu - (uint32_t)k);
-  }
+  if constexpr (F32) return make_key<true>(order32(((const uint32_t *)row)[k]), (uint32_t)k);
+  else return make_key<false>(order16(((const uint16_t *)row)[k]), (uint32_t)k);
 }
 template <bool F32>
 __device__ __forceinline__ float key_value(typename SelKey<F32>::T key) {
@@ -51,73 +78,37 @@ __device__ __forceinline__ uint32_t key_index(typename SelKey<F32>::T key) {
   else return 0xFFFFu - (key & 0xFFFFu);
 }
 
-// Largest t with count_ge(t) >= need (count_ge is wave-uniform and non-increasing in t; count_ge(0) >= need).
+// Largest t with count_ge(t) >= need, searching bits [0, bits) (count_ge is wave-uniform, non-increasing in t,
+// count_ge(0) >= need, and no key has bits at or above `bits`).
 template <typename Key, typename CountGE>
-__device__ __forceinline__ Key threshold_search(int need, CountGE count_ge) {
+__device__ __forceinline__ Key threshold_search(int need, int bits, CountGE count_ge) {
   Key t = 0;
-  for (int b = (int)sizeof(Key) * 8 - 1; b >= 0; --b) {
+  for (int b = bits - 1; b >= 0; --b) {
     const Key c = t | ((Key)1 << b);
     if (count_ge(c) >= need) t = c;
   }
   return t;
 }
 
-// Exact top-knn keys of one score row (NK elements), written to out[0..knn) in descending order.
-template <bool F32>
-__device__ void half_topk(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
-                          typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
-  using Key = typename SelKey<F32>::T;
+__device__ __forceinline__ int wave_exclusive_sum(int v, int *total) {
+  int incl = v;
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int u = __shfl_up(incl, o, kWave);
+    if (lane_id() >= o) incl += u;
+  }
+  *total = __shfl(incl, kWave - 1, kWave);
+  return incl - v;
+}
+
+// The knn keys >= t (exactly knn exist) from `src` (n entries, LDS) into out[] in descending order.
+template <typename Key, typename Fetch>
+__device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetch, Key *sel, Key *out) {
   const int lane = lane_id();
-
-  Key mx = 0;
-  for (int k = lane; k < NK; k += kWave) {
-    const Key u = half_key<F32>(row, k);
-    mx = u > mx ? u : mx;
-  }
-  const Key t0 = threshold_search<Key>(knn, [&](Key t) { return (int)__popcll(ballot(mx >= t)); });
-
-  int C = 0;
-  for (int k0 = 0; k0 < NK; k0 += kWave) {
-    const int k = k0 + lane;
-    const Key u = k < NK ? half_key<F32>(row, k) : (Key)0;
-    const bool take = k < NK && u >= t0;
-    const uint64_t m = ballot(take);
-    const int pos = C + lanes_below(m);
-    if (take && pos < kCap) cand[pos] = u;
-    C += (int)__popcll(m);
-  }
-  wave_lds_sync();
-
-  const bool in_lds = C <= kCap;
-  Key t1;
-  if (in_lds) {
-    t1 = threshold_search<Key>(knn, [&](Key t) {
-      int cnt = 0;
-      for (int p0 = 0; p0 < C; p0 += kWave) {
-        const int p = p0 + lane;
-        cnt += (int)__popcll(ballot(p < C && cand[p] >= t));
-      }
-      return cnt;
-    });
-  } else {
-    t1 = threshold_search<Key>(knn, [&](Key t) {
-      int cnt = 0;
-      for (int k0 = 0; k0 < NK; k0 += kWave) {
-        const int k = k0 + lane;
-        cnt += (int)__popcll(ballot(k < NK && half_key<F32>(row, k) >= t));
-      }
-      return cnt;
-    });
-  }
-
-  // exactly knn keys are >= t1
   int S = 0;
-  const int total = in_lds ? C : NK;
-  for (int p0 = 0; p0 < total; p0 += kWave) {
+  for (int p0 = 0; p0 < n; p0 += kWave) {
     const int p = p0 + lane;
-    Key u = 0;
-    if (p < total) u = in_lds ? cand[p] : half_key<F32>(row, p);
-    const bool ge = p < total && u >= t1;
+    const Key u = p < n ? fetch(p) : (Key)0;
+    const bool ge = p < n && u >= t;
     const uint64_t m = ballot(ge);
     const int pos = S + lanes_below(m);
     if (ge && pos < kMaxKnn) sel[pos] = u;
@@ -133,7 +124,175 @@ __device__ void half_topk(const void *row, int NK, int knn, typename SelKey<F32>
   wave_lds_sync();
 }
 
+// Exact top-knn among C candidate keys in LDS, into out[] descending.
 template <bool F32>
+__device__ void topk_of_candidates(int C, int knn, typename SelKey<F32>::T *cand, typename SelKey<F32>::T *sel,
+                                   typename SelKey<F32>::T *out) {
+  using Key = typename SelKey<F32>::T;
+  constexpr int kBits = F32 ? 64 : 32;
+  const int lane = lane_id();
+  Key t;
+  if (C <= kRegCand * kWave) {
+    Key reg[kRegCand];
+    bool val[kRegCand];
+#pragma unroll
+    for (int s = 0; s < kRegCand; ++s) {
+      const int p = s * kWave + lane;
+      val[s] = p < C;
+      reg[s] = val[s] ? cand[p] : (Key)0;
+    }
+    t = threshold_search<Key>(knn, kBits, [&](Key c) {
+      int n = 0;
+#pragma unroll
+      for (int s = 0; s < kRegCand; ++s) n += (int)__popcll(ballot(val[s] && reg[s] >= c));
+      return n;
+    });
+  } else {
+    t = threshold_search<Key>(knn, kBits, [&](Key c) {
+      int n = 0;
+      for (int p0 = 0; p0 < C; p0 += kWave) {
+        const int p = p0 + lane;
+        n += (int)__popcll(ballot(p < C && cand[p] >= c));
+      }
+      return n;
+    });
+  }
+  collect_sorted<Key>(C, knn, t, [&](int p) { return cand[p]; }, sel, out);
+}
+
+// Streaming half top-k: any NK, searching the row in global memory.
+template <bool F32>
+__device__ void half_topk_stream(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
+                                 typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
+  using Key = typename SelKey<F32>::T;
+  constexpr int kBits = F32 ? 64 : 32;
+  const int lane = lane_id();
+  Key mx = 0;
+  for (int k = lane; k < NK; k += kWave) {
+    const Key u = half_key<F32>(row, k);
+    mx = u > mx ? u : mx;
+  }
+  const Key t0 = threshold_search<Key>(knn, kBits, [&](Key t) { return (int)__popcll(ballot(mx >= t)); });
+  int C = 0;
+  for (int k0 = 0; k0 < NK; k0 += kWave) {
+    const int k = k0 + lane;
+    const Key u = k < NK ? half_key<F32>(row, k) : (Key)0;
+    const bool take = k < NK && u >= t0;
+    const uint64_t m = ballot(take);
+    const int pos = C + lanes_below(m);
+    if (take && pos < kCap) cand[pos] = u;
+    C += (int)__popcll(m);
+  }
+  wave_lds_sync();
+  if (C <= kCap) {
+    topk_of_candidates<F32>(C, knn, cand, sel, out);
+    return;
+  }
+  const Key t1 = threshold_search<Key>(knn, kBits, [&](Key t) {
+    int cnt = 0;
+    for (int k0 = 0; k0 < NK; k0 += kWave) {
+      const int k = k0 + lane;
+      cnt += (int)__popcll(ballot(k < NK && half_key<F32>(row, k) >= t));
+    }
+    return cnt;
+  });
+  collect_sorted<Key>(NK, knn, t1, [&](int k) { return half_key<F32>(row, k); }, sel, out);
+}
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// order codes of one 16-byte chunk, in place: bf16 -> two 16-bit codes per dword; fp32 -> one code per dword
+template <bool F32>
+__device__ __forceinline__ uint4 chunk_codes(uint4 v) {
+  uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (F32) {
+      d[e] ^= (uint32_t)((int32_t)d[e] >> 31) | 0x80000000u;
+    } else {
+      const s16x2 sgn = __builtin_bit_cast(s16x2, d[e]) >> (short)15;  // 0xFFFF where negative
+      d[e] ^= __builtin_bit_cast(uint32_t, sgn) | 0x80008000u;
+    }
+  }
+  return uint4{d[0], d[1], d[2], d[3]};
+}
+
+// Register half top-k for NK = CPL * 64 chunks of 16 bytes (or fewer chunks, down to one).
+template <bool F32, int CPL>
+__device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
+                              typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
+  using Key = typename SelKey<F32>::T;
+  constexpr int EPC = F32 ? 4 : 8;  // elements per chunk
+  const int lane = lane_id();
+  const int nchunks = NK / EPC;
+
+  uint4 code[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + j * kWave;
+    code[j] = c < nchunks ? ((const uint4 *)row)[c] : uint4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + j * kWave;
+    code[j] = c < nchunks ? chunk_codes<F32>(code[j]) : uint4{0u, 0u, 0u, 0u};  // invalid -> code 0 (minimum)
+  }
+
+  // lane maximum of the codes, then code0 = knn-th largest lane maximum
+  uint32_t mx;
+  if constexpr (F32) {
+    mx = 0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) mx = max(max(max(mx, code[j].x), max(code[j].y, code[j].z)), code[j].w);
+  } else {
+    u16x2 pm = {0, 0};
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].x));
+      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].y));
+      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].z));
+      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].w));
+    }
+    mx = max((uint32_t)pm.x, (uint32_t)pm.y);
+  }
+  const uint32_t code0 = threshold_search<uint32_t>(knn, F32 ? 32 : 16,
+                                                    [&](uint32_t t) { return (int)__popcll(ballot(mx >= t)); });
+
+  // compact the elements with code >= code0 (valid ones only: code0 may be 0)
+  auto elem_code = [&](int j, int e) -> uint32_t {
+    const uint32_t d[4] = {code[j].x, code[j].y, code[j].z, code[j].w};
+    if constexpr (F32) return d[e];
+    else return (d[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+  };
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    if (lane + j * kWave >= nchunks) continue;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) mine += elem_code(j, e) >= code0;
+  }
+  int C;
+  int pos = wave_exclusive_sum(mine, &C);
+  if (C <= kCap) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = lane + j * kWave;
+      if (c >= nchunks) continue;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const uint32_t cd = elem_code(j, e);
+        if (cd >= code0) cand[pos++] = make_key<F32>(cd, (uint32_t)(c * EPC + e));
+      }
+    }
+    wave_lds_sync();
+    topk_of_candidates<F32>(C, knn, cand, sel, out);
+  } else {
+    half_topk_stream<F32>(row, NK, knn, cand, sel, out);
+  }
+}
+
+template <bool F32, int CPL>
 __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1, const void *__restrict__ s2,
                                                      int NK, int knn, void *__restrict__ scores,
                                                      int64_t *__restrict__ idx, float *__restrict__ w) {
@@ -141,7 +300,6 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
   __shared__ Key s_cand[2][kCap];
   __shared__ Key s_sel[2][kMaxKnn];
   __shared__ Key s_top[2][kMaxKnn];
-  __shared__ uint64_t s_ck[kMaxPairs];
   __shared__ uint64_t s_fsel[kMaxKnn];
   __shared__ uint64_t s_fin[kMaxKnn];
 
@@ -150,63 +308,58 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
   const int64_t row = blockIdx.x;  // n * H + h
   const size_t esz = F32 ? 4 : 2;
   const void *src = (const char *)(wave == 0 ? s1 : s2) + row * (int64_t)NK * esz;
-  half_topk<F32>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+  if constexpr (CPL > 0) half_topk_reg<F32, CPL>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+  else half_topk_stream<F32>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
   __syncthreads();
   if (wave != 0) return;
 
-  // Cartesian candidates: lane i < knn owns pairs (i, j), j < knn / (i + 1), at offset sum_{i'<i} knn/(i'+1)
-  const int cnt = lane < knn ? knn / (lane + 1) : 0;
-  int incl = cnt;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int v = __shfl_up(incl, o, kWave);
-    if (lane >= o) incl += v;
-  }
-  const int P = __shfl(incl, kWave - 1, kWave);
-  const int off = incl - cnt;
-  if (lane < knn) {
-    const Key k1 = s_top[0][lane];
-    const float v1 = key_value<F32>(k1);
-    const uint32_t i1 = key_index<F32>(k1);
-    for (int j = 0; j < cnt; ++j) {
-      const Key k2 = s_top[1][j];
-      const float s = v1 + key_value<F32>(k2);
-      const uint32_t code = F32 ? order32(__float_as_uint(s)) : order16(bf16_bits_rtne(s));
-      const uint32_t full = i1 * (uint32_t)NK + key_index<F32>(k2);
-      s_ck[off + j] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
+  // Cartesian candidates (i, j) with (i+1)(j+1) <= knn, spread over the lanes, keys held in registers
+  const int lg = 31 - __builtin_clz(knn);
+  const int base = kPairs.off[lg];
+  const int P = kPairs.off[lg + 1] - base;
+  uint64_t ck[kMaxPairSlots];
+  bool cv[kMaxPairSlots];
+#pragma unroll
+  for (int s = 0; s < kMaxPairSlots; ++s) {
+    const int p = s * kWave + lane;
+    cv[s] = p < P;
+    ck[s] = 0;
+    if (cv[s]) {
+      const Key k1 = s_top[0][kPairs.i[base + p]];
+      const Key k2 = s_top[1][kPairs.j[base + p]];
+      const float sum = key_value<F32>(k1) + key_value<F32>(k2);
+      const uint32_t code = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
+      const uint32_t full = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
+      ck[s] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
     }
   }
-  wave_lds_sync();
-
-  const uint64_t t = threshold_search<uint64_t>(knn, [&](uint64_t c) {
+  const uint64_t t = threshold_search<uint64_t>(knn, F32 ? 64 : 48, [&](uint64_t c) {
     int n = 0;
-    for (int p0 = 0; p0 < P; p0 += kWave) {
-      const int p = p0 + lane;
-      n += (int)__popcll(ballot(p < P && s_ck[p] >= c));
-    }
+#pragma unroll
+    for (int s = 0; s < kMaxPairSlots; ++s) n += (int)__popcll(ballot(cv[s] && ck[s] >= c));
     return n;
   });
   int S = 0;
-  for (int p0 = 0; p0 < P; p0 += kWave) {
-    const int p = p0 + lane;
-    const uint64_t u = p < P ? s_ck[p] : 0;
-    const bool ge = p < P && u >= t;
+#pragma unroll
+  for (int s = 0; s < kMaxPairSlots; ++s) {
+    const bool ge = cv[s] && ck[s] >= t;
     const uint64_t m = ballot(ge);
     const int pos = S + lanes_below(m);
-    if (ge && pos < kMaxKnn) s_fsel[pos] = u;
+    if (ge && pos < kMaxKnn) s_fsel[pos] = ck[s];
     S += (int)__popcll(m);
   }
   wave_lds_sync();
+  uint64_t mine = 0;
   if (lane < knn) {
-    const uint64_t u = s_fsel[lane];
+    mine = s_fsel[lane];
     int rank = 0;
-    for (int j = 0; j < knn; ++j) rank += s_fsel[j] > u;
-    s_fin[rank] = u;
+    for (int j = 0; j < knn; ++j) rank += s_fsel[j] > mine;
+    s_fin[rank] = mine;
   }
   wave_lds_sync();
 
   float sc = 0.f;
-  uint32_t full = 0;
-  uint32_t code = 0;
+  uint32_t full = 0, code = 0;
   if (lane < knn) {
     const uint64_t u = s_fin[lane];
     code = (uint32_t)(u >> 32);
@@ -223,6 +376,23 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
     idx[o] = (int64_t)full;
     w[o] = e / sum;
   }
+}
+
+template <bool F32>
+void launch_select(const void *s1, const void *s2, int64_t rows, int NK, int knn, void *scores, int64_t *idx,
+                   float *w, hipStream_t stream) {
+  const int epc = F32 ? 4 : 8;
+  const bool aligned = (((uintptr_t)s1 | (uintptr_t)s2) % 16) == 0 && NK % epc == 0;
+  const int chunks = NK / epc;
+  const dim3 grid((unsigned)rows), block(2 * kWave);
+#define SMLM_SELECT(CPL) \
+  hipLaunchKernelGGL((select_kernel<F32, CPL>), grid, block, 0, stream, s1, s2, NK, knn, scores, idx, w)
+  if (!aligned || chunks > 8 * kWave) SMLM_SELECT(0);
+  else if (chunks <= kWave) SMLM_SELECT(1);
+  else if (chunks <= 2 * kWave) SMLM_SELECT(2);
+  else if (chunks <= 4 * kWave) SMLM_SELECT(4);
+  else SMLM_SELECT(8);
+#undef SMLM_SELECT
 }
 
 }  // namespace
@@ -242,12 +412,7 @@ extern "C" int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_
   if (!is_pow2(NK) || NK > 65536 || NK < knn)
     return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select: NK=%d must be a power of two in [knn, 65536]", NK);
   if (N == 0) return SMLM_OK;
-  const dim3 grid((unsigned)(N * H));
-  if (dtype == SMLM_F32)
-    hipLaunchKernelGGL(select_kernel<true>, grid, dim3(2 * kWave), 0, (hipStream_t)stream, s1, s2, NK, knn,
-                       scores, idx, w);
-  else
-    hipLaunchKernelGGL(select_kernel<false>, grid, dim3(2 * kWave), 0, (hipStream_t)stream, s1, s2, NK, knn,
-                       scores, idx, w);
+  if (dtype == SMLM_F32) launch_select<true>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
+  else launch_select<false>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
   return launch_status("smlm_pkm_select");
 }
