@@ -101,6 +101,22 @@ int smlm_pkm_bag(const void *idx, int idx_dtype, const float *w, int64_t N, int 
 int smlm_pkm_quantize(const void *src, int src_dtype, int64_t rows, int D, int kind, void *codes,
                       uint16_t *scales, void *stream);
 
+/*
+ * Single-token decode attention over a static KV cache.  Replaces, for T = 1 with a preallocated cache, the
+ * attention of smlm/model.py:90-107 after the qkv projection: RoPE on the new q and k (model.py:63-78, the two
+ * halves of each head rotated), the cache append (model.py:94-98, here a write at a device-side position) and
+ * scaled dot-product attention over positions 0..pos (model.py:100-106), in one launch per layer.
+ *   qkv       (B, 3*H*head_dim) bf16, row b at qkv + b*qkv_row_stride: [q | k | v], each (H, head_dim)
+ *   rope_cos/rope_sin  (rope_len, head_dim/2) of rope_dtype (SMLM_F32 or SMLM_BF16)
+ *   pos       device int64 scalar: the new token's position (also its cache slot)
+ *   k_cache, v_cache   (B, H, max_len, head_dim) bf16, written at slot pos
+ *   out       (B, H*head_dim) bf16
+ * head_dim in {16, 32, 64, 128}.  A pos outside [0, min(max_len, rope_len)) writes no cache slot and NaN output.
+ */
+int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, const void *rope_cos, const void *rope_sin,
+                          int rope_dtype, int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B,
+                          int H, int head_dim, int max_len, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,207 @@
+// Single-token decode attention with a static KV cache: the attention of smlm/model.py:90-107 for one new token
+// per sequence (T = 1), fused into one kernel so the captured decode step does not pay ~35 small launches per
+// layer.  Per (sequence b, head h), one workgroup:
+//   1. RoPE (model.py:63-78: rotate the two halves of the head) on the new token's q and k, in fp32, rounded to
+//      bf16 as the bf16 model holds them; k and v are written into the cache at the device-side position `pos`;
+//   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos (the new token's own k from LDS), each cache row read
+//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles;
+//   3. softmax over t in fp32;
+//   4. y = sum_t p_t v_t, rows split over the workgroup's lanes, partial sums added through LDS; y is written as
+//      bf16 into the (B, H*head_dim) layout the output projection reads.
+// A position outside [0, min(max_len, rope_len)) writes nothing to the cache and NaN to the output.
+#include "pkm_common.h"
+
+namespace smlm {
+namespace {
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+
+template <bool ROPE_F32>
+__device__ __forceinline__ float table_val(const void *t, int64_t i) {
+  if constexpr (ROPE_F32) return ((const float *)t)[i];
+  else return bf16_bits_to_f32(((const uint16_t *)t)[i]);
+}
+
+__device__ __forceinline__ void unpack8(const uint4 v, float *f) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(u[e] << 16);
+    f[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
+  }
+}
+
+template <bool ROPE_F32, int HD>
+__global__ void __launch_bounds__(kAttnThreads)
+    decode_attention_kernel(const uint16_t *__restrict__ qkv, int64_t qkv_stride, const void *__restrict__ rope_cos,
+                            const void *__restrict__ rope_sin, int rope_len, const int64_t *__restrict__ pos_ptr,
+                            uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, int H, int max_len,
+                            uint16_t *__restrict__ out) {
+  constexpr int LPR = HD / 8;            // lanes per cache row (8 dims, 16 bytes each)
+  constexpr int RPW = kWave / LPR;       // rows per wavefront per pass
+  constexpr int RPB = RPW * kAttnWaves;  // rows per workgroup per pass
+  extern __shared__ __align__(16) float smem[];
+  float *s_q = smem;                     // [HD]
+  float *s_k = s_q + HD;                 // [HD] new token's k (bf16 values)
+  float *s_v = s_k + HD;                 // [HD]
+  float *s_red = s_v + HD;               // [RPB][HD] partial sums of p * v
+  float *s_w = s_red + RPB * HD;         // [kAttnWaves] wavefront partials
+  float *s_p = s_w + 2 * kAttnWaves;     // [max_len] scores, then probabilities
+
+  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
+  const int C = H * HD;
+  const int64_t P = *pos_ptr;
+  uint16_t *o = out + (int64_t)b * C + (int64_t)h * HD;
+  if (P < 0 || P >= max_len || P >= rope_len) {
+    for (int i = tid; i < HD; i += kAttnThreads) o[i] = 0x7FC0;  // bf16 NaN
+    return;
+  }
+  const uint16_t *row = qkv + (int64_t)b * qkv_stride;
+  const int64_t cache_row = ((int64_t)b * H + h) * max_len;
+
+  // 1. RoPE on q, k; v as is; new k, v into the cache
+  for (int i = tid; i < HD / 2; i += kAttnThreads) {
+    const float c = table_val<ROPE_F32>(rope_cos, P * (HD / 2) + i);
+    const float s = table_val<ROPE_F32>(rope_sin, P * (HD / 2) + i);
+    const float q1 = bf16_bits_to_f32(row[h * HD + i]), q2 = bf16_bits_to_f32(row[h * HD + HD / 2 + i]);
+    const float k1 = bf16_bits_to_f32(row[C + h * HD + i]), k2 = bf16_bits_to_f32(row[C + h * HD + HD / 2 + i]);
+    s_q[i] = round_bf16(q1 * c - q2 * s);
+    s_q[i + HD / 2] = round_bf16(q1 * s + q2 * c);
+    const uint32_t ka = bf16_bits_rtne(k1 * c - k2 * s), kb = bf16_bits_rtne(k1 * s + k2 * c);
+    s_k[i] = bf16_bits_to_f32(ka);
+    s_k[i + HD / 2] = bf16_bits_to_f32(kb);
+    k_cache[(cache_row + P) * HD + i] = (uint16_t)ka;
+    k_cache[(cache_row + P) * HD + HD / 2 + i] = (uint16_t)kb;
+  }
+  for (int i = tid; i < HD; i += kAttnThreads) {
+    const uint16_t vb = row[2 * C + h * HD + i];
+    s_v[i] = bf16_bits_to_f32(vb);
+    v_cache[(cache_row + P) * HD + i] = vb;
+  }
+  __syncthreads();
+
+  // 2. scores
+  const int sub = lane % LPR, rw = lane / LPR;
+  const float scale = rsqrtf((float)HD);
+  float qf[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qf[e] = s_q[sub * 8 + e];
+  for (int t0 = 0; t0 <= P; t0 += RPB) {
+    const int t = t0 + wave * RPW + rw;
+    float kf[8];
+    if (t < P) {
+      unpack8(*(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8), kf);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[e] = t == P ? s_k[sub * 8 + e] : 0.f;
+    }
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) d += __shfl_xor(d, m, kWave);
+    if (sub == 0 && t <= P) s_p[t] = d * scale;
+  }
+  __syncthreads();
+
+  // 3. softmax over t = 0..P
+  float mx = -INFINITY;
+  for (int t = tid; t <= P; t += kAttnThreads) mx = fmaxf(mx, s_p[t]);
+  for (int m = kWave / 2; m > 0; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
+  if (lane == 0) s_w[wave] = mx;
+  __syncthreads();
+  mx = s_w[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) mx = fmaxf(mx, s_w[w]);
+  float sum = 0.f;
+  for (int t = tid; t <= P; t += kAttnThreads) {
+    const float e = expf(s_p[t] - mx);
+    s_p[t] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) s_w[kAttnWaves + wave] = sum;
+  __syncthreads();
+  sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) sum += s_w[kAttnWaves + w];
+
+  // 4. y = sum_t p_t v_t / sum
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int t = wave * RPW + rw; t <= P; t += RPB) {
+    const float pt = s_p[t];
+    float vf[8];
+    if (t < P) {
+      unpack8(*(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8), vf);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vf[e] = s_v[sub * 8 + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
+  }
+  const int slot = wave * RPW + rw;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_red[slot * HD + sub * 8 + e] = acc[e];
+  __syncthreads();
+  const float inv = 1.0f / sum;
+  for (int i = tid; i < HD; i += kAttnThreads) {
+    float y = 0.f;
+    for (int r = 0; r < RPB; ++r) y += s_red[r * HD + i];
+    o[i] = (uint16_t)bf16_bits_rtne(y * inv);
+  }
+}
+
+template <int HD>
+int launch_attention(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
+                     int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
+                     void *out, hipStream_t stream) {
+  constexpr int RPB = (kWave / (HD / 8)) * kAttnWaves;
+  const size_t shmem = sizeof(float) * (3 * HD + RPB * HD + 2 * kAttnWaves + (size_t)max_len);
+  if (shmem > 64 * 1024)
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len=%d too long for one workgroup", max_len);
+  const dim3 grid((unsigned)(B * H));
+  if (rope_f32)
+    hipLaunchKernelGGL((decode_attention_kernel<true, HD>), grid, dim3(kAttnThreads), shmem, stream,
+                       (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
+                       (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
+  else
+    hipLaunchKernelGGL((decode_attention_kernel<false, HD>), grid, dim3(kAttnThreads), shmem, stream,
+                       (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
+                       (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
+  return launch_status("smlm_decode_attention");
+}
+
+}  // namespace
+}  // namespace smlm
+
+extern "C" int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, const void *rope_cos,
+                                     const void *rope_sin, int rope_dtype, int rope_len, const int64_t *pos,
+                                     void *k_cache, void *v_cache, int64_t B, int H, int head_dim, int max_len,
+                                     void *out, void *stream) {
+  using namespace smlm;
+  if (!qkv || !rope_cos || !rope_sin || !pos || !k_cache || !v_cache || !out)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: null pointer argument");
+  if (rope_dtype != SMLM_F32 && rope_dtype != SMLM_BF16)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: rope tables must be SMLM_F32 or SMLM_BF16");
+  if (B < 0 || H < 1 || max_len < 1 || rope_len < 1 || B * (int64_t)H > 0x7FFFFFFFLL)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: bad shape B=%lld H=%d max_len=%d", (long long)B, H, max_len);
+  if (qkv_row_stride < 3LL * H * head_dim)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv_row_stride %lld < 3*H*head_dim", (long long)qkv_row_stride);
+  if ((((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) || qkv_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv and caches must be 16-byte aligned");
+  if (B == 0) return SMLM_OK;
+  const int f32 = rope_dtype == SMLM_F32;
+  hipStream_t s = (hipStream_t)stream;
+  switch (head_dim) {
+    case 16: return launch_attention<16>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
+    case 32: return launch_attention<32>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
+    case 64: return launch_attention<64>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
+    case 128: return launch_attention<128>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
+    default: return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: head_dim %d not in {16, 32, 64, 128}", head_dim);
+  }
+}

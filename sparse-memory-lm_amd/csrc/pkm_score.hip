@@ -63,8 +63,8 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
         if constexpr (F32) {
-          const float *fa = (const float *)&a[i];
-          const float *fb = (const float *)&b[j];
+          const floatx4 fa = __builtin_bit_cast(floatx4, a[i]);
+          const floatx4 fb = __builtin_bit_cast(floatx4, b[j]);
 #pragma unroll
           for (int s = 0; s < 4; ++s)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s], fb[s], acc[i][j], 0, 0, 0);
@@ -95,12 +95,120 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
           *(uint2 *)(out + o * 2) = pk;
         }
       } else {
-        for (int e = 0; e < 4 && key + e < NK; ++e) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (key + e >= NK) continue;
           if constexpr (F32) ((float *)out)[o + e] = v[e];
           else ((uint16_t *)out)[o + e] = (uint16_t)bf16_bits_rtne(v[e]);
         }
       }
     }
+}
+
+// bf16, many tokens: 128 sub-keys x 128 tokens per workgroup (2 x 2 wavefronts of 64 x 64), the contraction in
+// chunks of 64 dims staged through LDS.  LDS rows are padded to 72 bf16 (144 B) so the 16 rows a fragment read
+// touches fall on disjoint banks; three resident workgroups per CU overlap one's loads with another's MFMAs.
+constexpr int kLdsKC = 64;            // dims per LDS chunk
+constexpr int kLdsRS = kLdsKC + 8;    // LDS row stride (bf16 elements)
+
+template <int WM, int WN>
+__global__ void __launch_bounds__(256)
+    score_lds_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
+                     int H, int NK, int half, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
+  constexpr int BM = 2 * 16 * WM, BN = 2 * 16 * WN;
+  constexpr int PPR = kLdsKC / 8;                      // 16-byte pieces per tile row and chunk
+  constexpr int PA = BM * PPR / 256, PB = BN * PPR / 256;
+  __shared__ __align__(16) uint16_t sAB[(BM + BN) * kLdsRS];
+  uint16_t *sA = sAB, *sB = sAB + BM * kLdsRS;
+  // 1-D grid, XCD-aware: workgroup b runs on XCD b % 8, so tile t = (b % 8) * per_xcd + b / 8 gives each XCD a
+  // contiguous run of tiles; tiles are ordered sub-key tile fastest, so an XCD's L2 reads each token tile's
+  // queries once and reuses them for all sub-key tiles of that (head, half).
+  const int key_tiles = (NK + BM - 1) / BM, tok_tiles = (N + BN - 1) / BN;
+  const int per_xcd = gridDim.x / 8;
+  const int t = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (t >= key_tiles * tok_tiles * 2 * H) return;
+  const int z = t / (key_tiles * tok_tiles);
+  const int h = z >> 1, p = z & 1;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int r = lane & 15, g = lane >> 4;
+  const int key0 = (t % key_tiles) * BM, tok0 = ((t / key_tiles) % tok_tiles) * BN;
+  const uint16_t *kbase = keys + (int64_t)(h * 2 + p) * NK * half;
+  const uint16_t *qbase = q + (int64_t)h * 2 * half + (int64_t)p * half;
+  const uint4 zero = {0u, 0u, 0u, 0u};
+
+  floatx4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = 0; k0 < half; k0 += kLdsKC) {
+    __syncthreads();  // the previous chunk's fragment reads are done
+    // stage chunk k0 of both tiles (zero outside the table, the tokens or the half)
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+      const int piece = tid + 256 * i, row = piece / PPR, kk = k0 + (piece % PPR) * 8;
+      const int key = key0 + row;
+      const uint4 v = (key < NK && kk < half) ? *(const uint4 *)(kbase + (int64_t)key * half + kk) : zero;
+      *(uint4 *)&sA[row * kLdsRS + (piece % PPR) * 8] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const int piece = tid + 256 * i, row = piece / PPR, kk = k0 + (piece % PPR) * 8;
+      const int tok = tok0 + row;
+      const uint4 v = (tok < N && kk < half) ? *(const uint4 *)(qbase + (int64_t)tok * q_stride + kk) : zero;
+      *(uint4 *)&sB[row * kLdsRS + (piece % PPR) * 8] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kLdsKC; ks += 32) {
+      bf16x8 a[WM], b[WN];
+#pragma unroll
+      for (int i = 0; i < WM; ++i) a[i] = *(const bf16x8 *)&sA[(wm * 16 * WM + i * 16 + r) * kLdsRS + ks + g * 8];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b[j] = *(const bf16x8 *)&sB[(wn * 16 * WN + j * 16 + r) * kLdsRS + ks + g * 8];
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue through LDS: the bf16 tile is written as [token][sub-key] rows (padded to kOutRS), then stored with
+  // 16-byte loads per lane covering whole 256-byte token rows of the output.
+  constexpr int kOutRS = BM + 8;
+  static_assert(BN * kOutRS <= (BM + BN) * kLdsRS, "output tile must fit in the operand LDS");
+  uint16_t *sOut = sA;  // sA and sB are contiguous in LDS; the tile spans both
+  __syncthreads();      // all fragment reads of the last chunk are done
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const floatx4 v = acc[i][j];
+      uint2 pk;
+      pk.x = bf16_bits_rtne(v[0]) | (bf16_bits_rtne(v[1]) << 16);
+      pk.y = bf16_bits_rtne(v[2]) | (bf16_bits_rtne(v[3]) << 16);
+      *(uint2 *)&sOut[(wn * 16 * WN + j * 16 + r) * kOutRS + wm * 16 * WM + i * 16 + g * 4] = pk;
+    }
+  __syncthreads();
+  uint16_t *out = p ? s2 : s1;
+  constexpr int PPT = BM / 8;  // 16-byte pieces per token row of the tile
+#pragma unroll
+  for (int k = 0; k < BN * PPT / 256; ++k) {
+    const int piece = tid + 256 * k, tl = piece / PPT, kl = (piece % PPT) * 8;
+    const int tok = tok0 + tl, key = key0 + kl;
+    if (tok >= N || key >= NK) continue;
+    const int64_t o = ((int64_t)tok * H + h) * NK + key;
+    const uint4 v = *(const uint4 *)&sOut[tl * kOutRS + kl];
+    if ((NK & 7) == 0) {
+      *(uint4 *)(out + o) = v;
+    } else {
+      const uint16_t *e = (const uint16_t *)&v;
+      for (int x = 0; x < 8; ++x)
+        if (key + x < NK) out[o + x] = e[x];
+    }
+  }
 }
 
 template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N>
@@ -115,10 +223,18 @@ void launch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, 
 template <bool F32>
 void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                     void *s2, hipStream_t stream) {
-  if (N <= 16)  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
+  if (N <= 16) {  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
     launch_score<F32, 2, 1, 4, 1>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
-  else          // 128 sub-keys x 64 tokens per workgroup
+  } else if (F32 || N <= 64 || (N / 128 + 1) * (NK / 128 + 1) * 2 * (int64_t)H >= (1LL << 30)) {
+    // 128 sub-keys x 64 tokens per workgroup, operands straight from memory
     launch_score<F32, 4, 2, 2, 2>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
+  } else {        // bf16, many tokens: LDS-staged 128 x 128 tiles
+    constexpr int BM = 128, BN = 128;
+    const int64_t tiles = ((NK + BM - 1) / BM) * ((N + BN - 1) / BN) * 2 * (int64_t)H;
+    const dim3 grid((unsigned)(8 * ((tiles + 7) / 8)));  // a multiple of 8: every XCD gets the same count
+    hipLaunchKernelGGL((score_lds_kernel<4, 4>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+                       (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
+  }
 }
 
 }  // namespace

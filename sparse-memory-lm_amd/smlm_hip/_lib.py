@@ -26,6 +26,7 @@ EXPORTS = {
     "smlm_pkm_select": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "smlm_pkm_bag": (_i, [_p, _i, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p]),
     "smlm_pkm_quantize": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
+    "smlm_decode_attention": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _p]),
 }
 
 _lib = None

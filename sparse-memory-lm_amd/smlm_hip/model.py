@@ -3,8 +3,10 @@ Transformer.forward(idx, targets, kv_caches, pos0), set_memory_decode_graphs, se
 with the memory layers on the gfx950 lookup of smlm_hip.pkm, plus a whole-decode-step HIP graph
 (Transformer.generate) over a static KV cache.
 
-The dense parts (RMSNorm, RoPE, SDPA attention, SwiGLU, tied lm_head) are PyTorch ops with the reference's
-arithmetic; state_dict keys are the reference's, so a reference checkpoint of a supported config loads as is.
+The dense parts (RMSNorm, RoPE, attention, SwiGLU, tied lm_head) are PyTorch ops with the reference's arithmetic,
+except the single-token decode step over the static cache, whose RoPE + cache write + attention is one HIP kernel
+(smlm_hip.kernels.decode_attention); state_dict keys are the reference's, so a reference checkpoint of a supported
+config loads as is.
 """
 import math
 from dataclasses import asdict, dataclass, field
@@ -104,6 +106,12 @@ class Attention(nn.Module):
 
     def forward(self, x, kv_cache=None, pos0=0):
         B, T, C = x.shape
+        if (T == 1 and torch.is_tensor(pos0) and isinstance(kv_cache, StaticKVCache) and x.is_cuda
+                and kv_cache.k.dtype == torch.bfloat16 and self.head_dim in (16, 32, 64, 128)):
+            # one decode step: RoPE, cache write and attention in one kernel (smlm_hip.kernels.decode_attention)
+            qkv = self.wqkv(x).view(B, 3 * C).to(torch.bfloat16)
+            y = kernels.decode_attention(qkv, self.rope.cos, self.rope.sin, pos0, kv_cache.k, kv_cache.v)
+            return self.wo(y.view(B, 1, C).to(x.dtype))
         q, k, v = self.wqkv(x).view(B, T, 3, self.n_heads, self.head_dim).permute(2, 0, 3, 1, 4)
         q, k = self.rope(q, pos0), self.rope(k, pos0)
         if isinstance(kv_cache, StaticKVCache):

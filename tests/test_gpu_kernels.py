@@ -124,7 +124,8 @@ def test_pk_select_golden():
 
 # ------------------------------------------------------------------------------------------------ scoring
 SCORE_SHAPES = [(1, 4, 4096, 256), (64, 4, 4096, 256), (2048, 4, 1024, 256), (100, 4, 2048, 256),
-                (5, 2, 16, 8), (17, 3, 64, 32), (300, 1, 512, 64)]
+                (5, 2, 16, 8), (17, 3, 64, 32), (300, 1, 512, 64), (1000, 4, 2048, 256), (200, 2, 64, 40),
+                (129, 3, 16, 8), (65, 2, 384, 128)]
 
 
 def _score_inputs(N, H, NK, half, seed):
@@ -325,3 +326,65 @@ def test_quantize_golden():
         codes, sc = K.quantize_q4(torch.tensor([case["row"]], dtype=torch.float32, device=DEV))
         assert codes[0].tolist() == case["packed"]
         assert int(sc.cpu().view(torch.int16)[0]) & 0xFFFF == case["scale_f16_bits"]
+
+
+# ------------------------------------------------------------------------------------------------ decode attention
+def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
+    """fp64 restatement: RoPE (oracle/torch_path.rope convention: rotate the two halves), then softmax attention
+    of the new token over cached slots 0..P-1 and itself."""
+    B = qkv.shape[0]
+    C = H * hd
+    q = qkv[:, :C].view(B, H, hd).double()
+    k = qkv[:, C:2 * C].view(B, H, hd).double()
+    v = qkv[:, 2 * C:].view(B, H, hd).double()
+    c, s = cos[P].double(), sin[P].double()
+
+    def rot(x):
+        a, b = x[..., :hd // 2], x[..., hd // 2:]
+        return torch.cat([a * c - b * s, a * s + b * c], -1)
+    qr, kr = rot(q), rot(k)
+    kr_b = kr.to(torch.bfloat16)
+    keys = torch.cat([kc[:, :, :P].double(), kr_b.double().unsqueeze(2)], 2)
+    vals = torch.cat([vc[:, :, :P].double(), v.unsqueeze(2)], 2)
+    sc = torch.einsum("bhd,bhtd->bht", qr.to(torch.bfloat16).double(), keys) / hd ** 0.5
+    y = torch.einsum("bht,bhtd->bhd", torch.softmax(sc, -1), vals)
+    return y.reshape(B, C), kr_b
+
+
+@pytest.mark.parametrize("B,H,hd,max_len,P,rope", [(64, 6, 64, 394, 300, "bf16"), (1, 6, 64, 394, 0, "bf16"),
+                                                    (1, 6, 64, 394, 393, "f32"), (3, 4, 32, 100, 57, "f32"),
+                                                    (2, 2, 16, 40, 1, "bf16"), (2, 3, 128, 300, 299, "bf16"),
+                                                    (5, 6, 64, 600, 511, "f32")])
+def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
+    note(f"decode attention B={B} H={H} hd={hd} max_len={max_len} P={P}")
+    g = torch.Generator().manual_seed(B * 1000 + P)
+    C = H * hd
+    qkv = torch.randn(B, 3 * C, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, H, max_len, hd, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, H, max_len, hd, generator=g).to(torch.bfloat16)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2).float() / hd))
+    ang = torch.outer(torch.arange(max_len).float(), inv)
+    dt = torch.bfloat16 if rope == "bf16" else torch.float32
+    cos, sin = ang.cos().to(dt), ang.sin().to(dt)
+    ref, kr = _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd)
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    out = K.decode_attention(qkv.to(DEV), cos.to(DEV), sin.to(DEV), torch.tensor(P, device=DEV), kd, vd)
+    got = out.float().cpu().double()
+    torch.testing.assert_close(got, ref, rtol=2 ** -7, atol=2 ** -7 * float(ref.abs().max()))
+    # the new slot holds the rotated k (within one bf16 ulp of the fp64 rotation) and v; other slots untouched
+    torch.testing.assert_close(kd[:, :, P].cpu().float(), kr.float(), rtol=2 ** -7, atol=1e-6)
+    assert torch.equal(vd[:, :, P].cpu(), qkv[:, 2 * C:].view(B, H, hd))
+    keep = [t for t in range(max_len) if t != P]
+    assert torch.equal(kd[:, :, keep].cpu(), kc[:, :, keep]) and torch.equal(vd[:, :, keep].cpu(), vc[:, :, keep])
+
+
+def test_decode_attention_bad_position():
+    B, H, hd, L = 2, 2, 64, 16
+    qkv = torch.randn(B, 3 * H * hd, device=DEV).to(torch.bfloat16)
+    kc = torch.zeros(B, H, L, hd, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    cos = torch.ones(L, hd // 2, device=DEV)
+    for P in (L, -1, 10 ** 6):
+        out = K.decode_attention(qkv, cos, cos, torch.tensor(P, device=DEV), kc, vc)
+        assert torch.isnan(out.float()).all()
+    assert not kc.any() and not vc.any()
