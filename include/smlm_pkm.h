@@ -117,6 +117,33 @@ int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, const void *r
                           int rope_dtype, int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B,
                           int H, int head_dim, int max_len, void *out, void *stream);
 
+/*
+ * SwiGLU activation of the dense FFN.  Replaces `a, b = w13(x).chunk(2, -1); F.silu(a) * b` of
+ * smlm/model.py:110-118 (after the w13 projection) in one launch, with the reference's bf16 roundings:
+ *   out[m, c] = bf16( bf16(silu(a[m, c])) * b[m, c] ),  a = in[m, :hidden], b = in[m, hidden:2*hidden]
+ *   in   (M, 2*hidden) bf16, row m at in + m*in_row_stride;  out (M, hidden) bf16 dense.  hidden % 8 == 0.
+ */
+int smlm_swiglu(const void *in, int64_t in_row_stride, void *out, int64_t M, int hidden, void *stream);
+
+/*
+ * Greedy token choice of the decode loop (smlm/train.py:297-299, `nxt = logits[:, -1:].argmax(-1)`): per row
+ * the first index of the largest bf16 logit, written to tok[b]; if hist is given, also to
+ * hist[b, *pos + 1] (skipped when that slot is outside [0, hist_len)).
+ *   logits (B, V) bf16, row b at logits + b*row_stride;  tok (B,) int64;  pos device int64 scalar.
+ */
+int smlm_greedy_argmax(const void *logits, int64_t row_stride, int64_t B, int V, const int64_t *pos, int64_t *tok,
+                       int64_t *hist, int64_t hist_row_stride, int64_t hist_len, void *stream);
+
+/*
+ * Residual add + RMSNorm of the decoder blocks (smlm/model.py:124-126, 156-163: `x = x + sublayer(...)` followed by
+ * the next sublayer's `norm(x)`), one launch per pair:
+ *   x_out = bf16(x + delta);   h_out = bf16(x_out * rsqrt(mean(x_out^2) + eps) * weight)   (fp32 statistics)
+ * With delta == NULL only the norm of x is computed (x_out unused).  x, delta, x_out, h_out (M, C) bf16 dense;
+ * weight (C,) bf16.
+ */
+int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float eps, int64_t M, int C, void *x_out,
+                     void *h_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -205,3 +205,161 @@ extern "C" int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, co
     default: return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: head_dim %d not in {16, 32, 64, 128}", head_dim);
   }
 }
+
+// ---- SwiGLU activation (smlm/model.py:110-118): out = bf16(silu(a)) * b rounded to bf16, a | b = halves of the
+// w13 projection.  The two roundings are the ones the bf16 reference makes (F.silu rounds to bf16, then the
+// product rounds).  8 outputs per thread with 16-byte loads and stores.
+namespace smlm {
+namespace {
+
+__global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t *__restrict__ in, int64_t in_stride,
+                                                     uint16_t *__restrict__ out, int64_t M, int hidden) {
+  const int per_row = hidden / 8;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= M * per_row) return;
+  const int64_t m = item / per_row;
+  const int c = (int)(item % per_row) * 8;
+  const uint4 av = *(const uint4 *)(in + m * in_stride + c);
+  const uint4 bv = *(const uint4 *)(in + m * in_stride + hidden + c);
+  float a[8], b[8];
+  unpack8(av, a);
+  unpack8(bv, b);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float s0 = round_bf16(a[2 * e] / (1.0f + expf(-a[2 * e])));
+    const float s1 = round_bf16(a[2 * e + 1] / (1.0f + expf(-a[2 * e + 1])));
+    o[e] = bf16_bits_rtne(s0 * b[2 * e]) | (bf16_bits_rtne(s1 * b[2 * e + 1]) << 16);
+  }
+  *(uint4 *)(out + m * hidden + c) = uint4{o[0], o[1], o[2], o[3]};
+}
+
+// ---- greedy step (smlm/train.py:297-299: nxt = logits[:, -1:].argmax(-1)): per row the first index of the
+// largest logit; the token is written to tok[b] and to hist[b, pos + 1] (pos read on the device).  1024 threads
+// per row, 16-byte loads; keys (order code << 32 | ~index) make "largest value, then lowest index" one max.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ uint64_t argmax_key(uint32_t bits, int i) {
+  return ((uint64_t)order16(bits) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+__global__ void __launch_bounds__(kArgmaxThreads)
+    argmax_kernel(const uint16_t *__restrict__ logits, int64_t row_stride, int V, const int64_t *__restrict__ pos,
+                  int64_t *__restrict__ tok, int64_t *__restrict__ hist, int64_t hist_stride, int64_t hist_len,
+                  int vec) {
+  __shared__ uint64_t s_best[kArgmaxThreads / kWave];
+  const int b = blockIdx.x;
+  const uint16_t *row = logits + (int64_t)b * row_stride;
+  uint64_t best = 0;
+  if (vec) {  // row 16-byte aligned, V % 8 == 0
+    for (int c = threadIdx.x; c < V / 8; c += kArgmaxThreads) {
+      const uint4 v = *(const uint4 *)(row + c * 8);
+      const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t k0 = argmax_key(u[e] & 0xFFFFu, c * 8 + 2 * e);
+        const uint64_t k1 = argmax_key(u[e] >> 16, c * 8 + 2 * e + 1);
+        best = k0 > best ? k0 : best;
+        best = k1 > best ? k1 : best;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < V; i += kArgmaxThreads) {
+      const uint64_t k = argmax_key(row[i], i);
+      best = k > best ? k : best;
+    }
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const uint64_t other = __shfl_xor(best, o, kWave);
+    best = other > best ? other : best;
+  }
+  if (lane_id() == 0) s_best[threadIdx.x / kWave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    best = s_best[0];
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) best = s_best[w] > best ? s_best[w] : best;
+    const int64_t t = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
+    tok[b] = t;
+    if (hist) {
+      const int64_t slot = *pos + 1;
+      if (slot >= 0 && slot < hist_len) hist[(int64_t)b * hist_stride + slot] = t;
+    }
+  }
+}
+
+// ---- residual add + RMSNorm (smlm/model.py:124-126, 156-163: x = x + sublayer(...); h = norm(x)): one wavefront
+// per row writes x + delta (bf16, the residual stream) and RMSNorm of it (fp32 statistics, bf16 out), so the add
+// and the next sublayer's norm are one launch.
+__global__ void __launch_bounds__(256) add_rmsnorm_kernel(const uint16_t *__restrict__ x,
+                                                          const uint16_t *__restrict__ delta,
+                                                          const uint16_t *__restrict__ weight, float eps, int64_t M,
+                                                          int C, uint16_t *__restrict__ x_out,
+                                                          uint16_t *__restrict__ h_out) {
+  const int64_t m = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (m >= M) return;
+  const int lane = lane_id();
+  const uint16_t *xr = x + m * C;
+  const uint16_t *dr = delta ? delta + m * C : nullptr;
+  float ss = 0.f;
+  for (int c = lane; c < C; c += kWave) {
+    float v = bf16_bits_to_f32(xr[c]);
+    if (dr) v = round_bf16(v + bf16_bits_to_f32(dr[c]));
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float rstd = rsqrtf(ss / (float)C + eps);
+  for (int c = lane; c < C; c += kWave) {
+    float v = bf16_bits_to_f32(xr[c]);
+    if (dr) {
+      v = round_bf16(v + bf16_bits_to_f32(dr[c]));
+      x_out[m * C + c] = (uint16_t)bf16_bits_rtne(v);
+    }
+    h_out[m * C + c] = (uint16_t)bf16_bits_rtne(v * rstd * bf16_bits_to_f32(weight[c]));
+  }
+}
+
+}  // namespace
+}  // namespace smlm
+
+extern "C" int smlm_swiglu(const void *in, int64_t in_row_stride, void *out, int64_t M, int hidden, void *stream) {
+  using namespace smlm;
+  if (!in || !out) return fail(SMLM_EINVAL, "smlm_swiglu: null pointer");
+  if (M < 0 || hidden < 8 || hidden % 8 || in_row_stride < 2LL * hidden || in_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_swiglu: bad shape M=%lld hidden=%d stride=%lld", (long long)M, hidden,
+                (long long)in_row_stride);
+  if ((((uintptr_t)in | (uintptr_t)out) % 16))
+    return fail(SMLM_EINVAL, "smlm_swiglu: in and out must be 16-byte aligned");
+  const int64_t items = M * (hidden / 8);
+  if (items == 0) return SMLM_OK;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t *)in, in_row_stride, (uint16_t *)out, M, hidden);
+  return launch_status("smlm_swiglu");
+}
+
+extern "C" int smlm_greedy_argmax(const void *logits, int64_t row_stride, int64_t B, int V, const int64_t *pos,
+                                  int64_t *tok, int64_t *hist, int64_t hist_row_stride, int64_t hist_len,
+                                  void *stream) {
+  using namespace smlm;
+  if (!logits || !tok || (hist && !pos)) return fail(SMLM_EINVAL, "smlm_greedy_argmax: null pointer");
+  if (B < 0 || B > 0x7FFFFFFFLL || V < 1 || row_stride < V)
+    return fail(SMLM_EINVAL, "smlm_greedy_argmax: bad shape B=%lld V=%d", (long long)B, V);
+  if (B == 0) return SMLM_OK;
+  const int vec = (((uintptr_t)logits % 16) == 0 && row_stride % 8 == 0 && V % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)B), dim3(kArgmaxThreads), 0, (hipStream_t)stream,
+                     (const uint16_t *)logits, row_stride, V, pos, tok, hist, hist_row_stride, hist_len, vec);
+  return launch_status("smlm_greedy_argmax");
+}
+
+extern "C" int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float eps, int64_t M, int C,
+                                void *x_out, void *h_out, void *stream) {
+  using namespace smlm;
+  if (!x || !weight || !h_out || (delta && !x_out)) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: null pointer");
+  if (M < 0 || C < 1 || !(eps >= 0.f)) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: bad shape or eps");
+  if (M == 0) return SMLM_OK;
+  const int64_t blocks = (M + 3) / 4;
+  if (blocks > 0x7FFFFFFFLL) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: M too large");
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)blocks), dim3(4 * kWave), 0, (hipStream_t)stream,
+                     (const uint16_t *)x, (const uint16_t *)delta, (const uint16_t *)weight, eps, M, C,
+                     (uint16_t *)x_out, (uint16_t *)h_out);
+  return launch_status("smlm_add_rmsnorm");
+}

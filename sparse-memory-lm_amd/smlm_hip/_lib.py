@@ -27,6 +27,9 @@ EXPORTS = {
     "smlm_pkm_bag": (_i, [_p, _i, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p]),
     "smlm_pkm_quantize": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
     "smlm_decode_attention": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _p]),
+    "smlm_swiglu": (_i, [_p, _i64, _p, _i64, _i, _p]),
+    "smlm_greedy_argmax": (_i, [_p, _i64, _i64, _i, _p, _p, _p, _i64, _i64, _p]),
+    "smlm_add_rmsnorm": (_i, [_p, _p, _p, ctypes.c_float, _i64, _i, _p, _p, _p]),
 }
 
 _lib = None

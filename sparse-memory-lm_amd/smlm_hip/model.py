@@ -173,8 +173,15 @@ class SwiGLU(nn.Module):
         self.w2 = nn.Linear(hidden, d, bias=False)
 
     def forward(self, x):
-        a, b = self.w13(x).chunk(2, dim=-1)
-        return self.w2(F.silu(a) * b)
+        """w2(silu(a) * b) with a | b = w13(x).  On bf16 GPU tensors the activation is one kernel
+        (smlm_hip.kernels.swiglu) with the same roundings."""
+        h = self.w13(x)
+        if h.is_cuda and h.dtype == torch.bfloat16 and h.shape[-1] % 16 == 0:
+            act = kernels.swiglu(h)
+        else:
+            a, b = h.chunk(2, dim=-1)
+            act = F.silu(a) * b
+        return self.w2(act)
 
 
 def _memory(cfg, shared):
@@ -292,13 +299,34 @@ class Transformer(nn.Module):
     def forward(self, idx, targets=None, kv_caches=None, pos0=0):
         """Logits (B, T, vocab), or (logits, loss) with targets (smlm/model.py:266-293)."""
         x = self.tok_emb(idx)
-        for i, blk in enumerate(self.layers):
-            x = blk(x, None if kv_caches is None else kv_caches[i], pos0)
-        logits = self.lm_head(self.norm(x))
+        if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_autocast_enabled("cuda"):
+            logits = self.lm_head(self._blocks_fused_norms(x, kv_caches, pos0))
+        else:
+            for i, blk in enumerate(self.layers):
+                x = blk(x, None if kv_caches is None else kv_caches[i], pos0)
+            logits = self.lm_head(self.norm(x))
         if targets is None:
             return logits
         loss = F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.reshape(-1))
         return logits, loss
+
+    def _blocks_fused_norms(self, x, kv_caches, pos0):
+        """The blocks of forward() on bf16 GPU tensors with every residual add fused into the RMSNorm that follows
+        it (smlm_hip.kernels.add_rmsnorm): the same sequence x = x + sublayer(norm(x)) per sublayer, ending with
+        the final norm.  Returns the normed last hidden state."""
+        norms, subs = [], []
+        for i, blk in enumerate(self.layers):
+            cache = None if kv_caches is None else kv_caches[i]
+            norms += [blk.attn_norm, blk.ffn_norm]
+            subs += [lambda h, blk=blk, cache=cache: blk.attn(h, cache, pos0), blk.ffn]
+            if blk.ffn_r2 is not None:
+                norms.append(blk.ffn_norm_r2)
+                subs.append(blk.ffn_r2)
+        norms.append(self.norm)
+        x, h = kernels.add_rmsnorm(x, None, norms[0])
+        for sub, norm in zip(subs, norms[1:]):
+            x, h = kernels.add_rmsnorm(x, sub(h), norm)
+        return h
 
     # ---- whole-step graph decode -------------------------------------------------------------------------
     @torch.no_grad()
@@ -339,9 +367,14 @@ class _StepDecoder:
 
     def _step(self):
         logits = self.model(self.tok, kv_caches=self.caches, pos0=self.pos)
-        nxt = logits[:, -1].argmax(-1, keepdim=True)
-        self.hist.index_copy_(1, (self.pos + 1).view(1), nxt)
-        self.tok.copy_(nxt)
+        last = logits[:, -1]
+        if last.is_cuda and last.dtype == torch.bfloat16:
+            # argmax, next token and its history slot in one kernel
+            kernels.greedy_argmax(last, self.pos, self.tok.view(-1), self.hist)
+        else:
+            nxt = last.argmax(-1, keepdim=True)
+            self.hist.index_copy_(1, (self.pos + 1).view(1), nxt)
+            self.tok.copy_(nxt)
         self.pos.add_(1)
 
     def _capture(self):

@@ -91,6 +91,7 @@ class ProductKeyMemory(nn.Module):
         self.decode_graph = False
         self._graph = None
         self._keys_cache = None
+        self._bn_cache = None
         self.reset_parameters()
 
     @torch.no_grad()
@@ -184,10 +185,24 @@ class ProductKeyMemory(nn.Module):
         if bn is not None:
             if bn.training:
                 raise NotImplementedError("smlm_hip is inference-only: put the model in eval() mode")
-            # BatchNorm in fp32 with the running statistics, whatever the parameter dtype
-            q = F.batch_norm(q.float(), bn.running_mean.float(), bn.running_var.float(), bn.weight.float(),
-                             bn.bias.float(), False, 0.0, bn.eps)
+            # BatchNorm with the running statistics, in fp32 whatever the parameter dtype: q * scale + shift
+            scale, shift = self._bn_affine()
+            q = torch.addcmul(shift, q, scale)
         return q
+
+    def _bn_affine(self):
+        """fp32 (scale, shift) of the eval-mode BatchNorm, cached until its parameters or statistics change."""
+        bn = self.query_norm
+        parts = (bn.running_mean, bn.running_var, bn.weight, bn.bias)
+        tag = tuple((t.data_ptr(), t._version) if t is not None else None for t in parts)
+        if self._bn_cache is None or self._bn_cache[0] != tag:
+            inv = torch.rsqrt(bn.running_var.float() + bn.eps)
+            scale = inv * bn.weight.float() if bn.weight is not None else inv
+            shift = -bn.running_mean.float() * scale
+            if bn.bias is not None:
+                shift = shift + bn.bias.float()
+            self._bn_cache = (tag, scale, shift)
+        return self._bn_cache[1], self._bn_cache[2]
 
     def _forward(self, x):
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):

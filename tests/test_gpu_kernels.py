@@ -388,3 +388,54 @@ def test_decode_attention_bad_position():
         out = K.decode_attention(qkv, cos, cos, torch.tensor(P, device=DEV), kc, vc)
         assert torch.isnan(out.float()).all()
     assert not kc.any() and not vc.any()
+
+
+# ------------------------------------------------------------------------------------------------ decode-step helpers
+@pytest.mark.parametrize("M,hidden", [(64, 1024), (1, 1024), (7, 24), (300, 256)])
+def test_swiglu_matches_reference_ops(M, hidden):
+    """smlm/model.py:110-118 on bf16: F.silu(a) * b, each op rounded to bf16 -- within one bf16 ulp (the exp
+    implementations may differ in the last fp32 bit)."""
+    g = torch.Generator().manual_seed(M + hidden)
+    h = (torch.randn(M, 2 * hidden, generator=g) * 3).to(torch.bfloat16)
+    got = K.swiglu(h.to(DEV)).cpu().float()
+    a, b = h.chunk(2, -1)
+    ref = (torch.nn.functional.silu(a.double()).to(torch.bfloat16).double() * b.double()).to(torch.bfloat16).float()
+    torch.testing.assert_close(got, ref, rtol=2 ** -7, atol=1e-30)
+
+
+def test_greedy_argmax_first_index_and_history():
+    g = torch.Generator().manual_seed(3)
+    B, V, L = 64, 32000, 20
+    logits = torch.randn(B, V, generator=g).to(torch.bfloat16)
+    logits[1] = 0.0                                      # all tied -> index 0
+    logits[2, 17] = logits[2, 900] = 50.0                # tied maximum -> the first
+    logits[3, -1] = 60.0
+    hist = torch.full((B, L), -1, dtype=torch.int64, device=DEV)
+    tok = torch.empty(B, dtype=torch.int64, device=DEV)
+    pos = torch.tensor(4, device=DEV)
+    K.greedy_argmax(logits.to(DEV), pos, tok, hist)
+    ref = logits.float().argmax(-1)
+    assert torch.equal(tok.cpu(), ref) and ref[1] == 0 and ref[2] == 17 and ref[3] == V - 1
+    assert torch.equal(hist[:, 5].cpu(), ref) and bool((hist[:, :5] == -1).all()) and bool((hist[:, 6:] == -1).all())
+    K.greedy_argmax(logits.to(DEV), torch.tensor(L - 1, device=DEV), tok, hist)   # slot L: outside, no write
+    assert bool((hist[:, 6:] == -1).all())
+
+
+@pytest.mark.parametrize("M,C", [(64, 384), (1, 384), (5, 100), (4096, 384)])
+def test_add_rmsnorm_matches_reference_ops(M, C):
+    """x + delta rounded to bf16 (the residual stream), then RMSNorm with fp32 statistics and bf16 weight."""
+    g = torch.Generator().manual_seed(M + C)
+    x = torch.randn(M, C, generator=g).to(torch.bfloat16)
+    d = torch.randn(M, C, generator=g).to(torch.bfloat16)
+    norm = torch.nn.RMSNorm(C, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(C, generator=g) + 0.5)
+    norm = norm.to(DEV, torch.bfloat16)
+    xo, h = K.add_rmsnorm(x.to(DEV), d.to(DEV), norm)
+    xs = (x.double() + d.double()).to(torch.bfloat16)
+    assert torch.equal(xo.cpu(), xs)
+    ref = (torch.nn.functional.rms_norm(xs.double(), (C,), eps=1e-5) * norm.weight.cpu().double()).float()
+    torch.testing.assert_close(h.cpu().float(), ref, rtol=2 ** -7, atol=1e-6)
+    x0, h0 = K.add_rmsnorm(x.to(DEV), None, norm)
+    ref0 = (torch.nn.functional.rms_norm(x.double(), (C,), eps=1e-5) * norm.weight.cpu().double()).float()
+    torch.testing.assert_close(h0.cpu().float(), ref0, rtol=2 ** -7, atol=1e-6)
