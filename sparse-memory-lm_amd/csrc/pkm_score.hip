@@ -105,21 +105,19 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
     }
 }
 
-// bf16, many tokens: 128 sub-keys x 128 tokens per workgroup (2 x 2 wavefronts of 64 x 64), the contraction in
-// chunks of 64 dims staged through LDS.  LDS rows are padded to 72 bf16 (144 B) so the 16 rows a fragment read
-// touches fall on disjoint banks; three resident workgroups per CU overlap one's loads with another's MFMAs.
-constexpr int kLdsKC = 64;            // dims per LDS chunk
-constexpr int kLdsRS = kLdsKC + 8;    // LDS row stride (bf16 elements)
+// bf16, many tokens: 128 sub-keys x 128 tokens per workgroup (2 x 2 wavefronts of 64 x 64).  The contraction
+// runs in chunks of 32 dims through two LDS stages: while the MFMAs consume one stage, the next chunk is already
+// in flight from memory into registers (two 16-byte pieces of each operand per thread) and is written to the
+// other stage afterwards, so one barrier per chunk separates them.  LDS rows are padded to 40 bf16 (80 B) so the
+// 16 rows a fragment read touches fall on distinct banks.
 
 template <int WM, int WN>
 __global__ void __launch_bounds__(256)
     score_lds_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
                      int H, int NK, int half, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
   constexpr int BM = 2 * 16 * WM, BN = 2 * 16 * WN;
-  constexpr int PPR = kLdsKC / 8;                      // 16-byte pieces per tile row and chunk
-  constexpr int PA = BM * PPR / 256, PB = BN * PPR / 256;
-  __shared__ __align__(16) uint16_t sAB[(BM + BN) * kLdsRS];
-  uint16_t *sA = sAB, *sB = sAB + BM * kLdsRS;
+  constexpr int KC = 32, RS = KC + 8, PR = KC / 8;   // dims per chunk, LDS row stride, 16-byte pieces per row
+  __shared__ __align__(16) uint16_t sAB[2 * (BM + BN) * RS];
   // 1-D grid, XCD-aware: workgroup b runs on XCD b % 8, so tile t = (b % 8) * per_xcd + b / 8 gives each XCD a
   // contiguous run of tiles; tiles are ordered sub-key tile fastest, so an XCD's L2 reads each token tile's
   // queries once and reuses them for all sub-key tiles of that (head, half).
@@ -143,43 +141,54 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < half; k0 += kLdsKC) {
-    __syncthreads();  // the previous chunk's fragment reads are done
-    // stage chunk k0 of both tiles (zero outside the table, the tokens or the half)
-#pragma unroll
-    for (int i = 0; i < PA; ++i) {
-      const int piece = tid + 256 * i, row = piece / PPR, kk = k0 + (piece % PPR) * 8;
-      const int key = key0 + row;
-      const uint4 v = (key < NK && kk < half) ? *(const uint4 *)(kbase + (int64_t)key * half + kk) : zero;
-      *(uint4 *)&sA[row * kLdsRS + (piece % PPR) * 8] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < PB; ++i) {
-      const int piece = tid + 256 * i, row = piece / PPR, kk = k0 + (piece % PPR) * 8;
-      const int tok = tok0 + row;
-      const uint4 v = (tok < N && kk < half) ? *(const uint4 *)(qbase + (int64_t)tok * q_stride + kk) : zero;
-      *(uint4 *)&sB[row * kLdsRS + (piece % PPR) * 8] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < kLdsKC; ks += 32) {
-      bf16x8 a[WM], b[WN];
-#pragma unroll
-      for (int i = 0; i < WM; ++i) a[i] = *(const bf16x8 *)&sA[(wm * 16 * WM + i * 16 + r) * kLdsRS + ks + g * 8];
-#pragma unroll
-      for (int j = 0; j < WN; ++j) b[j] = *(const bf16x8 *)&sB[(wn * 16 * WN + j * 16 + r) * kLdsRS + ks + g * 8];
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+  static_assert(BM * PR == 512 && BN * PR == 512, "two pieces per thread per operand");
+  // thread -> (row, piece) for its two A and two B pieces
+  const int pr0 = tid / PR, pc0 = (tid % PR) * 8, pr1 = pr0 + 64;
+  uint4 a0, a1, b0, b1;
+#define SMLM_FETCH(k0)                                                                                      \
+  {                                                                                                         \
+    const int kk = (k0) + pc0;                                                                              \
+    const bool kin = kk < half;                                                                             \
+    a0 = (kin && key0 + pr0 < NK) ? *(const uint4 *)(kbase + (int64_t)(key0 + pr0) * half + kk) : zero;    \
+    a1 = (kin && key0 + pr1 < NK) ? *(const uint4 *)(kbase + (int64_t)(key0 + pr1) * half + kk) : zero;    \
+    b0 = (kin && tok0 + pr0 < N) ? *(const uint4 *)(qbase + (int64_t)(tok0 + pr0) * q_stride + kk) : zero; \
+    b1 = (kin && tok0 + pr1 < N) ? *(const uint4 *)(qbase + (int64_t)(tok0 + pr1) * q_stride + kk) : zero; \
   }
+#define SMLM_STAGE(s)                                                                                       \
+  {                                                                                                         \
+    uint16_t *sa = sAB + (s) * (BM + BN) * RS, *sb = sa + BM * RS;                                          \
+    *(uint4 *)&sa[pr0 * RS + pc0] = a0;                                                                     \
+    *(uint4 *)&sa[pr1 * RS + pc0] = a1;                                                                     \
+    *(uint4 *)&sb[pr0 * RS + pc0] = b0;                                                                     \
+    *(uint4 *)&sb[pr1 * RS + pc0] = b1;                                                                     \
+  }
+  SMLM_FETCH(0)
+  SMLM_STAGE(0)
+  const int nck = (half + KC - 1) / KC;
+  for (int c = 0; c < nck; ++c) {
+    if (c + 1 < nck) SMLM_FETCH((c + 1) * KC)
+    __syncthreads();
+    const uint16_t *sa = sAB + (c & 1) * (BM + BN) * RS, *sb = sa + BM * RS;
+    bf16x8 fa[WM], fb[WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) fa[i] = *(const bf16x8 *)&sa[(wm * 16 * WM + i * 16 + r) * RS + g * 8];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) fb[j] = *(const bf16x8 *)&sb[(wn * 16 * WN + j * 16 + r) * RS + g * 8];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    if (c + 1 < nck) SMLM_STAGE((c + 1) & 1)
+  }
+#undef SMLM_FETCH
+#undef SMLM_STAGE
 
   // Epilogue through LDS: the bf16 tile is written as [token][sub-key] rows (padded to kOutRS), then stored with
   // 16-byte loads per lane covering whole 256-byte token rows of the output.
   constexpr int kOutRS = BM + 8;
-  static_assert(BN * kOutRS <= (BM + BN) * kLdsRS, "output tile must fit in the operand LDS");
-  uint16_t *sOut = sA;  // sA and sB are contiguous in LDS; the tile spans both
+
+  static_assert(BN * kOutRS <= 2 * (BM + BN) * RS, "output tile must fit in the operand LDS");
+  uint16_t *sOut = sAB;
   __syncthreads();      // all fragment reads of the last chunk are done
 #pragma unroll
   for (int i = 0; i < WM; ++i)
