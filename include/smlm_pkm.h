@@ -72,6 +72,20 @@ int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_t N, int H,
                     int64_t *idx, float *w, void *stream);
 
 /*
+ * Selection fused with the value bag, for decode-sized batches: the work of smlm_pkm_select followed by
+ * smlm_pkm_bag on its (idx, w) viewed as (N, H*knn), in one launch (one workgroup per token), with identical results.
+ * Replaces pk_select + bag_infer of smlm/pkm.py:197-223 (kernels.py:214-226, 364-378).
+ *   s1, s2 (N, H, NK) of dtype; table / table_dtype / rows / D / scales / pre / out / out_dtype as smlm_pkm_bag;
+ *   scores, idx, w: optional (NULL = not written) copies of the selection, as smlm_pkm_select writes them.
+ * H <= 4; a table row must be whole 16-byte chunks, c of them, and the bag's row-slot layout for c
+ * (lcm(c, 64) threads, at least 128; c * floor(256 / c) if lcm(c, 64) > 256) must fit in the 2*H*64 threads.
+ */
+int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, int64_t N, int H, int NK, int knn,
+                        const void *table, int table_dtype, int64_t rows, int D, const uint16_t *scales,
+                        const uint16_t *pre, void *out, int out_dtype, void *scores, int64_t *idx, float *w,
+                        void *stream);
+
+/*
  * Weighted value bag.  Replaces bag_forward (smlm/kernels.py:229-237) and bag_infer (smlm/kernels.py:364-378):
  *   out[n, :] = sum_{j<K} w[n, j] * row(idx[n, j])        (fp32 accumulation)
  * with row() = table row for SMLM_F32 / SMLM_BF16 tables and scale[r] * code[r, :] for SMLM_I8 / SMLM_Q4 tables
@@ -143,6 +157,82 @@ int smlm_greedy_argmax(const void *logits, int64_t row_stride, int64_t B, int V,
  */
 int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float eps, int64_t M, int C, void *x_out,
                      void *h_out, void *stream);
+
+/*
+ * Fused linear layer of the single-token decode step (M = decode batch rows):  y = h W^T on the matrix cores with
+ * the op in front of it and the op after it in one launch.  Replaces, per decode step, the nn.Linear calls of
+ * smlm/model.py:90-118 and 266-293 (wqkv, wo, w13, w2, lm_head) and smlm/pkm.py:188-191, 213-224 (query_proj,
+ * swilu_proj, value_proj), together with their neighbours:
+ *   prologue SMLM_LIN_PLAIN          h = x
+ *            SMLM_LIN_RMSNORM        xs = bf16(x + delta) (delta may be NULL), h = bf16(xs * rsqrt(mean(xs^2) + eps) * g)
+ *                                    (the residual add, smlm/model.py:156-163, and the next sublayer's RMSNorm)
+ *            SMLM_LIN_EMBED_RMSNORM  xs = emb[tok[m]] (smlm/model.py:268), then as SMLM_LIN_RMSNORM
+ *            with an RMSNorm prologue, xs is also written to x_out (if not NULL): the residual stream
+ *   epilogue SMLM_LIN_STORE          v = bf16(acc + bias); on columns < n_affine v = bf16(v * scale + shift) (eval
+ *                                    BatchNorm of the memory query); columns < n_split to out, the rest to out2
+ *            SMLM_LIN_SWIGLU         out[:, j] = bf16(bf16(silu(a_j)) * b_j), a_j = bf16(acc_j), b_j = bf16(acc_{N/2+j})
+ *                                    (w13 followed by the SwiGLU activation, smlm/model.py:110-118)
+ *            SMLM_LIN_ARGMAX         no logits are written: partial[m, b] = the largest (order16(bf16 logit) << 32 |
+ *                                    ~column) over column block b of smlm_linear_argmax_blocks(N) blocks of 64;
+ *                                    smlm_argmax_finish turns them into tokens (lm_head + greedy argmax)
+ * Shapes: W (N, K) bf16 row-major (nn.Linear.weight), K a multiple of 32, N a multiple of 16 (SWIGLU: 32);
+ * RMSNorm prologues need K <= 480; x rows at x + m*x_stride; delta, x_out (M, K) dense; bias (N,) bf16;
+ * scale/shift (n_affine,) fp32; out/out2 bf16 with row strides in elements.  All inputs 16-byte aligned, outputs
+ * 8-byte aligned.  Deterministic (no atomics); the library allocates nothing.
+ */
+typedef enum smlm_linear_prologue {
+  SMLM_LIN_PLAIN = 0,
+  SMLM_LIN_RMSNORM = 1,
+  SMLM_LIN_EMBED_RMSNORM = 2
+} smlm_linear_prologue;
+
+typedef enum smlm_linear_epilogue {
+  SMLM_LIN_STORE = 0,
+  SMLM_LIN_SWIGLU = 1,
+  SMLM_LIN_ARGMAX = 2
+} smlm_linear_epilogue;
+
+typedef struct smlm_linear_args {
+  int prologue;             /* smlm_linear_prologue */
+  int epilogue;             /* smlm_linear_epilogue */
+  int64_t M;                /* rows (tokens) */
+  int N;                    /* weight rows (output features; SWIGLU: 2 * hidden) */
+  int K;                    /* input features */
+  const void *x;            /* (M, K) bf16 rows at x + m*x_stride (PLAIN, RMSNORM) */
+  int64_t x_stride;
+  const void *delta;        /* (M, K) bf16 or NULL (RMSNORM) */
+  const int64_t *tok;       /* (M,) token ids (EMBED_RMSNORM) */
+  const void *emb;          /* (emb_rows, K) bf16 (EMBED_RMSNORM) */
+  int64_t emb_rows;
+  const void *norm_w;       /* (K,) bf16 RMSNorm weight */
+  float eps;
+  void *x_out;              /* (M, K) bf16 or NULL: the prologue's xs */
+  const void *w;            /* (N, K) bf16 */
+  const void *bias;         /* (N,) bf16 or NULL (STORE) */
+  const float *scale;       /* (n_affine,) fp32 (STORE) */
+  const float *shift;       /* (n_affine,) fp32 (STORE) */
+  int n_affine;
+  int n_split;              /* STORE: columns [0, n_split) -> out, [n_split, N) -> out2 */
+  void *out;                /* STORE: (M, n_split); SWIGLU: (M, N/2) */
+  int64_t out_stride;
+  void *out2;               /* STORE: (M, N - n_split) */
+  int64_t out2_stride;
+  uint64_t *partial;        /* ARGMAX: (M, >= smlm_linear_argmax_blocks(N)) */
+  int64_t partial_stride;
+} smlm_linear_args;
+
+/* Number of 64-column blocks of the ARGMAX epilogue for N columns (the width partial needs). */
+int smlm_linear_argmax_blocks(int N);
+
+int smlm_decode_linear(const smlm_linear_args *args, void *stream);
+
+/*
+ * End of a greedy decode step (smlm/train.py:297-301: nxt = logits.argmax(-1), appended to the sequence), in one
+ * workgroup: tok[m] = the column of the largest of partial[m, 0..nblk); if hist is given, hist[m, *pos + 1] = tok[m]
+ * (skipped outside [0, hist_len)); then, if advance, *pos += 1 (after every row has read the old value).
+ */
+int smlm_argmax_finish(const uint64_t *partial, int64_t partial_stride, int nblk, int64_t M, int64_t *pos,
+                       int64_t *tok, int64_t *hist, int64_t hist_stride, int64_t hist_len, int advance, void *stream);
 
 #ifdef __cplusplus
 }

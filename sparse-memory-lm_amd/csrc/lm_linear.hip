@@ -1,0 +1,514 @@
+// Small-M fused linear layers of the single-token decode step: y = h W^T for M token rows (the decode batch) and
+// an (N, K) nn.Linear weight W, on the matrix cores (v_mfma_f32_16x16x32_bf16, fp32 accumulation), with the op in
+// front of it and the op after it in the same launch (smlm/model.py:110-163, 266-293; smlm/pkm.py:188-191, 213-224):
+//
+//   prologue  PLAIN          h = x
+//             RMSNORM        xs = bf16(x + delta) (delta optional), h = bf16(xs * rsqrt(mean(xs^2) + eps) * g):
+//                            the residual add and the RMSNorm of the next sublayer
+//             EMBED_RMSNORM  xs = emb[tok[m]] (the token embedding), then as RMSNORM
+//                            xs is written once to x_out (the residual stream), by the column block 0.
+//   epilogue  STORE          v = bf16(acc + bias); on the first n_affine columns v = bf16(v * scale + shift) (the
+//                            eval BatchNorm of the memory query); columns [0, n_split) go to out, [n_split, N) to
+//                            out2 (query_proj and swilu_proj of a memory layer are one launch)
+//             SWIGLU         out[:, j] = bf16(bf16(silu(a_j)) * b_j) with a_j = bf16(acc_j), b_j = bf16(acc_{H+j}),
+//                            H = N / 2 (w13 + the SwiGLU activation)
+//             ARGMAX         per token, the largest key (bf16 logit, then lowest column) over the block's 128
+//                            columns, to partial[m, block] (lm_head + greedy argmax; no logits are written)
+//
+// Workgroup = 4 wavefronts, 64 tokens (blockIdx.y) x one column block (blockIdx.x).  STORE / SWIGLU: one 16-column
+// tile per workgroup (SWIGLU: the 16 a columns and their 16 b columns), the 4 wavefronts split the contraction and
+// their partial sums are added in a fixed order through LDS.  ARGMAX: each wavefront owns 2 tiles (32 columns) over
+// the whole contraction.  Every result is deterministic.
+//
+// Latency is what matters at decode sizes, so every global load a lane needs is issued before the first one is
+// used: the weight fragments of the lane's K slice first (they do not depend on the prologue), then the prologue's
+// input rows (addresses clamped into range, no per-row branches), then the arithmetic.  The prologue works on rows
+// of 16 lanes (DPP reductions inside a row) and writes the normalised bf16 rows to LDS ([tokens][K + 8]), from which
+// the B fragments are read; a PLAIN input is read into registers directly.
+//
+// MFMA operand mapping (16x16x32, r = lane % 16, g = lane / 16): A = 16 weight rows x 32 k (lane: row r, k group g),
+// B = 32 k x 16 tokens (lane: token r, k group g), D: lane holds columns 4g..4g+3 of token r.
+#include "pkm_common.h"
+
+namespace smlm {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLinThreads = 256;
+constexpr int kLinWaves = kLinThreads / kWave;
+constexpr int kTokBlock = 64;     // tokens per workgroup (4 MFMA tiles)
+constexpr int kRowLanes = 16;     // lanes per prologue row
+constexpr int kMaxPasses = kTokBlock / (kLinWaves * (kWave / kRowLanes));  // 4 prologue passes of 16 rows
+constexpr int kArgTiles = 2;      // 16-column tiles per wavefront with the ARGMAX epilogue
+constexpr int kArgCols = kLinWaves * kArgTiles * 16;   // 128 columns per workgroup
+constexpr uint16_t kBf16NaN = 0x7FC0;
+
+__device__ __forceinline__ float silu_bf16(float a) { return round_bf16(a / (1.0f + expf(-a))); }
+
+__device__ __forceinline__ void unpack8(const uint4 v, float *f) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(u[e] << 16);
+    f[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 pack8(const float *f) {
+  uint32_t u[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] = bf16_bits_rtne(f[2 * e]) | (bf16_bits_rtne(f[2 * e + 1]) << 16);
+  return uint4{u[0], u[1], u[2], u[3]};
+}
+
+// Sum over the 16 lanes of a DPP row (xor 1, xor 2 within quads, then half-row and row mirrors); every lane of the
+// row ends with the row's total.  All 64 lanes must be active.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// Prologue: the workgroup's rows [0, nrows) normalised into sH (bf16, row stride KP), rows [nrows, pad_rows) zero.
+// Row rr = pass * 16 + wave * 4 + quarter is handled by the 16 lanes of one quarter wavefront; lane `sub` of it owns
+// the 16-byte chunks sub, sub + 16, ... (CPQ of them, K <= 128 * CPQ).
+template <int PRO, int CPQ>
+__device__ __forceinline__ void build_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
+                                                  uint16_t *sH, int KP) {
+  const int K = a.K, CH = K / 8;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int quarter = lane >> 4, sub = lane & 15;
+  const int passes = pad_rows / 16;
+  const bool write_x = a.x_out != nullptr && blockIdx.x == 0;
+  const uint16_t *nw = (const uint16_t *)a.norm_w;
+
+  uint4 xv[kMaxPasses][CPQ], dv[kMaxPasses][CPQ], gv[CPQ];
+  bool bad[kMaxPasses];
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) gv[j] = *(const uint4 *)(nw + min(sub + 16 * j, CH - 1) * 8);
+#pragma unroll
+  for (int p = 0; p < kMaxPasses; ++p) {
+    bad[p] = false;
+    if (p >= passes) continue;                      // wavefront-uniform
+    const int rr = p * 16 + wave * 4 + quarter;
+    const int64_t m = m0 + min(rr, nrows - 1);      // rows past the end re-read the last row (written as zero)
+    const uint16_t *src;
+    if constexpr (PRO == SMLM_LIN_EMBED_RMSNORM) {
+      const int64_t t = a.tok[m];
+      bad[p] = t < 0 || t >= a.emb_rows;
+      src = (const uint16_t *)a.emb + (bad[p] ? 0 : t) * (int64_t)K;
+    } else {
+      src = (const uint16_t *)a.x + m * a.x_stride;
+    }
+#pragma unroll
+    for (int j = 0; j < CPQ; ++j) xv[p][j] = *(const uint4 *)(src + min(sub + 16 * j, CH - 1) * 8);
+    if constexpr (PRO == SMLM_LIN_RMSNORM) {
+      if (a.delta) {
+        const uint16_t *dsrc = (const uint16_t *)a.delta + m * (int64_t)K;
+#pragma unroll
+        for (int j = 0; j < CPQ; ++j) dv[p][j] = *(const uint4 *)(dsrc + min(sub + 16 * j, CH - 1) * 8);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int p = 0; p < kMaxPasses; ++p) {
+    if (p >= passes) continue;
+    const int rr = p * 16 + wave * 4 + quarter;
+    const bool live = rr < nrows;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPQ; ++j) {
+      float xf[8];
+      unpack8(xv[p][j], xf);
+      if constexpr (PRO == SMLM_LIN_RMSNORM) {
+        if (a.delta) {
+          float df[8];
+          unpack8(dv[p][j], df);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xf[e] += df[e];
+          xv[p][j] = pack8(xf);                     // the residual stream is bf16: round the sum
+          unpack8(xv[p][j], xf);
+        }
+      }
+      if (bad[p]) {                                 // token id outside the embedding: a NaN row
+        const uint32_t nn = (uint32_t)kBf16NaN | ((uint32_t)kBf16NaN << 16);
+        xv[p][j] = uint4{nn, nn, nn, nn};
+        unpack8(xv[p][j], xf);
+      }
+      if (sub + 16 * j < CH) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(xf[e], xf[e], ss);
+      }
+    }
+    ss = row16_sum(ss);
+    const float rstd = rsqrtf(ss / (float)K + a.eps);
+    uint16_t *dst = sH + rr * KP;
+#pragma unroll
+    for (int j = 0; j < CPQ; ++j) {
+      const int c = sub + 16 * j;
+      if (c >= CH) continue;
+      if (!live) {
+        *(uint4 *)(dst + c * 8) = uint4{0u, 0u, 0u, 0u};
+        continue;
+      }
+      if (write_x) *(uint4 *)((uint16_t *)a.x_out + (m0 + rr) * (int64_t)K + c * 8) = xv[p][j];
+      float xf[8], gf[8];
+      unpack8(xv[p][j], xf);
+      unpack8(gv[j], gf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[e] = xf[e] * rstd * gf[e];
+      *(uint4 *)(dst + c * 8) = pack8(xf);
+    }
+  }
+}
+
+// PRO / EPI: prologue and epilogue; MAXS: k-steps of 32 per wavefront held in registers (>= its K slice);
+// CPQ: prologue chunks per lane.
+template <int PRO, int EPI, int MAXS, int CPQ>
+__global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_args a) {
+  constexpr bool ARG = EPI == SMLM_LIN_ARGMAX;
+  constexpr int KS = ARG ? 1 : kLinWaves;               // wavefronts along the contraction
+  constexpr int NT = EPI == SMLM_LIN_STORE ? 1 : 2;     // weight tiles per wavefront
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int K = a.K, KP = K + 8;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * kTokBlock;
+  const int nrows = (int)min((int64_t)kTokBlock, a.M - m0);
+  const int MT = (nrows + 15) / 16;
+  uint16_t *sH = (uint16_t *)smem;
+
+  // this wavefront's K slice [s_lo, s_lo + ns) in steps of 32, and its weight rows
+  const int ks = ARG ? 0 : wave;
+  const int nsteps = K / 32;
+  const int s_lo = ks * nsteps / KS, ns = (ks + 1) * nsteps / KS - s_lo;
+  const int cols = EPI == SMLM_LIN_SWIGLU ? a.N / 2 : a.N;                   // output columns
+  const int col0 = ARG ? blockIdx.x * kArgCols + wave * kArgTiles * 16 : blockIdx.x * 16;
+  const uint16_t *W = (const uint16_t *)a.w;
+
+  // 1. weight fragments (rows past N and steps past the slice re-read valid memory; their products are unused)
+  uint4 areg[NT][MAXS];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int wrow = EPI == SMLM_LIN_SWIGLU ? (t == 0 ? col0 : cols + col0) + r : col0 + t * 16 + r;
+    wrow = min(wrow, a.N - 1);
+    const uint16_t *wp = W + (int64_t)wrow * K + g * 8;
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      const int step = min(s_lo + min(s, ns - 1), nsteps - 1);
+      areg[t][s] = *(const uint4 *)(wp + max(step, 0) * 32);
+    }
+  }
+
+  // 2. activations: PLAIN rows straight into registers; otherwise the prologue into LDS
+  uint4 breg[4][PRO == SMLM_LIN_PLAIN ? MAXS : 1];
+  if constexpr (PRO == SMLM_LIN_PLAIN) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt >= MT) continue;                       // wavefront-uniform
+      const int tok = min(mt * 16 + r, nrows - 1);
+      const uint16_t *xp = (const uint16_t *)a.x + (m0 + tok) * a.x_stride + g * 8;
+#pragma unroll
+      for (int s = 0; s < MAXS; ++s) {
+        const int step = min(s_lo + min(s, ns - 1), nsteps - 1);
+        breg[mt][s] = *(const uint4 *)(xp + max(step, 0) * 32);
+      }
+    }
+  } else {
+    build_activations<PRO, CPQ>(a, m0, nrows, MT * 16, sH, KP);
+    __syncthreads();
+  }
+
+  // 3. products
+  floatx4 acc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[t][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    if (s >= ns) continue;                          // wavefront-uniform
+    const int k = (s_lo + s) * 32 + g * 8;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt >= MT) continue;
+      uint4 b;
+      if constexpr (PRO == SMLM_LIN_PLAIN) b = breg[mt][s];
+      else b = *(const uint4 *)(sH + (mt * 16 + r) * KP + k);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, areg[t][s]),
+                                                             __builtin_bit_cast(bf16x8, b), acc[t][mt], 0, 0, 0);
+    }
+  }
+
+  if constexpr (KS > 1) {
+    // partial sums of wavefronts 1..3 into LDS (over the activations, which every wavefront has finished reading
+    // after the barrier), added by wavefront 0 in order
+    floatx4 *sRed = (floatx4 *)smem;
+    if constexpr (PRO != SMLM_LIN_PLAIN) __syncthreads();
+    if (ks > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          if (mt < MT) sRed[(((ks - 1) * NT + t) * 4 + mt) * kWave + lane] = acc[t][mt];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int k2 = 1; k2 < KS; ++k2)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          if (mt < MT) acc[t][mt] += sRed[(((k2 - 1) * NT + t) * 4 + mt) * kWave + lane];
+  }
+
+  const int c = col0 + 4 * g;  // this lane's 4 columns c .. c+3 of tile 0 (cols % 16 == 0: all in or all out)
+  if constexpr (EPI == SMLM_LIN_STORE) {
+    if (c >= cols) return;
+    float bias[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f}, sh[4] = {0.f, 0.f, 0.f, 0.f};
+    const bool affine = c < a.n_affine;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (a.bias) bias[e] = bf16_bits_to_f32(((const uint16_t *)a.bias)[c + e]);
+      if (affine) {
+        sc[e] = a.scale[c + e];
+        sh[e] = a.shift[c + e];
+      }
+    }
+    const bool first = c < a.n_split;
+    uint16_t *dst = first ? (uint16_t *)a.out + c : (uint16_t *)a.out2 + (c - a.n_split);
+    const int64_t stride = first ? a.out_stride : a.out2_stride;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int tok = mt * 16 + r;
+      if (mt >= MT || tok >= nrows) continue;
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = round_bf16(acc[0][mt][e] + bias[e]);
+        if (affine) v = round_bf16(fmaf(v, sc[e], sh[e]));
+        o[e] = bf16_bits_rtne(v);
+      }
+      *(uint2 *)(dst + (m0 + tok) * stride) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    }
+  } else if constexpr (EPI == SMLM_LIN_SWIGLU) {
+    if (c >= cols) return;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int tok = mt * 16 + r;
+      if (mt >= MT || tok >= nrows) continue;
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = bf16_bits_rtne(silu_bf16(round_bf16(acc[0][mt][e])) * round_bf16(acc[1][mt][e]));
+      *(uint2 *)((uint16_t *)a.out + (m0 + tok) * a.out_stride + c) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    }
+  } else {  // ARGMAX
+    uint64_t *sArg = (uint64_t *)smem;  // [4 wavefronts][64 tokens]
+    if constexpr (PRO != SMLM_LIN_PLAIN) __syncthreads();  // activations no longer read
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt >= MT) continue;
+      uint64_t best = 0;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int col = c + t * 16 + e;
+          if (col >= cols) continue;
+          const uint64_t key = ((uint64_t)order16(bf16_bits_rtne(acc[t][mt][e])) << 32) |
+                               (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
+          best = key > best ? key : best;
+        }
+#pragma unroll
+      for (int o = 16; o < kWave; o <<= 1) {
+        const uint64_t other = __shfl_xor(best, o, kWave);
+        best = other > best ? other : best;
+      }
+      if (g == 0) sArg[wave * kTokBlock + mt * 16 + r] = best;
+    }
+    __syncthreads();
+    if (tid < nrows) {
+      uint64_t best = sArg[tid];
+#pragma unroll
+      for (int w2 = 1; w2 < kLinWaves; ++w2) best = sArg[w2 * kTokBlock + tid] > best ? sArg[w2 * kTokBlock + tid] : best;
+      a.partial[(m0 + tid) * a.partial_stride + blockIdx.x] = best;
+    }
+  }
+}
+
+// One workgroup: per row the largest of its nblk partial keys -> token; history slot *pos + 1; then *pos += 1.
+// Wavefront w takes rows w, w + 16, ... four at a time, with every partial load of the four rows in flight.
+constexpr int kFinishThreads = 1024;
+constexpr int kFinishRows = 4;
+constexpr int kFinishLoads = 4;   // partials per lane per row and round (256 blocks per round)
+
+__global__ void __launch_bounds__(kFinishThreads)
+    argmax_finish_kernel(const uint64_t *__restrict__ partial, int64_t pstride, int nblk, int64_t M,
+                         int64_t *__restrict__ pos, int64_t *__restrict__ tok, int64_t *__restrict__ hist,
+                         int64_t hstride, int64_t hlen, int advance) {
+  constexpr int kWaves = kFinishThreads / kWave;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int64_t P = *pos;
+  for (int64_t m0 = (int64_t)wave * kFinishRows; m0 < M; m0 += (int64_t)kWaves * kFinishRows) {
+    uint64_t best[kFinishRows];
+#pragma unroll
+    for (int i = 0; i < kFinishRows; ++i) best[i] = 0;
+    for (int b0 = 0; b0 < nblk; b0 += kWave * kFinishLoads) {
+      uint64_t v[kFinishRows][kFinishLoads];
+#pragma unroll
+      for (int i = 0; i < kFinishRows; ++i)
+#pragma unroll
+        for (int u = 0; u < kFinishLoads; ++u) {
+          const int b = b0 + u * kWave + lane;
+          const int64_t m = m0 + i < M ? m0 + i : M - 1;
+          v[i][u] = partial[m * pstride + (b < nblk ? b : nblk - 1)];
+        }
+#pragma unroll
+      for (int i = 0; i < kFinishRows; ++i)
+#pragma unroll
+        for (int u = 0; u < kFinishLoads; ++u) best[i] = v[i][u] > best[i] ? v[i][u] : best[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kFinishRows; ++i) {
+      for (int o = kWave / 2; o > 0; o >>= 1) {
+        const uint64_t other = __shfl_xor(best[i], o, kWave);
+        best[i] = other > best[i] ? other : best[i];
+      }
+      const int64_t m = m0 + i;
+      if (lane == 0 && m < M) {
+        const int64_t t = (int64_t)(0xFFFFFFFFu - (uint32_t)best[i]);
+        tok[m] = t;
+        if (hist && P + 1 >= 0 && P + 1 < hlen) hist[m * hstride + P + 1] = t;
+      }
+    }
+  }
+  __syncthreads();  // every wavefront has read *pos
+  if (advance && threadIdx.x == 0) *pos = P + 1;
+}
+
+template <int PRO, int EPI, int MAXS>
+void launch_linear_cpq(const smlm_linear_args &a, dim3 grid, size_t shmem, hipStream_t stream) {
+  if (PRO == SMLM_LIN_PLAIN || a.K <= 384)
+    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 3>), grid, dim3(kLinThreads), shmem, stream, a);
+  else
+    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 4>), grid, dim3(kLinThreads), shmem, stream, a);
+}
+
+template <int PRO>
+void launch_linear_pro(const smlm_linear_args &a, dim3 grid, size_t shmem, hipStream_t stream) {
+  const int steps = a.K / 32;
+  if (a.epilogue == SMLM_LIN_ARGMAX) {
+    if (steps <= 12) launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 12>(a, grid, shmem, stream);
+    else launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 16>(a, grid, shmem, stream);
+    return;
+  }
+  const int per_wave = (steps + kLinWaves - 1) / kLinWaves;
+#define SMLM_LIN_MAXS(EPI)                                                               \
+  if (per_wave <= 4) launch_linear_cpq<PRO, EPI, 4>(a, grid, shmem, stream);             \
+  else if (PRO == SMLM_LIN_PLAIN && per_wave <= 8) launch_linear_cpq<PRO, EPI, 8>(a, grid, shmem, stream); \
+  else launch_linear_cpq<PRO, EPI, 16>(a, grid, shmem, stream);
+  if (a.epilogue == SMLM_LIN_STORE) {
+    SMLM_LIN_MAXS(SMLM_LIN_STORE)
+  } else {
+    SMLM_LIN_MAXS(SMLM_LIN_SWIGLU)
+  }
+#undef SMLM_LIN_MAXS
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p % 16) == 0; }
+
+}  // namespace
+}  // namespace smlm
+
+extern "C" int smlm_linear_argmax_blocks(int N) { return N <= 0 ? 0 : (N + smlm::kArgCols - 1) / smlm::kArgCols; }
+
+extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
+  using namespace smlm;
+  if (!a) return fail(SMLM_EINVAL, "smlm_decode_linear: null argument block");
+  const smlm_linear_args &A = *a;
+  const int pro = A.prologue, epi = A.epilogue;
+  if (pro != SMLM_LIN_PLAIN && pro != SMLM_LIN_RMSNORM && pro != SMLM_LIN_EMBED_RMSNORM)
+    return fail(SMLM_EINVAL, "smlm_decode_linear: unknown prologue %d", pro);
+  if (epi != SMLM_LIN_STORE && epi != SMLM_LIN_SWIGLU && epi != SMLM_LIN_ARGMAX)
+    return fail(SMLM_EINVAL, "smlm_decode_linear: unknown epilogue %d", epi);
+  if (!A.w) return fail(SMLM_EINVAL, "smlm_decode_linear: null weight");
+  if (A.M < 0 || A.M > 65535LL * kTokBlock || A.K < 32 || A.K % 32 || A.N < 16 || A.N % 16)
+    return fail(SMLM_EINVAL, "smlm_decode_linear: bad shape M=%lld N=%d K=%d (K and N multiples of 32 and 16)",
+                (long long)A.M, A.N, A.K);
+  if (epi == SMLM_LIN_SWIGLU && A.N % 32)
+    return fail(SMLM_EINVAL, "smlm_decode_linear: SWIGLU needs N = 2 * hidden with hidden a multiple of 16");
+  const int max_k = epi == SMLM_LIN_ARGMAX ? 512 : (pro == SMLM_LIN_PLAIN ? 2048 : 512);
+  if (A.K > max_k)
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_linear: K=%d too large for this prologue / epilogue (at most %d)",
+                A.K, max_k);
+  if (!aligned16(A.w)) return fail(SMLM_EINVAL, "smlm_decode_linear: weight must be 16-byte aligned");
+  if (pro == SMLM_LIN_EMBED_RMSNORM) {
+    if (!A.tok || !A.emb || A.emb_rows < 1 || !aligned16(A.emb))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: EMBED_RMSNORM needs tok, a 16-byte aligned emb, emb_rows");
+  } else {
+    if (!A.x || !aligned16(A.x) || A.x_stride < A.K || A.x_stride % 8)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: x must be 16-byte aligned with x_stride >= K, a multiple of 8");
+  }
+  if (pro != SMLM_LIN_PLAIN) {
+    if (!A.norm_w || !aligned16(A.norm_w) || !(A.eps >= 0.f))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: the RMSNorm needs a 16-byte aligned weight and eps >= 0");
+    if (A.K > 480)
+      return fail(SMLM_EUNSUPPORTED, "smlm_decode_linear: normalised rows of K=%d > 480 do not fit in LDS", A.K);
+    if ((A.delta && (pro != SMLM_LIN_RMSNORM || !aligned16(A.delta))) || (A.x_out && !aligned16(A.x_out)))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: delta (RMSNORM only) and x_out must be 16-byte aligned");
+  } else if (A.delta || A.x_out) {
+    return fail(SMLM_EINVAL, "smlm_decode_linear: delta and x_out belong to the RMSNorm prologues");
+  }
+  const int cols = epi == SMLM_LIN_SWIGLU ? A.N / 2 : A.N;
+  if (epi == SMLM_LIN_STORE) {
+    if (A.n_split < 0 || A.n_split > A.N || A.n_split % 16 || A.n_affine < 0 || A.n_affine > A.N || A.n_affine % 16)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: n_split and n_affine must be multiples of 16 in [0, N]");
+    if ((A.n_split > 0 && (!A.out || A.out_stride < A.n_split || A.out_stride % 4 || (uintptr_t)A.out % 8)) ||
+        (A.n_split < A.N && (!A.out2 || A.out2_stride < A.N - A.n_split || A.out2_stride % 4 || (uintptr_t)A.out2 % 8)))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: out / out2 missing, misaligned or with a short row stride");
+    if (A.n_affine > 0 && (!A.scale || !A.shift))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: n_affine > 0 needs scale and shift");
+  } else if (epi == SMLM_LIN_SWIGLU) {
+    if (!A.out || A.out_stride < cols || A.out_stride % 4 || (uintptr_t)A.out % 8)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: SWIGLU out missing, misaligned or with a short row stride");
+  } else {
+    if (!A.partial || A.partial_stride < smlm_linear_argmax_blocks(A.N) || (uintptr_t)A.partial % 8)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: ARGMAX needs partial (M, >= %d) uint64",
+                  smlm_linear_argmax_blocks(A.N));
+  }
+  if (A.M == 0) return SMLM_OK;
+  const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
+  const dim3 grid((unsigned)((cols + cols_per_block - 1) / cols_per_block), (unsigned)((A.M + kTokBlock - 1) / kTokBlock));
+  const int pad_rows = (int)(((A.M < kTokBlock ? A.M : kTokBlock) + 15) / 16 * 16);
+  const size_t act = pro != SMLM_LIN_PLAIN ? (size_t)pad_rows * (A.K + 8) * 2 : 0;
+  const size_t red = epi == SMLM_LIN_ARGMAX ? (size_t)kLinWaves * kTokBlock * 8
+                                            : (size_t)(kLinWaves - 1) * (epi == SMLM_LIN_SWIGLU ? 2 : 1) * 4 * kWave * 16;
+  const size_t shmem = act > red ? act : red;
+  hipStream_t s = (hipStream_t)stream;
+  if (pro == SMLM_LIN_PLAIN) launch_linear_pro<SMLM_LIN_PLAIN>(A, grid, shmem, s);
+  else if (pro == SMLM_LIN_RMSNORM) launch_linear_pro<SMLM_LIN_RMSNORM>(A, grid, shmem, s);
+  else launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, grid, shmem, s);
+  return launch_status("smlm_decode_linear");
+}
+
+extern "C" int smlm_argmax_finish(const uint64_t *partial, int64_t partial_stride, int nblk, int64_t M, int64_t *pos,
+                                  int64_t *tok, int64_t *hist, int64_t hist_stride, int64_t hist_len, int advance,
+                                  void *stream) {
+  using namespace smlm;
+  if (!partial || !tok || !pos) return fail(SMLM_EINVAL, "smlm_argmax_finish: null partial, tok or pos");
+  if (M < 0 || nblk < 1 || partial_stride < nblk || (hist && hist_stride < hist_len))
+    return fail(SMLM_EINVAL, "smlm_argmax_finish: bad shape M=%lld nblk=%d", (long long)M, nblk);
+  if (M == 0 && !advance) return SMLM_OK;
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3(1), dim3(kFinishThreads), 0, (hipStream_t)stream, partial,
+                     partial_stride, nblk, M, pos, tok, hist, hist_stride, hist_len, advance);
+  return launch_status("smlm_argmax_finish");
+}

@@ -10,98 +10,12 @@
 // slot and issues kUnroll independent row loads at a time; the rpr partial sums per column are added through
 // LDS at the end, followed by the epilogue.  Lookups (row offsets, weights premultiplied by the row scale) are
 // staged in LDS first, so each row load depends on one LDS read only.
-#include "pkm_common.h"
+#include "pkm_bag_dev.h"
 
 namespace smlm {
 namespace {
 
-enum TableKind { kF32 = SMLM_F32, kBF16 = SMLM_BF16, kI8 = SMLM_I8, kQ4 = SMLM_Q4 };
-
-constexpr int kStage = 256;   // lookups staged in LDS per pass
-constexpr int kUnroll = 8;    // independent 16-byte row loads in flight per thread
-
-template <int TK>
-constexpr int vals_per_chunk() {
-  return TK == kF32 ? 4 : TK == kBF16 ? 8 : TK == kI8 ? 16 : 32;
-}
-
-// output column of value e of chunk c (q4: values 0..15 are the low nibbles = columns c*16+e, values 16..31
-// the high nibbles = columns D/2 + c*16 + e)
-template <int TK>
-__device__ __forceinline__ int chunk_col(int c, int e, int D) {
-  if constexpr (TK == kQ4) return e < 16 ? c * 16 + e : (D >> 1) + c * 16 + (e - 16);
-  else return c * vals_per_chunk<TK>() + e;
-}
-
-template <int TK>
-__device__ __forceinline__ void accumulate(float *acc, const uint4 v, const float wt) {
-  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if constexpr (TK == kF32) {
-      acc[e] = fmaf(wt, __uint_as_float(u[e]), acc[e]);
-    } else if constexpr (TK == kBF16) {
-      acc[2 * e] = fmaf(wt, __uint_as_float(u[e] << 16), acc[2 * e]);
-      acc[2 * e + 1] = fmaf(wt, __uint_as_float(u[e] & 0xFFFF0000u), acc[2 * e + 1]);
-    } else if constexpr (TK == kI8) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        acc[4 * e + b] = fmaf(wt, (float)(int8_t)(u[e] >> (8 * b)), acc[4 * e + b]);
-    } else {
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int byte = (int)((u[e] >> (8 * b)) & 0xFFu);
-        acc[4 * e + b] = fmaf(wt, (float)((byte & 15) - 8), acc[4 * e + b]);
-        acc[16 + 4 * e + b] = fmaf(wt, (float)((byte >> 4) - 8), acc[16 + 4 * e + b]);
-      }
-    }
-  }
-}
-
-// value of column `col` of a row (generic kernel)
-template <int TK>
-__device__ __forceinline__ float row_value(const uint8_t *row, int col, int D) {
-  if constexpr (TK == kF32) return ((const float *)row)[col];
-  else if constexpr (TK == kBF16) return bf16_bits_to_f32(((const uint16_t *)row)[col]);
-  else if constexpr (TK == kI8) return (float)((const int8_t *)row)[col];
-  else {
-    const int half = D >> 1;
-    const int byte = row[col < half ? col : col - half];
-    return (float)((col < half ? (byte & 15) : (byte >> 4)) - 8);
-  }
-}
-
-// Stage lookups [k0, k0 + kc) of token n: byte offset of the row and weight (times the row scale).  An index
-// outside [0, rows) contributes nothing and marks the token bad.
-template <int TK, bool IDX64>
-__device__ __forceinline__ void stage_lookups(const void *__restrict__ idx, const float *__restrict__ w,
-                                              const uint16_t *__restrict__ scales, int64_t base, int kc,
-                                              int64_t rows, int64_t row_bytes, int64_t *s_off, float *s_w,
-                                              int *s_bad) {
-  for (int j = threadIdx.x; j < kc; j += blockDim.x) {
-    int64_t r = IDX64 ? ((const int64_t *)idx)[base + j] : (int64_t)((const int32_t *)idx)[base + j];
-    float wt = w[base + j];
-    if (r < 0 || r >= rows) {
-      *s_bad = 1;
-      r = 0;
-      wt = 0.f;
-    }
-    if constexpr (TK == kI8 || TK == kQ4) wt *= f16_bits_to_f32(scales[r]);
-    s_off[j] = r * row_bytes;
-    s_w[j] = wt;
-  }
-}
-
-__device__ __forceinline__ void store_out(void *out, int64_t o, float a, bool bad, const uint16_t *pre,
-                                          bool out_bf16) {
-  if (bad) a = __builtin_nanf("");
-  if (pre) {
-    const float p = bf16_bits_to_f32(pre[o]);
-    a *= round_bf16(p / (1.0f + expf(-p)));  // bf16(silu(pre)), as smlm/kernels.py:304-307
-  }
-  if (out_bf16) ((uint16_t *)out)[o] = (uint16_t)bf16_bits_rtne(a);
-  else ((float *)out)[o] = a;
-}
+using namespace bag;
 
 template <int TK, bool IDX64>
 __global__ void __launch_bounds__(256) bag_rows_kernel(const void *__restrict__ idx, const float *__restrict__ w,
@@ -135,15 +49,7 @@ __global__ void __launch_bounds__(256) bag_rows_kernel(const void *__restrict__ 
     __syncthreads();  // previous pass has finished reading s_off / s_w
     stage_lookups<TK, IDX64>(idx, w, scales, lbase + k0, kc, rows, row_bytes, s_off, s_w, &s_bad);
     __syncthreads();
-    int j = slot;
-    for (; j + (kUnroll - 1) * rpr < kc; j += kUnroll * rpr) {
-      uint4 v[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) v[u] = *(const uint4 *)(colbase + s_off[j + u * rpr]);
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) accumulate<TK>(acc, v[u], s_w[j + u * rpr]);
-    }
-    for (; j < kc; j += rpr) accumulate<TK>(acc, *(const uint4 *)(colbase + s_off[j]), s_w[j]);
+    accumulate_rows<TK>(colbase, slot, rpr, kc, s_off, s_w, acc);
   }
 
 #pragma unroll
@@ -193,12 +99,7 @@ int launch_bag(const void *idx, const float *w, int64_t N, int K, const void *ta
   const bool aligned = ((uintptr_t)table % 16) == 0;
   const int cpr = row_bytes / 16;
   if (aligned && row_bytes % 16 == 0 && cpr >= 1 && cpr <= 256) {
-    // threads = lcm(cpr, 64) (whole wavefronts, every lane busy), at least 128; else as many row slots as fit
-    int g = cpr, b = kWave;
-    while (b) { const int t = g % b; g = b; b = t; }
-    int nthr = cpr / g * kWave;
-    if (nthr > 256) nthr = cpr * (256 / cpr);
-    while (nthr < 128) nthr *= 2;
+    const int nthr = bag_threads(cpr);
     const int rpr = nthr / cpr;
     const size_t shmem = kStage * (sizeof(int64_t) + sizeof(float)) + (size_t)rpr * D * sizeof(float);
     hipLaunchKernelGGL((bag_rows_kernel<TK, IDX64>), dim3((unsigned)N), dim3(nthr), shmem, stream, idx, w,

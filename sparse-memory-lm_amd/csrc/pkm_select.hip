@@ -19,6 +19,7 @@
 //      in registers; the knn keys >= t1 are compacted and put in descending order by counting ranks.
 // Rows outside the register shapes, or with more than kCap elements at or above code0 (adversarial ties),
 // take the streaming path, which searches the row in global memory directly.
+#include "pkm_bag_dev.h"
 #include "pkm_common.h"
 
 namespace smlm {
@@ -29,29 +30,40 @@ constexpr int kRegCand = 4;      // candidates per lane held in registers for th
 constexpr int kMaxKnn = 64;
 
 // ---- the Cartesian pair list, built at compile time: for knn = 2^lg, pairs [off[lg], off[lg+1]) ------------
+// Pair p of knn = 2^lg is ij[off[lg] + p] = i | j << 8; entries past the list read as kNoPair.
+constexpr uint32_t kNoPair = 0xFFFFu;
+constexpr int kMaxPairSlots = 5;  // ceil(280 / 64)
 struct PairTable {
-  uint16_t off[8];
-  uint8_t i[512];
-  uint8_t j[512];
+  uint32_t off[8];
+  uint16_t ij[481 + kMaxPairSlots * 64];
 };
 constexpr PairTable make_pairs() {
   PairTable t{};
   int n = 0;
   for (int lg = 0; lg <= 6; ++lg) {
     const int knn = 1 << lg;
-    t.off[lg] = (uint16_t)n;
+    t.off[lg] = (uint32_t)n;
     for (int i = 0; i < knn; ++i)
-      for (int j = 0; (i + 1) * (j + 1) <= knn; ++j) {
-        t.i[n] = (uint8_t)i;
-        t.j[n] = (uint8_t)j;
-        ++n;
-      }
+      for (int j = 0; (i + 1) * (j + 1) <= knn; ++j) t.ij[n++] = (uint16_t)(i | (j << 8));
   }
-  t.off[7] = (uint16_t)n;  // 1 + 3 + 8 + 20 + 50 + 119 + 280 = 481
+  t.off[7] = (uint32_t)n;  // 1 + 3 + 8 + 20 + 50 + 119 + 280 = 481
+  for (int p = n; p < 481 + kMaxPairSlots * 64; ++p) t.ij[p] = (uint16_t)kNoPair;
   return t;
 }
 __constant__ PairTable kPairs = make_pairs();
-constexpr int kMaxPairSlots = 5;  // ceil(280 / 64)
+
+// This lane's Cartesian pairs for knn (slot s: pair s * 64 + lane, or kNoPair past the list), loaded at kernel
+// start so that the Cartesian step, after the half selections, does not wait on memory.
+__device__ __forceinline__ void load_pairs(int knn, uint32_t (&pc)[kMaxPairSlots]) {
+  const int lg = 31 - __builtin_clz(knn);
+  const int base = (int)kPairs.off[lg], P = (int)kPairs.off[lg + 1] - base;
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 0; s < kMaxPairSlots; ++s) {
+    const int p = s * kWave + lane;
+    pc[s] = p < P ? kPairs.ij[base + p] : kNoPair;
+  }
+}
 
 template <bool F32> struct SelKey;
 template <> struct SelKey<false> { using T = uint32_t; };
@@ -161,7 +173,7 @@ __device__ void topk_of_candidates(int C, int knn, typename SelKey<F32>::T *cand
 }
 
 // Streaming half top-k: any NK, searching the row in global memory.
-template <bool F32>
+template <bool F32, int CAP>
 __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
                                  typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
@@ -180,11 +192,11 @@ __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelK
     const bool take = k < NK && u >= t0;
     const uint64_t m = ballot(take);
     const int pos = C + lanes_below(m);
-    if (take && pos < kCap) cand[pos] = u;
+    if (take && pos < CAP) cand[pos] = u;
     C += (int)__popcll(m);
   }
   wave_lds_sync();
-  if (C <= kCap) {
+  if (C <= CAP) {
     topk_of_candidates<F32>(C, knn, cand, sel, out);
     return;
   }
@@ -219,7 +231,7 @@ __device__ __forceinline__ uint4 chunk_codes(uint4 v) {
 }
 
 // Register half top-k for NK = CPL * 64 chunks of 16 bytes (or fewer chunks, down to one).
-template <bool F32, int CPL>
+template <bool F32, int CPL, int CAP>
 __device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
                               typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
@@ -274,7 +286,7 @@ __device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<
   }
   int C;
   int pos = wave_exclusive_sum(mine, &C);
-  if (C <= kCap) {
+  if (C <= CAP) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + j * kWave;
@@ -288,49 +300,36 @@ __device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<
     wave_lds_sync();
     topk_of_candidates<F32>(C, knn, cand, sel, out);
   } else {
-    half_topk_stream<F32>(row, NK, knn, cand, sel, out);
+    half_topk_stream<F32, CAP>(row, NK, knn, cand, sel, out);
   }
 }
 
-template <bool F32, int CPL>
-__global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1, const void *__restrict__ s2,
-                                                     int NK, int knn, void *__restrict__ scores,
-                                                     int64_t *__restrict__ idx, float *__restrict__ w) {
+// Cartesian step of one head, by one wavefront: candidates (i, j) with (i+1)(j+1) <= knn of the two halves'
+// descending top lists, scored dtype(v1[i] + v2[j]), top-knn by (score, lowest table index), softmax in fp32.
+// Lane j < knn ends with the j-th best pair: its score `sc` (code = order code of its bits), table index `full`
+// and weight `wt`.  pc: the lane's pairs from load_pairs; s_fsel, s_fin: kMaxKnn entries of LDS scratch.
+template <bool F32>
+__device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *top1,
+                                               const typename SelKey<F32>::T *top2, int NK, int knn,
+                                               const uint32_t (&pc)[kMaxPairSlots], uint64_t *s_fsel,
+                                               uint64_t *s_fin, float &sc, uint32_t &full, uint32_t &code,
+                                               float &wt) {
   using Key = typename SelKey<F32>::T;
-  __shared__ Key s_cand[2][kCap];
-  __shared__ Key s_sel[2][kMaxKnn];
-  __shared__ Key s_top[2][kMaxKnn];
-  __shared__ uint64_t s_fsel[kMaxKnn];
-  __shared__ uint64_t s_fin[kMaxKnn];
-
-  const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
-  const int64_t row = blockIdx.x;  // n * H + h
-  const size_t esz = F32 ? 4 : 2;
-  const void *src = (const char *)(wave == 0 ? s1 : s2) + row * (int64_t)NK * esz;
-  if constexpr (CPL > 0) half_topk_reg<F32, CPL>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
-  else half_topk_stream<F32>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
-  __syncthreads();
-  if (wave != 0) return;
-
-  // Cartesian candidates (i, j) with (i+1)(j+1) <= knn, spread over the lanes, keys held in registers
-  const int lg = 31 - __builtin_clz(knn);
-  const int base = kPairs.off[lg];
-  const int P = kPairs.off[lg + 1] - base;
+  // Cartesian candidates (i, j) with (i+1)(j+1) <= knn (this lane's pairs pc), keys held in registers
   uint64_t ck[kMaxPairSlots];
   bool cv[kMaxPairSlots];
 #pragma unroll
   for (int s = 0; s < kMaxPairSlots; ++s) {
-    const int p = s * kWave + lane;
-    cv[s] = p < P;
+    cv[s] = pc[s] != kNoPair;
     ck[s] = 0;
     if (cv[s]) {
-      const Key k1 = s_top[0][kPairs.i[base + p]];
-      const Key k2 = s_top[1][kPairs.j[base + p]];
+      const Key k1 = top1[pc[s] & 0xFFu];
+      const Key k2 = top2[pc[s] >> 8];
       const float sum = key_value<F32>(k1) + key_value<F32>(k2);
-      const uint32_t code = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
-      const uint32_t full = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
-      ck[s] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
+      const uint32_t pc = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
+      const uint32_t pf = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
+      ck[s] = ((uint64_t)pc << 32) | (uint64_t)(0xFFFFFFFFu - pf);
     }
   }
   const uint64_t t = threshold_search<uint64_t>(knn, F32 ? 64 : 48, [&](uint64_t c) {
@@ -358,8 +357,9 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
   }
   wave_lds_sync();
 
-  float sc = 0.f;
-  uint32_t full = 0, code = 0;
+  sc = 0.f;
+  full = 0;
+  code = 0;
   if (lane < knn) {
     const uint64_t u = s_fin[lane];
     code = (uint32_t)(u >> 32);
@@ -369,12 +369,41 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
   const float mxs = __shfl(sc, 0, kWave);  // descending: lane 0 holds the largest score
   const float e = lane < knn ? expf(sc - mxs) : 0.f;
   const float sum = wave_sum(e);
+  wt = e / sum;
+}
+
+template <bool F32, int CPL>
+__global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1, const void *__restrict__ s2,
+                                                     int NK, int knn, void *__restrict__ scores,
+                                                     int64_t *__restrict__ idx, float *__restrict__ w) {
+  using Key = typename SelKey<F32>::T;
+  __shared__ Key s_cand[2][kCap];
+  __shared__ Key s_sel[2][kMaxKnn];
+  __shared__ Key s_top[2][kMaxKnn];
+  __shared__ uint64_t s_fsel[kMaxKnn];
+  __shared__ uint64_t s_fin[kMaxKnn];
+
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int64_t row = blockIdx.x;  // n * H + h
+  const size_t esz = F32 ? 4 : 2;
+  const void *src = (const char *)(wave == 0 ? s1 : s2) + row * (int64_t)NK * esz;
+  uint32_t pc[kMaxPairSlots];
+  load_pairs(knn, pc);
+  if constexpr (CPL > 0) half_topk_reg<F32, CPL, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+  else half_topk_stream<F32, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+  __syncthreads();
+  if (wave != 0) return;
+
+  float sc, wt;
+  uint32_t full, code;
+  cartesian_topk<F32>(s_top[0], s_top[1], NK, knn, pc, s_fsel, s_fin, sc, full, code, wt);
   if (lane < knn) {
     const int64_t o = row * knn + lane;
     if constexpr (F32) ((float *)scores)[o] = sc;
     else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
     idx[o] = (int64_t)full;
-    w[o] = e / sum;
+    w[o] = wt;
   }
 }
 
@@ -393,6 +422,139 @@ void launch_select(const void *s1, const void *s2, int64_t rows, int NK, int knn
   else if (chunks <= 4 * kWave) SMLM_SELECT(4);
   else SMLM_SELECT(8);
 #undef SMLM_SELECT
+}
+
+// ---- selection fused with the value bag (decode): one workgroup per token, 2H wavefronts ----------------------
+// Wavefront (h, p) selects in s_p[n, h, :]; wavefront (h, 0) then does head h's Cartesian step and softmax and
+// stages its knn lookups (row offset, weight x row scale) in LDS; finally the workgroup gathers the token's H*knn
+// rows in the row-slot layout of bag_rows_kernel (bag_threads(cpr) threads, the rest idle), with twice the loads in
+// flight per thread, adds the slots through LDS (over the candidate buffers, no longer needed) and applies the bag
+// epilogue.  Same selection and the same bag additions in the same order as select_kernel followed by
+// bag_rows_kernel, so the results are bit-identical; it saves the launch and the round trip of the lookups.
+constexpr int kFusedCapBytes = 2048;   // LDS candidate bytes per half (512 bf16 / 256 fp32 keys)
+
+constexpr int kFusedMaxHeads = 4;       // 2H wavefronts per workgroup
+
+template <bool F32, int CPL, int TK>
+__global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
+    select_bag_kernel(const void *__restrict__ s1, const void *__restrict__ s2, int H, int NK, int knn,
+                      const uint8_t *__restrict__ table, int64_t rows, int D, int row_bytes, int cpr,
+                      const uint16_t *__restrict__ scales, const uint16_t *__restrict__ pre, void *__restrict__ out,
+                      int out_bf16, size_t union_bytes, void *__restrict__ scores, int64_t *__restrict__ idx,
+                      float *__restrict__ w) {
+  using Key = typename SelKey<F32>::T;
+  constexpr int CAP = kFusedCapBytes / (int)sizeof(Key);
+  constexpr int VPC = bag::vals_per_chunk<TK>();
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nw = 2 * H;
+  Key *s_cand = (Key *)smem;                            // [nw][CAP]; then float [rpr][D] partial sums
+  Key *s_sel = (Key *)(smem + union_bytes);             // [nw][kMaxKnn]
+  Key *s_top = s_sel + nw * kMaxKnn;                    // [nw][kMaxKnn]
+  uint64_t *s_fsel = (uint64_t *)(s_top + nw * kMaxKnn);  // [H][kMaxKnn]
+  uint64_t *s_fin = s_fsel + H * kMaxKnn;               // [H][kMaxKnn]
+  int64_t *s_off = (int64_t *)(s_fin + H * kMaxKnn);    // [H * knn]
+  float *s_w = (float *)(s_off + H * knn);              // [H * knn]
+  __shared__ int s_bad;
+
+  const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
+  const int h = wave >> 1, p = wave & 1;
+  const int64_t n = blockIdx.x;
+  const int64_t row = n * H + h;
+  const size_t esz = F32 ? 4 : 2;
+  if (tid == 0) s_bad = 0;
+  const void *src = (const char *)(p ? s2 : s1) + row * (int64_t)NK * esz;
+  Key *sel = s_sel + wave * kMaxKnn, *top = s_top + wave * kMaxKnn;
+  uint32_t pc[kMaxPairSlots];
+  load_pairs(knn, pc);
+  if constexpr (CPL > 0) half_topk_reg<F32, CPL, CAP>(src, NK, knn, s_cand + wave * CAP, sel, top);
+  else half_topk_stream<F32, CAP>(src, NK, knn, s_cand + wave * CAP, sel, top);
+  __syncthreads();
+
+  if (p == 0) {
+    float sc, wt;
+    uint32_t full, code;
+    cartesian_topk<F32>(s_top + 2 * h * kMaxKnn, s_top + (2 * h + 1) * kMaxKnn, NK, knn, pc,
+                        s_fsel + h * kMaxKnn, s_fin + h * kMaxKnn, sc, full, code, wt);
+    if (lane < knn) {
+      const int64_t o = row * knn + lane;
+      if (scores) {
+        if constexpr (F32) ((float *)scores)[o] = sc;
+        else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
+      }
+      if (idx) idx[o] = (int64_t)full;
+      if (w) w[o] = wt;
+      int64_t r = full;
+      float ww = wt;
+      if (r >= rows) {  // a table with fewer than NK^2 rows: the token's output is NaN, as in the bag
+        s_bad = 1;
+        r = 0;
+        ww = 0.f;
+      }
+      if constexpr (TK == bag::kI8 || TK == bag::kQ4) ww *= f16_bits_to_f32(scales[r]);
+      s_off[h * knn + lane] = r * row_bytes;
+      s_w[h * knn + lane] = ww;
+    }
+  }
+  __syncthreads();
+
+  const int rpr = bag::bag_threads(cpr) / cpr, slot = tid / cpr, c = tid % cpr;
+  float *s_red = (float *)smem;
+  float acc[VPC];
+#pragma unroll
+  for (int e = 0; e < VPC; ++e) acc[e] = 0.f;
+  if (slot < rpr) {
+    bag::accumulate_rows<TK, 2 * bag::kUnroll>(table + (int64_t)c * 16, slot, rpr, H * knn, s_off, s_w, acc);
+#pragma unroll
+    for (int e = 0; e < VPC; ++e) s_red[slot * D + bag::chunk_col<TK>(c, e, D)] = acc[e];
+  }
+  __syncthreads();
+  const bool bad = s_bad != 0;
+  for (int col = tid; col < D; col += blockDim.x) {
+    float a = 0.f;
+    for (int r = 0; r < rpr; ++r) a += s_red[r * D + col];
+    bag::store_out(out, n * D + col, a, bad, pre, out_bf16 != 0);
+  }
+}
+
+template <bool F32, int TK>
+void launch_select_bag(const void *s1, const void *s2, int64_t N, int H, int NK, int knn, const void *table,
+                       int64_t rows, int D, const uint16_t *scales, const uint16_t *pre, void *out, int out_bf16,
+                       void *scores, int64_t *idx, float *w, hipStream_t stream) {
+  using Key = typename SelKey<F32>::T;
+  const int row_bytes = TK == bag::kF32 ? 4 * D : TK == bag::kBF16 ? 2 * D : TK == bag::kI8 ? D : D / 2;
+  const int cpr = row_bytes / 16;
+  const int nthr = 2 * H * kWave;
+  const int rpr = bag::bag_threads(cpr) / cpr;
+  const size_t cand = (size_t)2 * H * kFusedCapBytes, red = (size_t)rpr * D * sizeof(float);
+  const size_t union_bytes = (cand > red ? cand : red + 15) / 16 * 16;
+  const size_t shmem = union_bytes + (size_t)2 * 2 * H * kMaxKnn * sizeof(Key) + (size_t)2 * H * kMaxKnn * 8 +
+                       (size_t)H * knn * (8 + 4);
+  const int epc = F32 ? 4 : 8;
+  const bool aligned = (((uintptr_t)s1 | (uintptr_t)s2) % 16) == 0 && NK % epc == 0;
+  const int chunks = NK / epc;
+  const dim3 grid((unsigned)N), block(nthr);
+#define SMLM_SELECT_BAG(CPL)                                                                                     \
+  hipLaunchKernelGGL((select_bag_kernel<F32, CPL, TK>), grid, block, shmem, stream, s1, s2, H, NK, knn,          \
+                     (const uint8_t *)table, rows, D, row_bytes, cpr, scales, pre, out, out_bf16, union_bytes, \
+                     scores, idx, w)
+  if (!aligned || chunks > 8 * kWave) SMLM_SELECT_BAG(0);
+  else if (chunks <= kWave) SMLM_SELECT_BAG(1);
+  else if (chunks <= 2 * kWave) SMLM_SELECT_BAG(2);
+  else if (chunks <= 4 * kWave) SMLM_SELECT_BAG(4);
+  else SMLM_SELECT_BAG(8);
+#undef SMLM_SELECT_BAG
+}
+
+template <bool F32>
+void launch_select_bag_table(int table_dtype, const void *s1, const void *s2, int64_t N, int H, int NK, int knn,
+                             const void *table, int64_t rows, int D, const uint16_t *scales, const uint16_t *pre,
+                             void *out, int out_bf16, void *scores, int64_t *idx, float *w, hipStream_t stream) {
+  switch (table_dtype) {
+    case SMLM_F32: launch_select_bag<F32, bag::kF32>(s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16, scores, idx, w, stream); break;
+    case SMLM_BF16: launch_select_bag<F32, bag::kBF16>(s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16, scores, idx, w, stream); break;
+    case SMLM_I8: launch_select_bag<F32, bag::kI8>(s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16, scores, idx, w, stream); break;
+    default: launch_select_bag<F32, bag::kQ4>(s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16, scores, idx, w, stream); break;
+  }
 }
 
 }  // namespace
@@ -415,4 +577,46 @@ extern "C" int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_
   if (dtype == SMLM_F32) launch_select<true>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
   else launch_select<false>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
   return launch_status("smlm_pkm_select");
+}
+
+extern "C" int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, int64_t N, int H, int NK, int knn,
+                                   const void *table, int table_dtype, int64_t rows, int D, const uint16_t *scales,
+                                   const uint16_t *pre, void *out, int out_dtype, void *scores, int64_t *idx,
+                                   float *w, void *stream) {
+  using namespace smlm;
+  if (!s1 || !s2 || !table || !out)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: null s1, s2, table or out pointer");
+  if (dtype != SMLM_BF16 && dtype != SMLM_F32)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: dtype must be SMLM_BF16 or SMLM_F32, got %d", dtype);
+  if (N < 0 || N > 0x7FFFFFFFLL || H < 1 || H > kFusedMaxHeads)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: N=%lld, H=%d (1 <= H <= %d)", (long long)N, H,
+                kFusedMaxHeads);
+  if (!is_pow2(knn) || knn > kMaxKnn)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: knn=%d must be a power of two <= %d", knn, kMaxKnn);
+  if (!is_pow2(NK) || NK > 65536 || NK < knn)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: NK=%d must be a power of two in [knn, 65536]", NK);
+  if (table_dtype != SMLM_F32 && table_dtype != SMLM_BF16 && table_dtype != SMLM_I8 && table_dtype != SMLM_Q4)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: table_dtype %d is not a table format", table_dtype);
+  if ((table_dtype == SMLM_I8 || table_dtype == SMLM_Q4) != (scales != nullptr))
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: scales are required for int8 / q4 tables and only for them");
+  if (out_dtype != SMLM_F32 && out_dtype != SMLM_BF16)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: out_dtype must be SMLM_F32 or SMLM_BF16");
+  const int64_t row_bytes = table_dtype == SMLM_F32 ? 4LL * D : table_dtype == SMLM_BF16 ? 2LL * D
+                            : table_dtype == SMLM_I8 ? (int64_t)D : D / 2;
+  if (D < 1 || (table_dtype == SMLM_Q4 && D % 2) || row_bytes % 16 || rows < 1 ||
+      bag::bag_threads((int)(row_bytes / 16)) > 2 * H * kWave)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: rows of D=%d must be whole 16-byte chunks that the "
+                "%d-thread workgroup covers in the value bag's row-slot layout", D, 2 * H * kWave);
+  if ((uintptr_t)table % 16)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_bag: the table must be 16-byte aligned");
+  if (N == 0) return SMLM_OK;
+  const int out_bf16 = out_dtype == SMLM_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == SMLM_F32)
+    launch_select_bag_table<true>(table_dtype, s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16,
+                                  scores, idx, w, s);
+  else
+    launch_select_bag_table<false>(table_dtype, s1, s2, N, H, NK, knn, table, rows, D, scales, pre, out, out_bf16,
+                                   scores, idx, w, s);
+  return launch_status("smlm_pkm_select_bag");
 }

@@ -347,6 +347,112 @@ class Transformer(nn.Module):
         return self._decoders[key]
 
 
+class _FusedDecodeStep:
+    """One greedy decode step of a bf16 model on the fused decode kernels of smlm_hip.kernels.  Per dense block
+        [residual add + attn_norm + wqkv] [RoPE + cache write + attention] [wo]
+        [residual add + ffn_norm + w13 + SwiGLU] [w2]
+    and per memory block, after the attention,
+        [residual add + ffn_norm + query_proj | swilu_proj + eval BatchNorm] [sub-key scores]
+        [selection + value bag + swilu] [value_proj]
+    then [residual add + final norm + lm_head + argmax partials] [token, history slot, position + 1]; the first
+    block's prologue gathers the token embeddings.  These are the ops of Transformer.forward on bf16 weights
+    (smlm/model.py:63-118, 156-163, 266-293; smlm/pkm.py:186-228) with the same bf16 roundings: 5 launches per
+    dense block, 7 per memory block and 2 for the head, instead of the ~10 PyTorch launches per block.
+
+    Derived weights (the concatenated query_proj | swilu_proj and its bias) are built at construction and rebuilt
+    on an eager run after a parameter changed; a captured graph keeps what it was captured with."""
+
+    @staticmethod
+    def supported(model, dtype):
+        """Whether the model's shapes and options are covered by the fused kernels (else the step runs
+        Transformer.forward)."""
+        cfg = model.cfg
+        w = model.tok_emb.weight
+        if dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not w.is_cuda:
+            return False
+        C, hd = cfg.d_model, cfg.d_model // cfg.n_heads
+        if C % 32 or C > 480 or C % cfg.n_heads or hd not in (16, 32, 64, 128) or cfg.ffn_hidden % 16 \
+                or cfg.vocab_size % 16:
+            return False
+        for blk in model.layers:
+            if blk.ffn_r2 is not None:
+                return False
+            if blk.is_memory:
+                m = blk.ffn
+                table = (getattr(m.values, "infer_table", None) or (m.values.weight, None))[0]
+                if (not m.swilu or m.log_score_scale is not None or m.record or m.heads > 4
+                        or (m.heads * m.k_dim) % 16 or (m.k_dim // 2) % 8 or m.v_dim % 32
+                        or m.query_proj.weight.dtype != torch.bfloat16
+                        or (m.query_norm is not None and m.query_norm.training)
+                        or not kernels.select_bag_supported(m.heads, table)):
+                    return False
+        return True
+
+    def __init__(self, model):
+        self.model = model
+        self._tag = None
+        self._prepare()
+
+    def _params_tag(self):
+        return tuple((p.data_ptr(), p._version) for p in self.model.parameters())
+
+    def _prepare(self):
+        self.mem = {}
+        for i, blk in enumerate(self.model.layers):
+            if blk.is_memory:
+                m = blk.ffn
+                w = torch.cat([m.query_proj.weight.detach(), m.swilu_proj.weight.detach()]).contiguous()
+                b = torch.cat([m.query_proj.bias.detach(), m.swilu_proj.bias.detach()]).contiguous()
+                self.mem[i] = (w, b)
+        self._tag = self._params_tag()
+
+    def run(self, tok, pos, caches, hist, logits=False, record=None):
+        """The step for tok (B, 1) at device position pos: writes the next token to tok and hist[:, pos + 1] and
+        advances pos.  With logits=True it returns the (B, vocab) bf16 logits instead and changes none of tok,
+        hist and pos (the KV caches get the same slot written).  With a dict `record`, record[layer] =
+        (s1, s2, scores, indices, weights) of each memory layer's lookup."""
+        model = self.model
+        if not torch.cuda.is_current_stream_capturing() and self._params_tag() != self._tag:
+            self._prepare()
+        B = tok.shape[0]
+        x = delta = None
+        for i, blk in enumerate(model.layers):
+            at = blk.attn
+            if x is None:
+                x, qkv = kernels.decode_linear(at.wqkv.weight, tok=tok.view(-1), emb=model.tok_emb.weight,
+                                               norm=blk.attn_norm, write_x=True)
+            else:
+                x, qkv = kernels.decode_linear(at.wqkv.weight, x, delta=delta, norm=blk.attn_norm, write_x=True)
+            y = kernels.decode_attention(qkv, at.rope.cos, at.rope.sin, pos, caches[i].k, caches[i].v)
+            delta = kernels.decode_linear(at.wo.weight, y)
+            if blk.is_memory:
+                m = blk.ffn
+                w, b = self.mem[i]
+                nq = m.heads * m.k_dim
+                affine = m._bn_affine() if m.query_norm is not None else None
+                x, (q, pre) = kernels.decode_linear(w, x, delta=delta, norm=blk.ffn_norm, write_x=True, bias=b,
+                                                    affine=affine, n_split=nq)
+                s1, s2 = kernels.pk_scores(q.view(B, m.heads, m.k_dim), m._keys_as(torch.bfloat16))
+                table, scales = getattr(m.values, "infer_table", None) or (m.values.weight.detach(), None)
+                if record is None:
+                    out = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True)
+                else:
+                    out, sc, idx, wt = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True,
+                                                             record=True)
+                    record[i] = (s1, s2, sc, idx, wt)
+                delta = kernels.decode_linear(m.value_proj.weight, out, bias=m.value_proj.bias)
+            else:
+                f = blk.ffn
+                x, act = kernels.decode_linear(f.w13.weight, x, delta=delta, norm=blk.ffn_norm, write_x=True,
+                                               swiglu=True)
+                delta = kernels.decode_linear(f.w2.weight, act)
+        if logits:
+            return kernels.decode_linear(model.lm_head.weight, x, delta=delta, norm=model.norm)
+        partial = kernels.decode_linear(model.lm_head.weight, x, delta=delta, norm=model.norm, argmax=True)
+        kernels.argmax_finish(partial, pos, tok.view(-1), hist)
+        return None
+
+
 class _StepDecoder:
     """Static buffers and the captured graph of one decode step for batch B, sequences up to max_len."""
 
@@ -364,8 +470,12 @@ class _StepDecoder:
         self.pos = torch.zeros((), dtype=torch.long, device=device)
         self.hist = torch.zeros(B, max_len, dtype=torch.long, device=device)
         self.graph = None
+        self.fused = _FusedDecodeStep(model) if _FusedDecodeStep.supported(model, dtype) else None
 
     def _step(self):
+        if self.fused is not None:
+            self.fused.run(self.tok, self.pos, self.caches, self.hist)
+            return
         logits = self.model(self.tok, kv_caches=self.caches, pos0=self.pos)
         last = logits[:, -1]
         if last.is_cuda and last.dtype == torch.bfloat16:

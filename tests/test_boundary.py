@@ -96,3 +96,43 @@ def test_kernels_refuse_cpu_tensors():
     s = torch.zeros(1, 1, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP"):
         kernels.pk_select(s, s, 8)
+
+
+def test_linear_args_struct_layout_matches_header(tmp_path):
+    """The ctypes mirror of struct smlm_linear_args has the C compiler's field offsets and size."""
+    import subprocess
+    fields = [f for f, _ in _lib.LinearArgs._fields_]
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("{f} %zu\\n", offsetof(smlm_linear_args, {f}));\n' for f in fields)
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "smlm_pkm.h"\nint main(void) {\n' + body +
+                   '  printf("sizeof %zu\\n", sizeof(smlm_linear_args));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                       text=True).stdout.splitlines())
+    for f in fields:
+        assert int(got[f]) == getattr(_lib.LinearArgs, f).offset, f
+    assert int(got["sizeof"]) == ctypes.sizeof(_lib.LinearArgs)
+
+
+def test_decode_linear_argument_checks():
+    lib = _lib.lib()
+    fake = 256
+    assert lib.smlm_decode_linear(None, None) == _lib.EINVAL
+    a = _lib.LinearArgs()
+    a.prologue, a.epilogue, a.M, a.N, a.K = _lib.LIN_PLAIN, _lib.LIN_STORE, 4, 64, 384
+    a.x, a.x_stride, a.w, a.n_split, a.out, a.out_stride = fake, 384, fake, 64, fake, 64
+    a.N = 40                                              # not a multiple of 16
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.N, a.K = 64, 100                                    # K not a multiple of 32
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.K, a.x_stride, a.prologue, a.norm_w = 512, 512, _lib.LIN_RMSNORM, fake  # normalised rows too wide for LDS
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    a.K, a.x_stride, a.prologue, a.epilogue = 384, 384, _lib.LIN_PLAIN, _lib.LIN_ARGMAX    # partial missing
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "partial" in _lib.last_error()
+    a.epilogue, a.delta = _lib.LIN_STORE, fake            # delta without an RMSNorm prologue
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.delta, a.M = None, 0                                # zero rows: a valid no-op
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.OK
+    assert lib.smlm_linear_argmax_blocks(32000) == 250 and lib.smlm_linear_argmax_blocks(129) == 2
+    assert lib.smlm_argmax_finish(None, 1, 1, 1, fake, fake, None, 0, 0, 1, None) == _lib.EINVAL

@@ -1,0 +1,337 @@
+"""Fused decode-step kernels (smlm_decode_linear, smlm_argmax_finish) against fp64 CPU restatements of the
+reference ops they replace: nn.Linear (smlm/model.py:90-118), the residual add + RMSNorm (model.py:156-163), the
+token embedding (model.py:268), the eval BatchNorm of the memory query (smlm/pkm.py:188-191), SwiGLU
+(model.py:110-118) and the greedy argmax of the decode loop (smlm/train.py:297-301).
+
+Tolerances: bf16 outputs within 2^-7 relative of the fp64 value plus 2^-9 of the output scale (the kernel
+accumulates in fp32 in its own order and rounds once); the residual stream (x + delta in bf16) is bit-exact; the
+argmax token is exact wherever the best logit is separated from the runner-up, and planted exact ties resolve to
+the lowest column.
+"""
+import pytest
+import torch
+
+from smlm_hip import _lib
+from smlm_hip import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+def rms_ref(xs, g, eps):
+    """bf16(xs * rsqrt(mean(xs^2) + eps) * g) in fp64 (xs, g bf16)."""
+    x = xs.double()
+    return bf(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * g.double())
+
+
+def assert_bf16_close(got, ref, what):
+    got, ref = got.float().cpu().double(), ref.double()
+    scale = float(ref.abs().max())
+    err = (got - ref).abs() - (2 ** -7 * ref.abs() + 2 ** -9 * scale)
+    assert float(err.max()) <= 0, f"{what}: worst excess {float(err.max())} (scale {scale})"
+
+
+def make_norm(K_, g):
+    norm = torch.nn.RMSNorm(K_, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(K_, generator=g) + 0.5)
+    return norm.to(DEV, torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,N,K_", [(1, 1152, 384), (64, 1152, 384), (5, 384, 1024), (100, 48, 64),
+                                    (64, 384, 384), (130, 2432, 384)])
+def test_plain_store(M, N, K_):
+    note(f"decode_linear plain M={M} N={N} K={K_}")
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = bf(torch.randn(M, K_, generator=g))
+    w = bf(torch.randn(N, K_, generator=g) * 0.05)
+    b = bf(torch.randn(N, generator=g) * 0.1)
+    got = K.decode_linear(w.to(DEV), x.to(DEV))
+    assert_bf16_close(got, bf(x.double() @ w.double().T).double(), "plain")
+    got_b = K.decode_linear(w.to(DEV), x.to(DEV), bias=b.to(DEV))
+    assert_bf16_close(got_b, bf(x.double() @ w.double().T + b.double()).double(), "plain + bias")
+
+
+def test_plain_strided_input():
+    """x rows taken from a wider buffer (row stride > K), as the attention output of a fused qkv buffer."""
+    g = torch.Generator().manual_seed(11)
+    big = bf(torch.randn(8, 1152, generator=g))
+    w = bf(torch.randn(384, 384, generator=g) * 0.05)
+    xd = big.to(DEV)[:, 384:768]
+    got = K.decode_linear(w.to(DEV), xd)
+    assert_bf16_close(got, bf(big[:, 384:768].double() @ w.double().T).double(), "strided x")
+
+
+@pytest.mark.parametrize("M", [1, 3, 64, 77])
+@pytest.mark.parametrize("with_delta", [False, True])
+def test_rmsnorm_store_affine_split(M, with_delta):
+    """Residual add + RMSNorm + the memory layer's query_proj | swilu_proj with bias, eval-BatchNorm affine on
+    the query columns, split into (q, pre)."""
+    note(f"decode_linear rmsnorm+affine M={M} delta={with_delta}")
+    g = torch.Generator().manual_seed(M + 100 * with_delta)
+    K_, NQ, NP = 384, 2048, 384
+    x = bf(torch.randn(M, K_, generator=g))
+    d = bf(torch.randn(M, K_, generator=g)) if with_delta else None
+    w = bf(torch.randn(NQ + NP, K_, generator=g) * 0.05)
+    b = bf(torch.randn(NQ + NP, generator=g) * 0.1)
+    scale = torch.rand(NQ, generator=g) + 0.5
+    shift = torch.randn(NQ, generator=g) * 0.1
+    norm = make_norm(K_, g)
+    xs_ref = bf(x.double() + d.double()) if with_delta else x
+    h = rms_ref(xs_ref, norm.weight.detach().cpu(), 1e-5)
+    v = bf(h.double() @ w.double().T + b.double())
+    q_ref = bf(v[:, :NQ].double() * scale.double() + shift.double())
+    pre_ref = v[:, NQ:]
+    xs, (q, pre) = K.decode_linear(w.to(DEV), x.to(DEV), delta=d.to(DEV) if d is not None else None, norm=norm,
+                                   write_x=True, bias=b.to(DEV), affine=(scale.to(DEV), shift.to(DEV)), n_split=NQ)
+    assert torch.equal(xs.cpu(), xs_ref)
+    assert_bf16_close(q, q_ref.double(), "query (affine)")
+    assert_bf16_close(pre, pre_ref.double(), "pre")
+
+
+@pytest.mark.parametrize("M", [1, 64, 65])
+def test_embed_rmsnorm_store(M):
+    note(f"decode_linear embed M={M}")
+    g = torch.Generator().manual_seed(M + 5)
+    V, K_, N = 1000, 384, 1152
+    emb = bf(torch.randn(V, K_, generator=g) * 0.02)
+    tok = torch.randint(0, V, (M,), generator=g)
+    w = bf(torch.randn(N, K_, generator=g) * 0.05)
+    norm = make_norm(K_, g)
+    xs, y = K.decode_linear(w.to(DEV), tok=tok.to(DEV), emb=emb.to(DEV), norm=norm, write_x=True)
+    assert torch.equal(xs.cpu(), emb[tok])
+    h = rms_ref(emb[tok], norm.weight.detach().cpu(), 1e-5)
+    assert_bf16_close(y, bf(h.double() @ w.double().T).double(), "embed + norm + linear")
+
+
+@pytest.mark.parametrize("M", [1, 64, 70])
+def test_rmsnorm_swiglu(M):
+    note(f"decode_linear swiglu M={M}")
+    g = torch.Generator().manual_seed(M + 9)
+    K_, H = 384, 1024
+    x = bf(torch.randn(M, K_, generator=g))
+    d = bf(torch.randn(M, K_, generator=g))
+    w = bf(torch.randn(2 * H, K_, generator=g) * 0.05)
+    norm = make_norm(K_, g)
+    got = K.decode_linear(w.to(DEV), x.to(DEV), delta=d.to(DEV), norm=norm, swiglu=True)
+    h = rms_ref(bf(x.double() + d.double()), norm.weight.detach().cpu(), 1e-5)
+    ab = bf(h.double() @ w.double().T)
+    a, b = ab[:, :H].double(), ab[:, H:].double()
+    ref = bf(bf(torch.nn.functional.silu(a)).double() * b)
+    # a and b may each sit one bf16 rounding away from the fp64 value: allow two roundings
+    got, ref = got.float().cpu().double(), ref.double()
+    scale = float(ref.abs().max())
+    assert float(((got - ref).abs() - (2 ** -6 * ref.abs() + 2 ** -8 * scale)).max()) <= 0
+
+
+@pytest.mark.parametrize("M,N", [(1, 32000), (64, 32000), (3, 128), (70, 1008)])
+def test_argmax_epilogue_and_finish(M, N):
+    """lm_head + greedy argmax: the token is the fp64 argmax wherever it is separated from the runner-up by more
+    than the bf16 rounding of the logits; exact ties (duplicated weight rows) go to the lowest column; the
+    history slot pos + 1 is written and pos advances by one."""
+    note(f"decode_linear argmax M={M} N={N}")
+    g = torch.Generator().manual_seed(M + N)
+    K_ = 384
+    x = bf(torch.randn(M, K_, generator=g))
+    d = bf(torch.randn(M, K_, generator=g))
+    w = bf(torch.randn(N, K_, generator=g) * 0.05)
+    norm = make_norm(K_, g)
+    h = rms_ref(bf(x.double() + d.double()), norm.weight.detach().cpu(), 1e-5)
+    logits = h.double() @ w.double().T
+    best = logits.argmax(-1)
+    # plant an exact tie for row 0: a later column with the same weight row as the winner
+    j = int(best[0])
+    dup = N - 1 if j != N - 1 else 0
+    w[j] = bf(w[j].double() * 1.5)        # a clear winner for row 0 ...
+    w[dup] = w[j]                          # ... tied exactly with a later column
+    logits = h.double() @ w.double().T
+    top2 = logits.topk(2, -1).values
+    sep = (top2[:, 0] - top2[:, 1]) > 2 ** -6 * top2[:, 0].abs()
+    ref = logits.argmax(-1)            # torch.argmax: first index of the maximum
+    L = 10
+    hist = torch.full((M, L), -1, dtype=torch.int64, device=DEV)
+    pos = torch.tensor(3, device=DEV)
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    partial = K.decode_linear(w.to(DEV), x.to(DEV), delta=d.to(DEV), norm=norm, argmax=True)
+    assert partial.shape == (M, _lib.lib().smlm_linear_argmax_blocks(N))
+    K.argmax_finish(partial, pos, tok, hist)
+    got = tok.cpu()
+    assert int(got[0]) == min(j, dup), (int(got[0]), j, dup)
+    assert torch.equal(got[sep], ref[sep])
+    assert int(pos) == 4
+    assert torch.equal(hist[:, 4].cpu(), got) and bool((hist[:, :4] == -1).all()) and bool((hist[:, 5:] == -1).all())
+    K.argmax_finish(partial, torch.tensor(L - 1, device=DEV), tok, hist)   # slot L is outside: no write
+    assert bool((hist[:, 5:] == -1).all())
+
+
+def test_argmax_all_equal_logits_gives_column_zero():
+    M, N, K_ = 4, 640, 64
+    w = torch.zeros(N, K_, dtype=torch.bfloat16, device=DEV)
+    x = torch.randn(M, K_, device=DEV).to(torch.bfloat16)
+    partial = K.decode_linear(w, x, argmax=True)
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    pos = torch.tensor(0, device=DEV)
+    K.argmax_finish(partial, pos, tok, advance=False)
+    assert bool((tok == 0).all()) and int(pos) == 0
+
+
+def test_decode_linear_rejects_bad_shapes():
+    w = torch.zeros(100, 384, dtype=torch.bfloat16, device=DEV)      # N not a multiple of 16
+    x = torch.zeros(2, 384, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.SmlmError):
+        K.decode_linear(w, x)
+    w2 = torch.zeros(64, 1024, dtype=torch.bfloat16, device=DEV)     # RMSNorm prologue with K > 480
+    x2 = torch.zeros(2, 1024, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(_lib.SmlmError):
+        K.decode_linear(w2, x2, norm=make_norm(1024, torch.Generator().manual_seed(0)))
+
+
+# ------------------------------------------------------------------------------------- fused selection + value bag
+def _tables(kind, rows, D, seed):
+    """A (rows, D) value table drawn on the device (N(0, 0.02)), in the given inference format."""
+    gd = torch.Generator(device=DEV).manual_seed(seed)
+    dt = torch.float32 if kind in ("fp32", "int8", "q4") else torch.bfloat16
+    vals = torch.empty(rows, D, dtype=dt, device=DEV).normal_(0.0, 0.02, generator=gd)
+    if kind in ("fp32", "bf16"):
+        return vals, None
+    return K.quantize_int8(vals) if kind == "int8" else K.quantize_q4(vals)
+
+
+@pytest.mark.parametrize("N,H,NK,knn,dtype,kind,with_pre,out_bf16", [
+    (1, 4, 4096, 32, torch.bfloat16, "bf16", True, True),
+    (64, 4, 4096, 32, torch.bfloat16, "bf16", True, True),
+    (5, 4, 1024, 32, torch.bfloat16, "int8", True, True),
+    (7, 4, 512, 32, torch.bfloat16, "q4", False, False),
+    (3, 2, 256, 16, torch.bfloat16, "fp32", False, False),
+    (9, 3, 2048, 64, torch.bfloat16, "bf16", True, False),
+    (4, 2, 2048, 32, torch.float32, "bf16", True, True),
+    (2, 4, 8192, 32, torch.bfloat16, "bf16", True, True),     # rows beyond the register path: streaming search
+])
+def test_select_bag_bit_identical_to_select_then_bag(N, H, NK, knn, dtype, kind, with_pre, out_bf16):
+    """pk_select_bag == pk_select followed by bag_infer, bit for bit (same selection, same bag additions)."""
+    note(f"select_bag N={N} H={H} NK={NK} knn={knn} {dtype} {kind}")
+    g = torch.Generator().manual_seed(N * 31 + NK + knn)
+    D = 384
+    s1 = torch.randn(N, H, NK, generator=g).to(DEV, dtype)
+    s2 = torch.randn(N, H, NK, generator=g).to(DEV, dtype)
+    rows = NK * NK if NK <= 4096 else 1 << 20     # NK 8192: a smaller table, tokens reaching beyond it are NaN
+    table, scales = _tables(kind, rows, D, N + NK)
+    pre = torch.randn(N, D, generator=g).to(DEV, torch.bfloat16) if with_pre else None
+    sc, idx, w = K.pk_select(s1, s2, knn)
+    ref = K.bag_infer(idx.view(N, -1), w.view(N, -1), table, scales, pre=pre, out_bf16=out_bf16)
+    out, sc2, idx2, w2 = K.pk_select_bag(s1, s2, knn, table, scales, pre=pre, out_bf16=out_bf16, record=True)
+    assert torch.equal(idx2, idx) and torch.equal(sc2.view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                                                  sc.view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+    assert torch.equal(w2, w)
+    assert torch.equal(torch.isnan(out), torch.isnan(ref))
+    assert torch.equal(torch.nan_to_num(out), torch.nan_to_num(ref))
+    out_only = K.pk_select_bag(s1, s2, knn, table, scales, pre=pre, out_bf16=out_bf16)
+    assert torch.equal(torch.nan_to_num(out_only), torch.nan_to_num(ref))
+
+
+def test_select_bag_rejects_unsupported():
+    s = torch.zeros(1, 5, 64, dtype=torch.bfloat16, device=DEV)                # 5 heads
+    t = torch.zeros(64 * 64, 384, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        K.pk_select_bag(s, s, 8, t)
+    s1 = torch.zeros(1, 1, 64, dtype=torch.bfloat16, device=DEV)               # 1 head: 128 threads < 192
+    assert not K.select_bag_supported(1, t)
+    with pytest.raises(_lib.SmlmError):
+        K.pk_select_bag(s1, s1, 8, t)
+
+
+# ------------------------------------------------------------------------------------------- the fused decode step
+def _bits(t):
+    return t.detach().view(torch.int16).cpu().numpy().view("uint16")
+
+
+def _prefilled(model, B, P, seed):
+    """A _StepDecoder for model with B random prompts of P tokens prefilled; returns (decoder, prompt)."""
+    dec = model._decoder(B, P + 8, DEV)
+    prompt = torch.randint(0, model.cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(seed)).to(DEV)
+    logits = model(prompt, kv_caches=dec.caches, pos0=0)
+    dec.hist[:, :P] = prompt
+    dec.hist[:, P] = logits[:, -1].argmax(-1)
+    dec.tok.copy_(dec.hist[:, P:P + 1])
+    dec.pos.fill_(P)
+    return dec, prompt
+
+
+@torch.no_grad()
+def test_fused_step_logits_match_generic_step():
+    """The fused decode step (no memory layer) against Transformer.forward's single-token static-cache step on
+    the same caches and token: logits within 2e-2 of their scale (the two paths round their GEMMs in different
+    orders), and the step's token is the argmax of its own logits wherever that is separated."""
+    from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
+    cfg = ModelConfig(vocab_size=1024, d_model=384, n_layers=3, n_heads=6, ffn_hidden=1024, max_seq_len=64)
+    torch.manual_seed(0)
+    m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
+    assert _FusedDecodeStep.supported(m, torch.bfloat16)
+    for B in (1, 5):
+        note(f"fused step vs generic B={B}")
+        dec, _ = _prefilled(m, B, 12, B)
+        assert dec.fused is not None
+        ref = m(dec.tok, kv_caches=dec.caches, pos0=dec.pos.clone()).float()[:, -1]
+        got = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True).float()
+        err = float((got - ref).abs().max() / ref.abs().max())
+        assert err < 2e-2, err
+        pos0 = int(dec.pos)
+        dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist)
+        assert int(dec.pos) == pos0 + 1
+        top2 = got.topk(2, -1).values
+        sep = (top2[:, 0] - top2[:, 1]) > 2 ** -6 * top2[:, 0].abs()
+        assert torch.equal(dec.tok.view(-1)[sep].cpu(), got.argmax(-1)[sep].cpu())
+        assert torch.equal(dec.hist[:, pos0 + 1], dec.tok.view(-1))
+
+
+@torch.no_grad()
+def test_fused_step_with_memory_layer_matches_torch_path():
+    """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its selection is
+    bit-exact against the oracle on the step's own sub-key scores, and its logits are within 1e-2 of the fp32
+    torch path (oracle/torch_path.py) given that selection (the prompt pass does not reach the step through
+    the last block, so the caches agree)."""
+    import numpy as np
+    import oracle.pkm_oracle as O
+    import oracle.torch_path as TP
+    from smlm_hip.model import ModelConfig, Transformer
+    cfg = ModelConfig(vocab_size=512, d_model=128, n_layers=3, n_heads=2, ffn_hidden=256, max_seq_len=64,
+                      mem_layers=[2], mem_n_keys=128, mem_heads=4, mem_knn=16, mem_k_dim=64)
+    torch.manual_seed(3)
+    m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
+    with torch.no_grad():
+        bn = m.layers[2].ffn.query_norm
+        bn.running_mean.normal_(0.0, 0.1)
+        bn.running_var.uniform_(0.5, 2.0)
+        bn.weight.uniform_(0.5, 1.5)
+        bn.bias.normal_(0.0, 0.1)
+    for kind in ("bf16", "int8"):
+        m.set_memory_inference_table(kind)
+        B, P = 3, 10
+        note(f"fused step memory layer table={kind}")
+        dec, prompt = _prefilled(m, B, P, 7)
+        assert dec.fused is not None
+        rec = {}
+        got = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec).float().cpu()
+        s1, s2, sc, idx, w = rec[2]
+        rs, ri, rw = O.pk_select(_bits(s1), _bits(s2), cfg.mem_knn)
+        assert np.array_equal(idx.cpu().numpy(), ri) and np.array_equal(_bits(sc), rs)
+        np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)
+        sd = {k: v.float().cpu() for k, v in m.state_dict().items()}
+        tables = None
+        if kind == "int8":
+            codes, scales = m.layers[2].ffn.values.infer_table
+            tables = {2: K.dequantize_int8(codes, scales).cpu()}
+        caches = [dict() for _ in range(cfg.n_layers)]
+        TP.lm_forward(sd, cfg.to_dict(), prompt.cpu(), caches, 0, tables=tables)
+        ref = TP.lm_forward(sd, cfg.to_dict(), dec.tok.cpu(), caches, P, tables=tables,
+                            selections={2: (idx.cpu(), w.cpu())})[:, -1]
+        err = float((got - ref).abs().max() / ref.abs().max())
+        assert err < 1e-2, err
