@@ -9,6 +9,10 @@ HBM GB/s".
                  prompts, then K greedy steps; each step is one replay of the captured whole-step HIP graph
                  (embedding, 6 blocks, lm_head, argmax, KV write).  value = 64 * K / time of the K steps.
   decode_bs1     the same at batch 1.
+  config1        config 1: the same LM with the B-1M memory (1024^2 rows), 512-token prompt, greedy decode at
+                 batch 1 (whole-step graph).
+  prefill        config 2: the LM with the B-4M memory (2048^2 rows) forward over 8 x 2048 prompt tokens (no
+                 cache), tokens / median forward time.
   pkm_lookup     config 2 (B-4M, 8 x 2048 tokens): scoring + selection + value bag kernels, tokens / time.
   gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out;
                  algorithmic bytes 3,439,329,280 per call; plus a uniform-index control.
@@ -62,19 +66,20 @@ def build_lm(cfg, dev, seed=0):
     return model
 
 
-def time_decode(model, B, steps, warmup, dev, seed=1):
-    """Prefill B uniform 128-token prompts, run `warmup` graph steps, then time `steps` graph replays."""
+def time_decode(model, B, steps, warmup, dev, seed=1, prompt_len=128):
+    """Prefill B uniform prompts of prompt_len tokens, run `warmup` graph steps, then time `steps` graph replays."""
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
-    prompt = torch.randint(0, model.cfg.vocab_size, (B, 128), generator=g, device=dev)
+    P = prompt_len
+    prompt = torch.randint(0, model.cfg.vocab_size, (B, P), generator=g, device=dev)
     with torch.no_grad():
-        dec = model._decoder(B, 128 + warmup + steps + 1, dev)
+        dec = model._decoder(B, P + warmup + steps + 1, dev)
         dec._capture()
         logits = model(prompt, kv_caches=dec.caches, pos0=0)
-        dec.hist[:, :128] = prompt
-        dec.hist[:, 128] = logits[:, -1].argmax(-1)
-        dec.tok.copy_(dec.hist[:, 128:129])
-        dec.pos.fill_(128)
+        dec.hist[:, :P] = prompt
+        dec.hist[:, P] = logits[:, -1].argmax(-1)
+        dec.tok.copy_(dec.hist[:, P:P + 1])
+        dec.pos.fill_(P)
         for _ in range(warmup):
             dec.graph.replay()
         torch.cuda.synchronize(dev)
@@ -84,6 +89,26 @@ def time_decode(model, B, steps, warmup, dev, seed=1):
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0
     return B * steps / dt, 1000.0 * dt / steps
+
+
+def time_prefill(model, B, T, reps, dev, seed=3):
+    """Config 2 prefill: the LM forward (no cache) over B uniform prompts of T tokens; median wall time of `reps`
+    forwards after 2 warm-ups, each synchronised."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    prompt = torch.randint(0, model.cfg.vocab_size, (B, T), generator=g, device=dev)
+    times = []
+    with torch.no_grad():
+        for i in range(2 + reps):
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            model(prompt)
+            torch.cuda.synchronize(dev)
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+    times.sort()
+    ms = 1000.0 * times[len(times) // 2]
+    return B * T / ms * 1e3, ms
 
 
 def event_time_ms(fn, reps, warm=3):
@@ -233,12 +258,13 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--reps", type=int, default=20, help="timed launches per kernel measurement")
+    ap.add_argument("--prefill-reps", type=int, default=5, help="timed forwards of the config-2 prefill")
     ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,lookup,gather,cpu",
-                    help="subset of decode,lookup,gather,cpu,calibrate (profiling runs); the JSON line is "
-                         "complete only with the default")
+    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,cpu",
+                    help="subset of decode,config1,prefill,lookup,gather,cpu,calibrate (profiling runs); the JSON "
+                         "line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
@@ -268,6 +294,25 @@ def main():
         log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
         tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
         log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
+    c1 = pf = None
+    if "config1" in phases:
+        t0 = time.perf_counter()
+        m1 = build_lm(lm_config(1024, 512 + args.warmup + args.steps + 2), dev)
+        tok_s, ms = time_decode(m1, 1, args.steps, args.warmup, dev, prompt_len=512)
+        c1 = {"tok_s": tok_s, "ms_per_step": ms, "batch": 1, "prompt_len": 512, "new_tokens": args.steps,
+              "table": "1,048,576 x 384 bf16 (B-1M)"}
+        log(f"decode config 1 (B-1M, 512-token prompt, bs1): {tok_s:.1f} tok/s ({ms:.3f} ms/step), "
+            f"{time.perf_counter() - t0:.1f} s")
+        del m1
+        torch.cuda.empty_cache()
+    if "prefill" in phases:
+        m2 = build_lm(lm_config(2048, 2048), dev)
+        tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
+        pf = {"tok_s": tok_s, "ms_per_forward": ms, "batch": 8, "seq_len": 2048,
+              "table": "4,194,304 x 384 bf16 (B-4M)"}
+        log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
+        del m2
+        torch.cuda.empty_cache()
     lk = ga = cpu = None
     if "lookup" in phases:
         lk = lookup_prefill(dev, args.reps)
@@ -304,6 +349,7 @@ def main():
                                "whole-step hipGraph", "global_batch": 64, "prompt_len": 128,
                    "new_tokens": args.steps},
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
+        "decode_config1_bs1": c1, "prefill_config2": pf,
         "pkm_lookup_config2": lk, "gather_config4": ga,
         "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
     }

@@ -14,7 +14,8 @@
 //      l, l+64, ...), and turned into order codes (packed 16-bit ops for bf16);
 //   2. each lane's maximum code; the knn-th largest of the 64 lane maxima, code0, is reached by at least knn
 //      elements (the top knn lanes each hold one), found by a bitwise search over ballot() counts;
-//   3. the elements with code >= code0 (typically a few dozen) are compacted into LDS via a lane prefix sum;
+//   3. the 16-byte chunks holding an element >= code0 are staged in LDS, and their elements >= code0 (typically a
+//      few dozen) are compacted into the candidate list via a lane prefix sum;
 //   4. the exact knn-th largest key t1 among them is found by the same bitwise search with the candidates held
 //      in registers; the knn keys >= t1 are compacted and put in descending order by counting ranks.
 // Rows outside the register shapes, or with more than kCap elements at or above code0 (adversarial ties),
@@ -102,13 +103,55 @@ __device__ __forceinline__ Key threshold_search(int need, int bits, CountGE coun
   return t;
 }
 
+// The same search over keys (code << S) | ((2^S - 1) - index) with index < 2^IB and codes in bits [S, top): bits
+// [IB, S) are set in every key, so the knn-th largest key has them too and they are set without a test; only the
+// code bits and the IB index bits are searched.
+template <typename Key, typename CountGE>
+__device__ __forceinline__ Key key_search(int need, int top, int S, int IB, CountGE count_ge) {
+  Key t = 0;
+  for (int b = top - 1; b >= S; --b) {
+    const Key c = t | ((Key)1 << b);
+    if (count_ge(c) >= need) t = c;
+  }
+  t |= (((Key)1 << S) - 1) & ~(((Key)1 << IB) - 1);
+  for (int b = IB - 1; b >= 0; --b) {
+    const Key c = t | ((Key)1 << b);
+    if (count_ge(c) >= need) t = c;
+  }
+  return t;
+}
+
+// Number of this wavefront's lanes whose key is >= c (c >= 1: lanes holding key 0 never count).
+template <typename Key>
+__device__ __forceinline__ int count_ge_lanes(Key v, Key c) {
+  return (int)__popcll(__builtin_amdgcn_ballot_w64(v >= c));
+}
+
+// rank of u among the n (a multiple of 4 not above kMaxKnn) keys of sel[]: how many are larger; 16-byte reads
+template <typename Key>
+__device__ __forceinline__ int rank_in(const Key *sel, int n, Key u) {
+  constexpr int PER = 16 / (int)sizeof(Key);
+  int rank = 0;
+  for (int j0 = 0; j0 < n; j0 += 2 * PER) {
+    const uint4 a = *(const uint4 *)(sel + j0), b = *(const uint4 *)(sel + j0 + PER);
+    const Key *ka = (const Key *)&a, *kb = (const Key *)&b;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) rank += (ka[e] > u) + (j0 + PER + e < n && kb[e] > u);
+  }
+  return rank;
+}
+
+// Exclusive prefix sum over the wavefront with DPP (shifts within 16-lane rows, then row broadcasts of lanes 15 and
+// 31), no LDS round trips; *total = the sum over all lanes.  All 64 lanes must be active.
 __device__ __forceinline__ int wave_exclusive_sum(int v, int *total) {
   int incl = v;
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int u = __shfl_up(incl, o, kWave);
-    if (lane_id() >= o) incl += u;
-  }
-  *total = __shfl(incl, kWave - 1, kWave);
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);   // row_shr:1
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);   // row_shr:2
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);   // row_shr:4
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);   // row_shr:8
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  *total = __builtin_amdgcn_readlane(incl, kWave - 1);
   return incl - v;
 }
 
@@ -126,45 +169,46 @@ __device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetc
     if (ge && pos < kMaxKnn) sel[pos] = u;
     S += (int)__popcll(m);
   }
+  if (lane >= knn && lane < 4) sel[lane] = 0;     // pad knn < 4 to whole 16-byte reads
   wave_lds_sync();
   if (lane < knn) {
     const Key u = sel[lane];
-    int rank = 0;
-    for (int j = 0; j < knn; ++j) rank += sel[j] > u;
-    out[rank] = u;
+    out[rank_in(sel, knn < 4 ? 4 : knn, u)] = u;
   }
   wave_lds_sync();
 }
 
 // Exact top-knn among C candidate keys in LDS, into out[] descending.
+// Exact top-knn among C candidate keys in LDS (keys of sub-key indices < 2^IB), into out[] descending.
 template <bool F32>
-__device__ void topk_of_candidates(int C, int knn, typename SelKey<F32>::T *cand, typename SelKey<F32>::T *sel,
-                                   typename SelKey<F32>::T *out) {
+__device__ __forceinline__ void topk_of_candidates(int C, int knn, int IB, typename SelKey<F32>::T *cand,
+                                                   typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
-  constexpr int kBits = F32 ? 64 : 32;
+  constexpr int kTop = F32 ? 64 : 32, kS = F32 ? 32 : 16;
   const int lane = lane_id();
   Key t;
-  if (C <= kRegCand * kWave) {
+  if (C <= kWave) {  // one key per lane (the common case)
+    const Key r0 = lane < C ? cand[lane] : (Key)0;
+    t = key_search<Key>(knn, kTop, kS, IB, [&](Key c) { return count_ge_lanes(r0, c); });
+  } else if (C <= kRegCand * kWave) {
     Key reg[kRegCand];
-    bool val[kRegCand];
 #pragma unroll
     for (int s = 0; s < kRegCand; ++s) {
       const int p = s * kWave + lane;
-      val[s] = p < C;
-      reg[s] = val[s] ? cand[p] : (Key)0;
+      reg[s] = p < C ? cand[p] : (Key)0;
     }
-    t = threshold_search<Key>(knn, kBits, [&](Key c) {
+    t = key_search<Key>(knn, kTop, kS, IB, [&](Key c) {
       int n = 0;
 #pragma unroll
-      for (int s = 0; s < kRegCand; ++s) n += (int)__popcll(ballot(val[s] && reg[s] >= c));
+      for (int s = 0; s < kRegCand; ++s) n += count_ge_lanes(reg[s], c);
       return n;
     });
   } else {
-    t = threshold_search<Key>(knn, kBits, [&](Key c) {
+    t = key_search<Key>(knn, kTop, kS, IB, [&](Key c) {
       int n = 0;
       for (int p0 = 0; p0 < C; p0 += kWave) {
         const int p = p0 + lane;
-        n += (int)__popcll(ballot(p < C && cand[p] >= c));
+        n += count_ge_lanes(p < C ? cand[p] : (Key)0, c);
       }
       return n;
     });
@@ -184,7 +228,7 @@ __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelK
     const Key u = half_key<F32>(row, k);
     mx = u > mx ? u : mx;
   }
-  const Key t0 = threshold_search<Key>(knn, kBits, [&](Key t) { return (int)__popcll(ballot(mx >= t)); });
+  const Key t0 = threshold_search<Key>(knn, kBits, [&](Key t) { return count_ge_lanes(mx, t); });
   int C = 0;
   for (int k0 = 0; k0 < NK; k0 += kWave) {
     const int k = k0 + lane;
@@ -197,14 +241,14 @@ __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelK
   }
   wave_lds_sync();
   if (C <= CAP) {
-    topk_of_candidates<F32>(C, knn, cand, sel, out);
+    topk_of_candidates<F32>(C, knn, 31 - __builtin_clz(NK), cand, sel, out);
     return;
   }
   const Key t1 = threshold_search<Key>(knn, kBits, [&](Key t) {
     int cnt = 0;
     for (int k0 = 0; k0 < NK; k0 += kWave) {
       const int k = k0 + lane;
-      cnt += (int)__popcll(ballot(k < NK && half_key<F32>(row, k) >= t));
+      cnt += count_ge_lanes(k < NK ? half_key<F32>(row, k) : (Key)0, t);
     }
     return cnt;
   });
@@ -230,12 +274,24 @@ __device__ __forceinline__ uint4 chunk_codes(uint4 v) {
   return uint4{d[0], d[1], d[2], d[3]};
 }
 
-// Register half top-k for NK = CPL * 64 chunks of 16 bytes (or fewer chunks, down to one).
+// Register half top-k for NK = CPL * 64 chunks of 16 bytes (or fewer chunks, down to one):
+//   1. the row into registers as order codes (lane l holds chunks l, l + 64, ...), with each chunk's largest code;
+//   2. code0 = the knn-th largest lane maximum: at least knn elements reach it (the top knn lanes hold one each);
+//   3. the chunks whose maximum reaches code0 (a few dozen) are staged in LDS, one per lane per round, so that
+//   4. each lane appends only its staged chunk's elements >= code0 to the candidate list (DPP prefix sum);
+//   5. the exact top knn of the candidates, in descending order.
+// The wavefront's CAP keys of LDS hold the candidates at the front and the staging area (16 bytes + chunk index
+// per lane) at the back; a row with more candidates than fit takes the streaming path.
 template <bool F32, int CPL, int CAP>
-__device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
+__device__ __forceinline__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
                               typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
   constexpr int EPC = F32 ? 4 : 8;  // elements per chunk
+  constexpr int kStageBytes = kWave * (16 + 4);
+  constexpr int kCandMax = (CAP * (int)sizeof(Key) - kStageBytes) / (int)sizeof(Key);
+  static_assert(kCandMax >= kMaxKnn, "candidate area too small");
+  uint4 *stage = (uint4 *)((char *)cand + CAP * sizeof(Key) - kStageBytes);
+  uint32_t *stage_id = (uint32_t *)(stage + kWave);
   const int lane = lane_id();
   const int nchunks = NK / EPC;
 
@@ -245,63 +301,129 @@ __device__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<
     const int c = lane + j * kWave;
     code[j] = c < nchunks ? ((const uint4 *)row)[c] : uint4{0u, 0u, 0u, 0u};
   }
+  uint32_t cmax[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const int c = lane + j * kWave;
     code[j] = c < nchunks ? chunk_codes<F32>(code[j]) : uint4{0u, 0u, 0u, 0u};  // invalid -> code 0 (minimum)
-  }
-
-  // lane maximum of the codes, then code0 = knn-th largest lane maximum
-  uint32_t mx;
-  if constexpr (F32) {
-    mx = 0;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) mx = max(max(max(mx, code[j].x), max(code[j].y, code[j].z)), code[j].w);
-  } else {
-    u16x2 pm = {0, 0};
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].x));
-      pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].y));
+    if constexpr (F32) {
+      cmax[j] = max(max(code[j].x, code[j].y), max(code[j].z, code[j].w));
+    } else {
+      u16x2 pm = __builtin_elementwise_max(__builtin_bit_cast(u16x2, code[j].x), __builtin_bit_cast(u16x2, code[j].y));
       pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].z));
       pm = __builtin_elementwise_max(pm, __builtin_bit_cast(u16x2, code[j].w));
+      cmax[j] = max((uint32_t)pm.x, (uint32_t)pm.y);
     }
-    mx = max((uint32_t)pm.x, (uint32_t)pm.y);
   }
+  uint32_t mx = 0;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) mx = max(mx, cmax[j]);
   const uint32_t code0 = threshold_search<uint32_t>(knn, F32 ? 32 : 16,
-                                                    [&](uint32_t t) { return (int)__popcll(ballot(mx >= t)); });
+                                                    [&](uint32_t t) { return count_ge_lanes(mx, t); });
 
-  // compact the elements with code >= code0 (valid ones only: code0 may be 0)
-  auto elem_code = [&](int j, int e) -> uint32_t {
-    const uint32_t d[4] = {code[j].x, code[j].y, code[j].z, code[j].w};
-    if constexpr (F32) return d[e];
-    else return (d[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-  };
-  int mine = 0;
+  // candidate chunks: per slot j a ballot, numbered slot by slot in lane order
+  uint64_t bm[CPL];
+  int base[CPL];
+  int Cc = 0;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    if (lane + j * kWave >= nchunks) continue;
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) mine += elem_code(j, e) >= code0;
+    bm[j] = ballot(lane + j * kWave < nchunks && cmax[j] >= code0);
+    base[j] = Cc;
+    Cc += (int)__popcll(bm[j]);
   }
-  int C;
-  int pos = wave_exclusive_sum(mine, &C);
-  if (C <= CAP) {
+  int C = 0;
+  for (int r0 = 0; r0 < Cc; r0 += kWave) {  // one round unless more than 64 chunks reach code0
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = lane + j * kWave;
-      if (c >= nchunks) continue;
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        const uint32_t cd = elem_code(j, e);
-        if (cd >= code0) cand[pos++] = make_key<F32>(cd, (uint32_t)(c * EPC + e));
+      const int p = base[j] + lanes_below(bm[j]) - r0;
+      if (((bm[j] >> lane) & 1) && p >= 0 && p < kWave) {
+        stage[p] = code[j];
+        stage_id[p] = (uint32_t)(lane + j * kWave);
       }
     }
     wave_lds_sync();
-    topk_of_candidates<F32>(C, knn, cand, sel, out);
+    const bool have = r0 + lane < Cc;
+    const uint4 v = have ? stage[lane] : uint4{0u, 0u, 0u, 0u};
+    const uint32_t cid = have ? stage_id[lane] : 0u;
+    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+    uint32_t ec[EPC];
+    int n = 0;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      if constexpr (F32) ec[e] = d[e];
+      else ec[e] = (d[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+      n += (have && ec[e] >= code0) ? 1 : 0;
+    }
+    int total;
+    int pos = C + wave_exclusive_sum(n, &total);
+    if (C + total <= kCandMax) {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e)
+        if (have && ec[e] >= code0) cand[pos++] = make_key<F32>(ec[e], cid * EPC + (uint32_t)e);
+    }
+    C += total;
+    wave_lds_sync();  // the staging area is rewritten by the next round
+  }
+  if (C <= kCandMax) {
+    topk_of_candidates<F32>(C, knn, 31 - __builtin_clz(NK), cand, sel, out);
   } else {
     half_topk_stream<F32, CAP>(row, NK, knn, cand, sel, out);
   }
+}
+
+// Cartesian step of one head, by one wavefront: candidates (i, j) with (i+1)(j+1) <= knn of the two halves'
+// descending top lists, scored dtype(v1[i] + v2[j]), top-knn by (score, lowest table index), softmax in fp32.
+// Lane j < knn ends with the j-th best pair: its score `sc` (code = order code of its bits), table index `full`
+// and weight `wt`.  pc: the lane's pairs from load_pairs; s_fsel, s_fin: kMaxKnn entries of LDS scratch.
+// Sum over the wavefront: DPP sums within each 16-lane row, then the four row totals.  All lanes active.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+template <bool F32, int SLOTS>
+__device__ __forceinline__ uint64_t cartesian_threshold(const typename SelKey<F32>::T *top1,
+                                                        const typename SelKey<F32>::T *top2, int NK, int knn,
+                                                        const uint32_t (&pc)[kMaxPairSlots], uint64_t *s_fsel) {
+  using Key = typename SelKey<F32>::T;
+  uint64_t ck[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    ck[s] = 0;  // no pair: key 0, never counted (every tested threshold is >= 1)
+    if (pc[s] != kNoPair) {
+      const Key k1 = top1[pc[s] & 0xFFu];
+      const Key k2 = top2[pc[s] >> 8];
+      const float sum = key_value<F32>(k1) + key_value<F32>(k2);
+      const uint32_t code = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
+      const uint32_t full = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
+      ck[s] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
+    }
+  }
+  // table indices are below NK^2 = 2^(2 log2 NK): the bits above them in the low word are set in every key
+  const int IB = 2 * (31 - __builtin_clz(NK));
+  const uint64_t t = key_search<uint64_t>(knn, F32 ? 64 : 48, 32, IB, [&](uint64_t c) {
+    int n = 0;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) n += count_ge_lanes(ck[s], c);
+    return n;
+  });
+  int S = 0;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const bool ge = ck[s] >= t;  // t >= 1: pair-less slots never qualify
+    const uint64_t m = __builtin_amdgcn_ballot_w64(ge);
+    const int pos = S + lanes_below(m);
+    if (ge && pos < kMaxKnn) s_fsel[pos] = ck[s];
+    S += (int)__popcll(m);
+  }
+  return t;
 }
 
 // Cartesian step of one head, by one wavefront: candidates (i, j) with (i+1)(j+1) <= knn of the two halves'
@@ -314,46 +436,16 @@ __device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *to
                                                const uint32_t (&pc)[kMaxPairSlots], uint64_t *s_fsel,
                                                uint64_t *s_fin, float &sc, uint32_t &full, uint32_t &code,
                                                float &wt) {
-  using Key = typename SelKey<F32>::T;
   const int lane = lane_id();
-  // Cartesian candidates (i, j) with (i+1)(j+1) <= knn (this lane's pairs pc), keys held in registers
-  uint64_t ck[kMaxPairSlots];
-  bool cv[kMaxPairSlots];
-#pragma unroll
-  for (int s = 0; s < kMaxPairSlots; ++s) {
-    cv[s] = pc[s] != kNoPair;
-    ck[s] = 0;
-    if (cv[s]) {
-      const Key k1 = top1[pc[s] & 0xFFu];
-      const Key k2 = top2[pc[s] >> 8];
-      const float sum = key_value<F32>(k1) + key_value<F32>(k2);
-      const uint32_t pc = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
-      const uint32_t pf = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
-      ck[s] = ((uint64_t)pc << 32) | (uint64_t)(0xFFFFFFFFu - pf);
-    }
-  }
-  const uint64_t t = threshold_search<uint64_t>(knn, F32 ? 64 : 48, [&](uint64_t c) {
-    int n = 0;
-#pragma unroll
-    for (int s = 0; s < kMaxPairSlots; ++s) n += (int)__popcll(ballot(cv[s] && ck[s] >= c));
-    return n;
-  });
-  int S = 0;
-#pragma unroll
-  for (int s = 0; s < kMaxPairSlots; ++s) {
-    const bool ge = cv[s] && ck[s] >= t;
-    const uint64_t m = ballot(ge);
-    const int pos = S + lanes_below(m);
-    if (ge && pos < kMaxKnn) s_fsel[pos] = ck[s];
-    S += (int)__popcll(m);
-  }
+  // pairs per knn: <= 50 (one slot of 64 lanes), 119 (two), 280 (five)
+  if (knn >= 64) cartesian_threshold<F32, 5>(top1, top2, NK, knn, pc, s_fsel);
+  else if (knn >= 32) cartesian_threshold<F32, 2>(top1, top2, NK, knn, pc, s_fsel);
+  else cartesian_threshold<F32, 1>(top1, top2, NK, knn, pc, s_fsel);
+  if (lane >= knn && lane < 2) s_fsel[lane] = 0;  // pad knn = 1 to a whole 16-byte read
   wave_lds_sync();
-  uint64_t mine = 0;
   if (lane < knn) {
-    mine = s_fsel[lane];
-    int rank = 0;
-    for (int j = 0; j < knn; ++j) rank += s_fsel[j] > mine;
-    s_fin[rank] = mine;
+    const uint64_t mine = s_fsel[lane];
+    s_fin[rank_in(s_fsel, knn < 2 ? 2 : knn, mine)] = mine;
   }
   wave_lds_sync();
 
@@ -366,10 +458,10 @@ __device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *to
     full = 0xFFFFFFFFu - (uint32_t)u;
     sc = F32 ? __uint_as_float(unorder32(code)) : bf16_bits_to_f32(unorder16(code));
   }
-  const float mxs = __shfl(sc, 0, kWave);  // descending: lane 0 holds the largest score
+  // descending: lane 0 holds the largest score
+  const float mxs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 0));
   const float e = lane < knn ? expf(sc - mxs) : 0.f;
-  const float sum = wave_sum(e);
-  wt = e / sum;
+  wt = e / wave_sum_dpp(e);
 }
 
 template <bool F32, int CPL>
@@ -377,11 +469,11 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
                                                      int NK, int knn, void *__restrict__ scores,
                                                      int64_t *__restrict__ idx, float *__restrict__ w) {
   using Key = typename SelKey<F32>::T;
-  __shared__ Key s_cand[2][kCap];
-  __shared__ Key s_sel[2][kMaxKnn];
-  __shared__ Key s_top[2][kMaxKnn];
-  __shared__ uint64_t s_fsel[kMaxKnn];
-  __shared__ uint64_t s_fin[kMaxKnn];
+  __shared__ __align__(16) Key s_cand[2][kCap];
+  __shared__ __align__(16) Key s_sel[2][kMaxKnn];
+  __shared__ __align__(16) Key s_top[2][kMaxKnn];
+  __shared__ __align__(16) uint64_t s_fsel[kMaxKnn];
+  __shared__ __align__(16) uint64_t s_fin[kMaxKnn];
 
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
@@ -431,7 +523,7 @@ void launch_select(const void *s1, const void *s2, int64_t rows, int NK, int knn
 // flight per thread, adds the slots through LDS (over the candidate buffers, no longer needed) and applies the bag
 // epilogue.  Same selection and the same bag additions in the same order as select_kernel followed by
 // bag_rows_kernel, so the results are bit-identical; it saves the launch and the round trip of the lookups.
-constexpr int kFusedCapBytes = 2048;   // LDS candidate bytes per half (512 bf16 / 256 fp32 keys)
+constexpr int kFusedCapBytes = 4096;   // LDS candidate + staging bytes per half (1024 bf16 / 512 fp32 keys)
 
 constexpr int kFusedMaxHeads = 4;       // 2H wavefronts per workgroup
 
