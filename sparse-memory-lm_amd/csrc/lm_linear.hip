@@ -15,10 +15,11 @@
 //             ARGMAX         per token, the largest key (bf16 logit, then lowest column) over the block's 128
 //                            columns, to partial[m, block] (lm_head + greedy argmax; no logits are written)
 //
-// Workgroup = 4 wavefronts, 64 tokens (blockIdx.y) x one column block (blockIdx.x).  STORE / SWIGLU: one 16-column
-// tile per workgroup (SWIGLU: the 16 a columns and their 16 b columns), the 4 wavefronts split the contraction and
-// their partial sums are added in a fixed order through LDS.  ARGMAX: each wavefront owns 2 tiles (32 columns) over
-// the whole contraction.  Every result is deterministic.
+// Workgroup = 4 wavefronts, a token group of 16 or 64 rows x one column block.  STORE / SWIGLU: one 16-column tile
+// per workgroup (SWIGLU: the 16 a columns and their 16 b columns), the 4 wavefronts split the contraction and their
+// partial sums are added in a fixed order through LDS.  ARGMAX: each wavefront owns 2 tiles (32 columns) over the
+// whole contraction.  Every result is deterministic.  With several token groups the grid is 1-D and the groups of
+// one column block share an XCD (workgroup id % 8), so its weight rows come from one L2.
 //
 // Latency is what matters at decode sizes, so every global load a lane needs is issued before the first one is
 // used: the weight fragments of the lane's K slice first (they do not depend on the prologue), then the prologue's
@@ -38,9 +39,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLinThreads = 256;
 constexpr int kLinWaves = kLinThreads / kWave;
-constexpr int kTokBlock = 64;     // tokens per workgroup (4 MFMA tiles)
-constexpr int kRowLanes = 16;     // lanes per prologue row
-constexpr int kMaxPasses = kTokBlock / (kLinWaves * (kWave / kRowLanes));  // 4 prologue passes of 16 rows
+constexpr int kMaxTiles = 4;      // token tiles of 16 per workgroup, at most
+constexpr int kXcds = 8;          // workgroup id % 8 selects the XCD
 constexpr int kArgTiles = 2;      // 16-column tiles per wavefront with the ARGMAX epilogue
 constexpr int kArgCols = kLinWaves * kArgTiles * 16;   // 128 columns per workgroup
 constexpr uint16_t kBf16NaN = 0x7FC0;
@@ -76,22 +76,22 @@ __device__ __forceinline__ float row16_sum(float v) {
 // Prologue: the workgroup's rows [0, nrows) normalised into sH (bf16, row stride KP), rows [nrows, pad_rows) zero.
 // Row rr = pass * 16 + wave * 4 + quarter is handled by the 16 lanes of one quarter wavefront; lane `sub` of it owns
 // the 16-byte chunks sub, sub + 16, ... (CPQ of them, K <= 128 * CPQ).
-template <int PRO, int CPQ>
+template <int PRO, int CPQ, int MTB>
 __device__ __forceinline__ void build_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
-                                                  uint16_t *sH, int KP) {
+                                                  uint16_t *sH, int KP, bool first_block) {
   const int K = a.K, CH = K / 8;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int quarter = lane >> 4, sub = lane & 15;
   const int passes = pad_rows / 16;
-  const bool write_x = a.x_out != nullptr && blockIdx.x == 0;
+  const bool write_x = a.x_out != nullptr && first_block;
   const uint16_t *nw = (const uint16_t *)a.norm_w;
 
-  uint4 xv[kMaxPasses][CPQ], dv[kMaxPasses][CPQ], gv[CPQ];
-  bool bad[kMaxPasses];
+  uint4 xv[MTB][CPQ], dv[MTB][CPQ], gv[CPQ];
+  bool bad[MTB];
 #pragma unroll
   for (int j = 0; j < CPQ; ++j) gv[j] = *(const uint4 *)(nw + min(sub + 16 * j, CH - 1) * 8);
 #pragma unroll
-  for (int p = 0; p < kMaxPasses; ++p) {
+  for (int p = 0; p < MTB; ++p) {
     bad[p] = false;
     if (p >= passes) continue;                      // wavefront-uniform
     const int rr = p * 16 + wave * 4 + quarter;
@@ -116,7 +116,7 @@ __device__ __forceinline__ void build_activations(const smlm_linear_args &a, int
   }
 
 #pragma unroll
-  for (int p = 0; p < kMaxPasses; ++p) {
+  for (int p = 0; p < MTB; ++p) {
     if (p >= passes) continue;
     const int rr = p * 16 + wave * 4 + quarter;
     const bool live = rr < nrows;
@@ -168,9 +168,9 @@ __device__ __forceinline__ void build_activations(const smlm_linear_args &a, int
 }
 
 // PRO / EPI: prologue and epilogue; MAXS: k-steps of 32 per wavefront held in registers (>= its K slice);
-// CPQ: prologue chunks per lane.
-template <int PRO, int EPI, int MAXS, int CPQ>
-__global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_args a) {
+// CPQ: prologue chunks per lane; MTB: token tiles of 16 per workgroup.  ncb column blocks x ntg token groups.
+template <int PRO, int EPI, int MAXS, int CPQ, int MTB>
+__global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_args a, int ncb, int ntg) {
   constexpr bool ARG = EPI == SMLM_LIN_ARGMAX;
   constexpr int KS = ARG ? 1 : kLinWaves;               // wavefronts along the contraction
   constexpr int NT = EPI == SMLM_LIN_STORE ? 1 : 2;     // weight tiles per wavefront
@@ -178,8 +178,16 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int K = a.K, KP = K + 8;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t m0 = (int64_t)blockIdx.y * kTokBlock;
-  const int nrows = (int)min((int64_t)kTokBlock, a.M - m0);
+  constexpr int TB = MTB * 16;
+  int cb = (int)blockIdx.x, tg = 0;
+  if (ntg > 1) {  // id = ((cb / 8) * ntg + tg) * 8 + cb % 8: the token groups of a column block on one XCD
+    const int q = (int)blockIdx.x / kXcds;
+    cb = q / ntg * kXcds + (int)blockIdx.x % kXcds;
+    tg = q % ntg;
+    if (cb >= ncb) return;                          // padding of the last XCD round: the whole workgroup leaves
+  }
+  const int64_t m0 = (int64_t)tg * TB;
+  const int nrows = (int)min((int64_t)TB, a.M - m0);
   const int MT = (nrows + 15) / 16;
   uint16_t *sH = (uint16_t *)smem;
 
@@ -188,7 +196,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int nsteps = K / 32;
   const int s_lo = ks * nsteps / KS, ns = (ks + 1) * nsteps / KS - s_lo;
   const int cols = EPI == SMLM_LIN_SWIGLU ? a.N / 2 : a.N;                   // output columns
-  const int col0 = ARG ? blockIdx.x * kArgCols + wave * kArgTiles * 16 : blockIdx.x * 16;
+  const int col0 = ARG ? cb * kArgCols + wave * kArgTiles * 16 : cb * 16;
   const uint16_t *W = (const uint16_t *)a.w;
 
   // 1. weight fragments (rows past N and steps past the slice re-read valid memory; their products are unused)
@@ -206,10 +214,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   }
 
   // 2. activations: PLAIN rows straight into registers; otherwise the prologue into LDS
-  uint4 breg[4][PRO == SMLM_LIN_PLAIN ? MAXS : 1];
+  uint4 breg[MTB][PRO == SMLM_LIN_PLAIN ? MAXS : 1];
   if constexpr (PRO == SMLM_LIN_PLAIN) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTB; ++mt) {
       if (mt >= MT) continue;                       // wavefront-uniform
       const int tok = min(mt * 16 + r, nrows - 1);
       const uint16_t *xp = (const uint16_t *)a.x + (m0 + tok) * a.x_stride + g * 8;
@@ -220,22 +228,22 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       }
     }
   } else {
-    build_activations<PRO, CPQ>(a, m0, nrows, MT * 16, sH, KP);
+    build_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0);
     __syncthreads();
   }
 
   // 3. products
-  floatx4 acc[NT][4];
+  floatx4 acc[NT][MTB];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[t][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MTB; ++mt) acc[t][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < MAXS; ++s) {
     if (s >= ns) continue;                          // wavefront-uniform
     const int k = (s_lo + s) * 32 + g * 8;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTB; ++mt) {
       if (mt >= MT) continue;
       uint4 b;
       if constexpr (PRO == SMLM_LIN_PLAIN) b = breg[mt][s];
@@ -256,8 +264,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          if (mt < MT) sRed[(((ks - 1) * NT + t) * 4 + mt) * kWave + lane] = acc[t][mt];
+        for (int mt = 0; mt < MTB; ++mt)
+          if (mt < MT) sRed[(((ks - 1) * NT + t) * MTB + mt) * kWave + lane] = acc[t][mt];
     }
     __syncthreads();
     if (ks > 0) return;
@@ -266,8 +274,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          if (mt < MT) acc[t][mt] += sRed[(((k2 - 1) * NT + t) * 4 + mt) * kWave + lane];
+        for (int mt = 0; mt < MTB; ++mt)
+          if (mt < MT) acc[t][mt] += sRed[(((k2 - 1) * NT + t) * MTB + mt) * kWave + lane];
   }
 
   const int c = col0 + 4 * g;  // this lane's 4 columns c .. c+3 of tile 0 (cols % 16 == 0: all in or all out)
@@ -287,7 +295,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
     uint16_t *dst = first ? (uint16_t *)a.out + c : (uint16_t *)a.out2 + (c - a.n_split);
     const int64_t stride = first ? a.out_stride : a.out2_stride;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTB; ++mt) {
       const int tok = mt * 16 + r;
       if (mt >= MT || tok >= nrows) continue;
       uint32_t o[4];
@@ -302,7 +310,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   } else if constexpr (EPI == SMLM_LIN_SWIGLU) {
     if (c >= cols) return;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTB; ++mt) {
       const int tok = mt * 16 + r;
       if (mt >= MT || tok >= nrows) continue;
       uint32_t o[4];
@@ -312,10 +320,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       *(uint2 *)((uint16_t *)a.out + (m0 + tok) * a.out_stride + c) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
     }
   } else {  // ARGMAX
-    uint64_t *sArg = (uint64_t *)smem;  // [4 wavefronts][64 tokens]
+    uint64_t *sArg = (uint64_t *)smem;  // [4 wavefronts][TB tokens]
     if constexpr (PRO != SMLM_LIN_PLAIN) __syncthreads();  // activations no longer read
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MTB; ++mt) {
       if (mt >= MT) continue;
       uint64_t best = 0;
 #pragma unroll
@@ -333,14 +341,14 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
         const uint64_t other = __shfl_xor(best, o, kWave);
         best = other > best ? other : best;
       }
-      if (g == 0) sArg[wave * kTokBlock + mt * 16 + r] = best;
+      if (g == 0) sArg[wave * TB + mt * 16 + r] = best;
     }
     __syncthreads();
     if (tid < nrows) {
       uint64_t best = sArg[tid];
 #pragma unroll
-      for (int w2 = 1; w2 < kLinWaves; ++w2) best = sArg[w2 * kTokBlock + tid] > best ? sArg[w2 * kTokBlock + tid] : best;
-      a.partial[(m0 + tid) * a.partial_stride + blockIdx.x] = best;
+      for (int w2 = 1; w2 < kLinWaves; ++w2) best = sArg[w2 * TB + tid] > best ? sArg[w2 * TB + tid] : best;
+      a.partial[(m0 + tid) * a.partial_stride + cb] = best;
     }
   }
 }
@@ -395,27 +403,42 @@ __global__ void __launch_bounds__(kFinishThreads)
   if (advance && threadIdx.x == 0) *pos = P + 1;
 }
 
-template <int PRO, int EPI, int MAXS>
-void launch_linear_cpq(const smlm_linear_args &a, dim3 grid, size_t shmem, hipStream_t stream) {
+// Launch geometry: ncb column blocks x ntg token groups of mtb tiles.
+struct LinGrid {
+  int ncb, ntg, mtb;
+  dim3 grid;
+  size_t shmem;
+};
+
+template <int PRO, int EPI, int MAXS, int MTB>
+void launch_linear_mtb(const smlm_linear_args &a, const LinGrid &lg, hipStream_t stream) {
   if (PRO == SMLM_LIN_PLAIN || a.K <= 384)
-    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 3>), grid, dim3(kLinThreads), shmem, stream, a);
+    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 3, MTB>), lg.grid, dim3(kLinThreads), lg.shmem, stream, a,
+                       lg.ncb, lg.ntg);
   else
-    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 4>), grid, dim3(kLinThreads), shmem, stream, a);
+    hipLaunchKernelGGL((linear_kernel<PRO, EPI, MAXS, 4, MTB>), lg.grid, dim3(kLinThreads), lg.shmem, stream, a,
+                       lg.ncb, lg.ntg);
+}
+
+template <int PRO, int EPI, int MAXS>
+void launch_linear_cpq(const smlm_linear_args &a, const LinGrid &lg, hipStream_t stream) {
+  if (lg.mtb == 1) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);
+  else launch_linear_mtb<PRO, EPI, MAXS, kMaxTiles>(a, lg, stream);
 }
 
 template <int PRO>
-void launch_linear_pro(const smlm_linear_args &a, dim3 grid, size_t shmem, hipStream_t stream) {
+void launch_linear_pro(const smlm_linear_args &a, const LinGrid &grid, hipStream_t stream) {
   const int steps = a.K / 32;
   if (a.epilogue == SMLM_LIN_ARGMAX) {
-    if (steps <= 12) launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 12>(a, grid, shmem, stream);
-    else launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 16>(a, grid, shmem, stream);
+    if (steps <= 12) launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 12>(a, grid, stream);
+    else launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 16>(a, grid, stream);
     return;
   }
   const int per_wave = (steps + kLinWaves - 1) / kLinWaves;
 #define SMLM_LIN_MAXS(EPI)                                                               \
-  if (per_wave <= 4) launch_linear_cpq<PRO, EPI, 4>(a, grid, shmem, stream);             \
-  else if (PRO == SMLM_LIN_PLAIN && per_wave <= 8) launch_linear_cpq<PRO, EPI, 8>(a, grid, shmem, stream); \
-  else launch_linear_cpq<PRO, EPI, 16>(a, grid, shmem, stream);
+  if (per_wave <= 4) launch_linear_cpq<PRO, EPI, 4>(a, grid, stream);                     \
+  else if (PRO == SMLM_LIN_PLAIN && per_wave <= 8) launch_linear_cpq<PRO, EPI, 8>(a, grid, stream); \
+  else launch_linear_cpq<PRO, EPI, 16>(a, grid, stream);
   if (a.epilogue == SMLM_LIN_STORE) {
     SMLM_LIN_MAXS(SMLM_LIN_STORE)
   } else {
@@ -441,7 +464,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   if (epi != SMLM_LIN_STORE && epi != SMLM_LIN_SWIGLU && epi != SMLM_LIN_ARGMAX)
     return fail(SMLM_EINVAL, "smlm_decode_linear: unknown epilogue %d", epi);
   if (!A.w) return fail(SMLM_EINVAL, "smlm_decode_linear: null weight");
-  if (A.M < 0 || A.M > 65535LL * kTokBlock || A.K < 32 || A.K % 32 || A.N < 16 || A.N % 16)
+  if (A.M < 0 || A.M > (1LL << 20) || A.K < 32 || A.K % 32 || A.N < 16 || A.N % 16)
     return fail(SMLM_EINVAL, "smlm_decode_linear: bad shape M=%lld N=%d K=%d (K and N multiples of 32 and 16)",
                 (long long)A.M, A.N, A.K);
   if (epi == SMLM_LIN_SWIGLU && A.N % 32)
@@ -486,17 +509,29 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
                   smlm_linear_argmax_blocks(A.N));
   }
   if (A.M == 0) return SMLM_OK;
+  // 16-token groups (more workgroups, shorter per-workgroup chains: decode is latency-bound), except the ARGMAX
+  // epilogue over more than 16 rows, whose 128-column blocks already fill the chip
+  LinGrid lg;
+  lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
+  const int tb = lg.mtb * 16;
   const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
-  const dim3 grid((unsigned)((cols + cols_per_block - 1) / cols_per_block), (unsigned)((A.M + kTokBlock - 1) / kTokBlock));
-  const int pad_rows = (int)(((A.M < kTokBlock ? A.M : kTokBlock) + 15) / 16 * 16);
+  lg.ncb = (cols + cols_per_block - 1) / cols_per_block;
+  lg.ntg = (int)((A.M + tb - 1) / tb);
+  const int64_t nwg = lg.ntg == 1 ? lg.ncb : (int64_t)(lg.ncb + kXcds - 1) / kXcds * kXcds * lg.ntg;
+  if (nwg > 0x7FFFFFFFLL)
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_linear: M=%lld x N=%d needs more workgroups than one launch holds",
+                (long long)A.M, A.N);
+  lg.grid = dim3((unsigned)nwg);
+  const int pad_rows = (int)(((A.M < tb ? A.M : tb) + 15) / 16 * 16);
   const size_t act = pro != SMLM_LIN_PLAIN ? (size_t)pad_rows * (A.K + 8) * 2 : 0;
-  const size_t red = epi == SMLM_LIN_ARGMAX ? (size_t)kLinWaves * kTokBlock * 8
-                                            : (size_t)(kLinWaves - 1) * (epi == SMLM_LIN_SWIGLU ? 2 : 1) * 4 * kWave * 16;
-  const size_t shmem = act > red ? act : red;
+  const size_t red = epi == SMLM_LIN_ARGMAX
+                         ? (size_t)kLinWaves * tb * 8
+                         : (size_t)(kLinWaves - 1) * (epi == SMLM_LIN_SWIGLU ? 2 : 1) * lg.mtb * kWave * 16;
+  lg.shmem = act > red ? act : red;
   hipStream_t s = (hipStream_t)stream;
-  if (pro == SMLM_LIN_PLAIN) launch_linear_pro<SMLM_LIN_PLAIN>(A, grid, shmem, s);
-  else if (pro == SMLM_LIN_RMSNORM) launch_linear_pro<SMLM_LIN_RMSNORM>(A, grid, shmem, s);
-  else launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, grid, shmem, s);
+  if (pro == SMLM_LIN_PLAIN) launch_linear_pro<SMLM_LIN_PLAIN>(A, lg, s);
+  else if (pro == SMLM_LIN_RMSNORM) launch_linear_pro<SMLM_LIN_RMSNORM>(A, lg, s);
+  else launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, lg, s);
   return launch_status("smlm_decode_linear");
 }
 

@@ -19,6 +19,14 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// 16 bytes at p (always a valid address: callers clamp row indices into range), or zeros if !ok.  Selecting the
+// loaded value rather than the address keeps the load a plain global load (a select between a global pointer and
+// a local zero turns it into a flat load with the zero in scratch memory).
+__device__ __forceinline__ uint4 load16_or_zero(const void *p, bool ok) {
+  const uint4 v = *(const uint4 *)p;
+  return ok ? v : uint4{0u, 0u, 0u, 0u};
+}
+
 template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
     score_kernel(const void *__restrict__ q, int64_t q_stride, const void *__restrict__ keys, int N, int H, int NK,
@@ -43,7 +51,6 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const uint4 zero = {0u, 0u, 0u, 0u};
   for (int k0 = 0; k0 < half; k0 += KSTEP) {
     const int kk = k0 + g * EPL;
     const bool kin = kk < half;  // half % EPL == 0: a lane's group is entirely inside or outside
@@ -51,12 +58,12 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
       const int key = key0 + i * 16 + r;
-      a[i] = (kin && key < NK) ? *(const uint4 *)(kbase + ((int64_t)key * half + kk) * ESZ) : zero;
+      a[i] = load16_or_zero(kbase + ((int64_t)min(key, NK - 1) * half + (kin ? kk : 0)) * ESZ, kin && key < NK);
     }
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int tok = tok0 + j * 16 + r;
-      b[j] = (kin && tok < N) ? *(const uint4 *)(qbase + ((int64_t)tok * q_stride + kk) * ESZ) : zero;
+      b[j] = load16_or_zero(qbase + ((int64_t)min(tok, N - 1) * q_stride + (kin ? kk : 0)) * ESZ, kin && tok < N);
     }
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -133,7 +140,6 @@ __global__ void __launch_bounds__(256)
   const int key0 = (t % key_tiles) * BM, tok0 = ((t / key_tiles) % tok_tiles) * BN;
   const uint16_t *kbase = keys + (int64_t)(h * 2 + p) * NK * half;
   const uint16_t *qbase = q + (int64_t)h * 2 * half + (int64_t)p * half;
-  const uint4 zero = {0u, 0u, 0u, 0u};
 
   floatx4 acc[WM][WN];
 #pragma unroll
@@ -149,10 +155,11 @@ __global__ void __launch_bounds__(256)
   {                                                                                                         \
     const int kk = (k0) + pc0;                                                                              \
     const bool kin = kk < half;                                                                             \
-    a0 = (kin && key0 + pr0 < NK) ? *(const uint4 *)(kbase + (int64_t)(key0 + pr0) * half + kk) : zero;    \
-    a1 = (kin && key0 + pr1 < NK) ? *(const uint4 *)(kbase + (int64_t)(key0 + pr1) * half + kk) : zero;    \
-    b0 = (kin && tok0 + pr0 < N) ? *(const uint4 *)(qbase + (int64_t)(tok0 + pr0) * q_stride + kk) : zero; \
-    b1 = (kin && tok0 + pr1 < N) ? *(const uint4 *)(qbase + (int64_t)(tok0 + pr1) * q_stride + kk) : zero; \
+    const int kc = kin ? kk : 0;                                                                            \
+    a0 = load16_or_zero(kbase + (int64_t)min(key0 + pr0, NK - 1) * half + kc, kin && key0 + pr0 < NK);     \
+    a1 = load16_or_zero(kbase + (int64_t)min(key0 + pr1, NK - 1) * half + kc, kin && key0 + pr1 < NK);     \
+    b0 = load16_or_zero(qbase + (int64_t)min(tok0 + pr0, N - 1) * q_stride + kc, kin && tok0 + pr0 < N);   \
+    b1 = load16_or_zero(qbase + (int64_t)min(tok0 + pr1, N - 1) * q_stride + kc, kin && tok0 + pr1 < N);   \
   }
 #define SMLM_STAGE(s)                                                                                       \
   {                                                                                                         \
@@ -220,6 +227,136 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// bf16, many tokens: query-stationary streaming.  A workgroup = 4 wavefronts = 256 tokens of one (head, half).
+// Wavefront w keeps the query fragments of its 64 tokens for the whole contraction in registers (half / 32 steps x
+// 4 token tiles), and the workgroup streams the sub-keys through LDS in blocks of 64 rows, double-buffered: while
+// the 16 x (half / 32) MFMAs of block b run, block b + 1 is in flight from memory into registers, written to the
+// other LDS buffer afterwards (one barrier per block).  Every A fragment read from LDS feeds 4 MFMAs (LDS traffic
+// half of its bandwidth at full MFMA rate), and the 64 x 64 scores of a block go straight from the accumulators to
+// memory (4 consecutive sub-keys = one 8-byte store per lane).  LDS rows are padded by 16 bytes so that the 16 rows
+// one fragment read touches fall on distinct banks.  1-D grid: workgroup i serves (head, half) z = i % 2H and runs
+// on XCD i % 8, so with 2H dividing 8 every XCD reads one sub-key set only (1 MB at NK 2048) and keeps it in its L2.
+// The sums run over the 32-dim steps in the same order as score_lds_kernel, so the bits are the same.
+constexpr int kStreamKeys = 64;     // sub-keys per streamed block
+constexpr int kStreamWaveTok = 64;  // tokens per wavefront
+
+// Two fp32 values as packed bf16, rounded to nearest even (one v_cvt_pk_bf16_f32 on gfx950; for finite values the
+// same bits as bf16_bits_rtne).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <int KSTEPS, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64)
+    score_stream_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
+                        int H, int NK, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
+  constexpr int NT = WAVES * 64;            // threads
+  constexpr int HALF = KSTEPS * 32;
+  constexpr int RS = HALF + 8;              // LDS row stride (bf16)
+  constexpr int PPR = HALF / 8;             // 16-byte pieces per sub-key row
+  constexpr int PPT = kStreamKeys * PPR / NT;   // pieces per thread per block
+  constexpr int ROWS_PER_PASS = NT / PPR;
+  static_assert(PPT >= 1 && kStreamKeys * PPR % NT == 0, "block pieces must split evenly over the threads");
+  __shared__ __align__(16) uint16_t sA[2][kStreamKeys * RS];
+  const int Z = 2 * H;
+  const int z = (int)(blockIdx.x % Z), tile = (int)(blockIdx.x / Z);
+  const int h = z >> 1, p = z & 1;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const int r = lane & 15, g = lane >> 4;
+  const int tok0 = tile * (WAVES * kStreamWaveTok) + wave * kStreamWaveTok;
+  const uint16_t *kbase = keys + (int64_t)z * NK * HALF;
+  const uint16_t *qbase = q + (int64_t)h * 2 * HALF + (int64_t)p * HALF;
+  uint16_t *out = p ? s2 : s1;
+  const bool all_tok = tok0 + kStreamWaveTok <= N;   // wavefront-uniform: no token guards needed
+
+  bf16x8 bq[4][KSTEPS];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tok = tok0 + j * 16 + r;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s)
+      bq[j][s] = __builtin_bit_cast(
+          bf16x8, load16_or_zero(qbase + (int64_t)min(tok, N - 1) * q_stride + s * 32 + g * 8, tok < N));
+  }
+
+  // this thread's pieces of a block: rows prow + ROWS_PER_PASS * i, 16-byte column pcol
+  const int prow = tid / PPR, pcol = (tid % PPR) * 8;
+  const int nkb = (NK + kStreamKeys - 1) / kStreamKeys;
+  const int nfull = NK / kStreamKeys;       // blocks with all 64 sub-keys present
+  uint4 stage[PPT];
+#define SMLM_STREAM_FETCH(kb)                                                                                    \
+  if ((kb) < nfull) {                                                                                           \
+    const uint16_t *src = kbase + ((int64_t)(kb) * kStreamKeys + prow) * HALF + pcol;                          \
+    _Pragma("unroll") for (int i = 0; i < PPT; ++i) stage[i] = *(const uint4 *)(src + ROWS_PER_PASS * i * HALF); \
+  } else {                                                                                                      \
+    _Pragma("unroll") for (int i = 0; i < PPT; ++i) {                                                           \
+      const int key = (kb) * kStreamKeys + prow + ROWS_PER_PASS * i;                                            \
+      stage[i] = load16_or_zero(kbase + (int64_t)min(key, NK - 1) * HALF + pcol, key < NK);                    \
+    }                                                                                                           \
+  }
+#define SMLM_STREAM_PUT(buf)                                                                                     \
+  _Pragma("unroll") for (int i = 0; i < PPT; ++i)                                                               \
+      *(uint4 *)&sA[(buf)][(prow + ROWS_PER_PASS * i) * RS + pcol] = stage[i];
+
+  SMLM_STREAM_FETCH(0)
+  SMLM_STREAM_PUT(0)
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    // 1. the next block in flight; 2. this block's products; 3. the next block into the other buffer;
+    // 4. this block's scores out (their stores drain during the next block's products)
+    if (kb + 1 < nkb) {
+      SMLM_STREAM_FETCH(kb + 1)
+    }
+    const uint16_t *A = sA[kb & 1];
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      bf16x8 a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8 *)&A[(i * 16 + r) * RS + s * 32 + g * 8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bq[j][s], acc[i][j], 0, 0, 0);
+    }
+    if (kb + 1 < nkb) {
+      SMLM_STREAM_PUT((kb + 1) & 1)
+    }
+    const int key0 = kb * kStreamKeys + g * 4;
+    if (all_tok && kb < nfull) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t *orow = out + ((int64_t)(tok0 + j * 16 + r) * H + h) * NK + key0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *(uint2 *)(orow + i * 16) = uint2{pack_bf16x2(acc[i][j][0], acc[i][j][1]),
+                                            pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = tok0 + j * 16 + r;
+        uint16_t *orow = out + ((int64_t)tok * H + h) * NK + key0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tok < N && key0 + i * 16 < NK)
+            *(uint2 *)(orow + i * 16) = uint2{pack_bf16x2(acc[i][j][0], acc[i][j][1]),
+                                              pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+      }
+    }
+    __syncthreads();
+  }
+#undef SMLM_STREAM_FETCH
+#undef SMLM_STREAM_PUT
+}
+
 template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N>
 void launch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                   void *s2, hipStream_t stream) {
@@ -237,6 +374,17 @@ void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N
   } else if (F32 || N <= 64 || (N / 128 + 1) * (NK / 128 + 1) * 2 * (int64_t)H >= (1LL << 30)) {
     // 128 sub-keys x 64 tokens per workgroup, operands straight from memory
     launch_score<F32, 4, 2, 2, 2>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
+  } else if (!F32 && (half == 64 || half == 128 || half == 256) && NK % 4 == 0 && N >= 256) {
+    // bf16, many tokens: query-stationary streaming of the sub-keys
+    const int64_t tiles = (N + 255) / 256;
+    const dim3 grid((unsigned)(tiles * 2 * H));
+#define SMLM_STREAM(KS)                                                                                       \
+  hipLaunchKernelGGL((score_stream_kernel<KS, 4>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,  \
+                     (const uint16_t *)keys, (int)N, H, NK, (uint16_t *)s1, (uint16_t *)s2)
+    if (half == 256) SMLM_STREAM(8);
+    else if (half == 128) SMLM_STREAM(4);
+    else SMLM_STREAM(2);
+#undef SMLM_STREAM
   } else {        // bf16, many tokens: LDS-staged 128 x 128 tiles
     constexpr int BM = 128, BN = 128;
     const int64_t tiles = ((NK + BM - 1) / BM) * ((N + BN - 1) / BN) * 2 * (int64_t)H;
