@@ -67,7 +67,8 @@ def build_lm(cfg, dev, seed=0):
 
 
 def time_decode(model, B, steps, warmup, dev, seed=1, prompt_len=128):
-    """Prefill B uniform prompts of prompt_len tokens, run `warmup` graph steps, then time `steps` graph replays."""
+    """Prefill B uniform prompts of prompt_len tokens, run `warmup` graph steps, then time `steps` decode steps
+    (graph replays of the decoder's multi-step runs)."""
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
     P = prompt_len
@@ -80,12 +81,10 @@ def time_decode(model, B, steps, warmup, dev, seed=1, prompt_len=128):
         dec.hist[:, P] = logits[:, -1].argmax(-1)
         dec.tok.copy_(dec.hist[:, P:P + 1])
         dec.pos.fill_(P)
-        for _ in range(warmup):
-            dec.graph.replay()
+        dec.replay(warmup)
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
-        for _ in range(steps):
-            dec.graph.replay()
+        dec.replay(steps)
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0
     return B * steps / dt, 1000.0 * dt / steps

@@ -333,7 +333,8 @@ class Transformer(nn.Module):
     def generate(self, prompt, new_tokens, use_graph=True, sync_every_step=False):
         """Greedy decoding: prefill `prompt` (B, P) into a static KV cache, then `new_tokens` single-token
         steps, each one forward + argmax (the loop of smlm/train.py:283-301).  With use_graph the whole step
-        (embedding, every block, lm_head, argmax, cache write, position update) is one HIP graph replay.
+        (embedding, every block, lm_head, argmax, cache write, position update) is captured in a HIP graph, and
+        runs of _StepDecoder.steps_per_graph steps are one replay each.
         Returns the generated ids (B, new_tokens + 1): the prompt's next token, then one per step."""
         B, P = prompt.shape
         dec = self._decoder(B, P + new_tokens + 1, prompt.device)
@@ -454,7 +455,11 @@ class _FusedDecodeStep:
 
 
 class _StepDecoder:
-    """Static buffers and the captured graph of one decode step for batch B, sequences up to max_len."""
+    """Static buffers and the captured graphs of one decode step and of `steps_per_graph` steps in a row for batch
+    B, sequences up to max_len.  A step reads its position and token from device memory and advances them itself,
+    so a run of steps is one graph replay: the replay boundary (about 15 us on MI355X) is paid once per run."""
+
+    steps_per_graph = 8
 
     def __init__(self, model, B, max_len, device):
         cfg = model.cfg
@@ -470,6 +475,7 @@ class _StepDecoder:
         self.pos = torch.zeros((), dtype=torch.long, device=device)
         self.hist = torch.zeros(B, max_len, dtype=torch.long, device=device)
         self.graph = None
+        self.graph_run = None
         self.fused = _FusedDecodeStep(model) if _FusedDecodeStep.supported(model, dtype) else None
 
     def _step(self):
@@ -502,6 +508,22 @@ class _StepDecoder:
         with torch.cuda.graph(graph), ctx:
             self._step()
         self.graph = graph
+        if self.steps_per_graph > 1:
+            run = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(run), ctx:
+                for _ in range(self.steps_per_graph):
+                    self._step()
+            self.graph_run = run
+
+    def replay(self, n):
+        """n decode steps as graph replays: runs of steps_per_graph, then single steps."""
+        if self.graph is None:
+            self._capture()
+        k = self.steps_per_graph if self.graph_run is not None else 1
+        for _ in range(n // k):
+            (self.graph_run if k > 1 else self.graph).replay()
+        for _ in range(n - n // k * k):
+            self.graph.replay()
 
     def run(self, prompt, new_tokens, use_graph, sync_every_step):
         B, P = prompt.shape
@@ -512,6 +534,9 @@ class _StepDecoder:
         self.hist[:, P] = logits[:, -1].argmax(-1)
         self.tok.copy_(self.hist[:, P:P + 1])
         self.pos.fill_(P)
+        if use_graph and not sync_every_step:
+            self.replay(new_tokens)
+            return self.hist[:, P:P + new_tokens + 1].clone()
         for _ in range(new_tokens):
             if use_graph:
                 self.graph.replay()

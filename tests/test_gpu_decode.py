@@ -293,6 +293,24 @@ def test_fused_step_logits_match_generic_step():
 
 
 @torch.no_grad()
+def test_fused_generate_multi_step_graph_matches_eager():
+    """generate() on the fused step: the graph of steps_per_graph steps in a row plus single-step replays (19
+    tokens = 2 runs of 8 + 3 single steps) gives the eager loop's tokens exactly, on every call."""
+    from smlm_hip.model import ModelConfig, Transformer, _StepDecoder
+    cfg = ModelConfig(vocab_size=1024, d_model=384, n_layers=3, n_heads=6, ffn_hidden=1024, max_seq_len=64)
+    torch.manual_seed(1)
+    m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
+    assert _StepDecoder.steps_per_graph == 8
+    prompt = torch.randint(0, 1024, (2, 9), generator=torch.Generator().manual_seed(5)).to(DEV)
+    note("fused generate multi-step graph B=2")
+    eager = m.generate(prompt, 19, use_graph=False)
+    graph = m.generate(prompt, 19, use_graph=True)
+    graph2 = m.generate(prompt, 19, use_graph=True)
+    assert eager.shape == (2, 20)
+    assert torch.equal(graph, eager) and torch.equal(graph2, eager)
+
+
+@torch.no_grad()
 def test_fused_step_with_memory_layer_matches_torch_path():
     """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its selection is
     bit-exact against the oracle on the step's own sub-key scores, and its logits are within 1e-2 of the fp32
