@@ -173,7 +173,7 @@ int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float
  *            SMLM_LIN_SWIGLU         out[:, j] = bf16(bf16(silu(a_j)) * b_j), a_j = bf16(acc_j), b_j = bf16(acc_{N/2+j})
  *                                    (w13 followed by the SwiGLU activation, smlm/model.py:110-118)
  *            SMLM_LIN_ARGMAX         no logits are written: partial[m, b] = the largest (order16(bf16 logit) << 32 |
- *                                    ~column) over column block b of smlm_linear_argmax_blocks(N) blocks of 64;
+ *                                    ~column) over column block b of smlm_linear_argmax_blocks(N) blocks of 128;
  *                                    smlm_argmax_finish turns them into tokens (lm_head + greedy argmax)
  * Shapes: W (N, K) bf16 row-major (nn.Linear.weight), K a multiple of 32, N a multiple of 16 (SWIGLU: 32);
  * RMSNorm prologues need K <= 480; x rows at x + m*x_stride; delta, x_out (M, K) dense; bias (N,) bf16;
@@ -221,7 +221,7 @@ typedef struct smlm_linear_args {
   int64_t partial_stride;
 } smlm_linear_args;
 
-/* Number of 64-column blocks of the ARGMAX epilogue for N columns (the width partial needs). */
+/* Number of 128-column blocks of the ARGMAX epilogue for N columns (the width partial needs). */
 int smlm_linear_argmax_blocks(int N);
 
 int smlm_decode_linear(const smlm_linear_args *args, void *stream);
