@@ -4,7 +4,8 @@
 //   1. RoPE (model.py:63-78: rotate the two halves of the head) on the new token's q and k, in fp32, rounded to
 //      bf16 as the bf16 model holds them; k and v are written into the cache at the device-side position `pos`;
 //   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos (the new token's own k from LDS), each cache row read
-//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles;
+//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles; the loads of 8 passes of rows are
+//      in flight together (a decode step is latency-bound);
 //   3. softmax over t in fp32;
 //   4. y = sum_t p_t v_t, rows split over the workgroup's lanes, partial sums added through LDS; y is written as
 //      bf16 into the (B, H*head_dim) layout the output projection reads.
@@ -16,6 +17,7 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
+constexpr int kAttnUnroll = 8;    // passes of cache rows whose loads are in flight together
 
 template <bool ROPE_F32>
 __device__ __forceinline__ float table_val(const void *t, int64_t i) {
@@ -82,27 +84,48 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
   __syncthreads();
 
-  // 2. scores
+  // 2. scores.  Every cache load of a group of U passes is issued before the first is used (the step is latency-
+  // bound: one round trip per group, not per pass), and the first group's value rows are loaded with its key rows.
+  constexpr int U = kAttnUnroll;
   const int sub = lane % LPR, rw = lane / LPR;
+  const int slot = wave * RPW + rw;
+  const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
   const float scale = rsqrtf((float)HD);
   float qf[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) qf[e] = s_q[sub * 8 + e];
-  for (int t0 = 0; t0 <= P; t0 += RPB) {
-    const int t = t0 + wave * RPW + rw;
-    float kf[8];
-    if (t < P) {
-      unpack8(*(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8), kf);
-    } else {
+  uint4 vpre[U];
+  for (int t0 = 0; t0 <= P; t0 += RPB * U) {
+    uint4 kv[U];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = t == P ? s_k[sub * 8 + e] : 0.f;
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
+      kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
     }
-    float d = 0.f;
+    if (t0 == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
+      for (int u = 0; u < U; ++u) {
+        const int64_t t = min((int64_t)(u * RPB + slot), last);
+        vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
+      }
+    }
 #pragma unroll
-    for (int m = 1; m < LPR; m <<= 1) d += __shfl_xor(d, m, kWave);
-    if (sub == 0 && t <= P) s_p[t] = d * scale;
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPB + slot;
+      float kf[8];
+      if (t < P) {
+        unpack8(kv[u], kf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] = t == P ? s_k[sub * 8 + e] : 0.f;
+      }
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
+#pragma unroll
+      for (int m = 1; m < LPR; m <<= 1) d += __shfl_xor(d, m, kWave);
+      if (sub == 0 && t <= P) s_p[t] = d * scale;
+    }
   }
   __syncthreads();
 
@@ -128,23 +151,38 @@ __global__ void __launch_bounds__(kAttnThreads)
 #pragma unroll
   for (int w = 0; w < kAttnWaves; ++w) sum += s_w[kAttnWaves + w];
 
-  // 4. y = sum_t p_t v_t / sum
+  // 4. y = sum_t p_t v_t / sum (each lane's rows in increasing t, as one pass at a time would add them)
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int t = wave * RPW + rw; t <= P; t += RPB) {
-    const float pt = s_p[t];
-    float vf[8];
-    if (t < P) {
-      unpack8(*(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8), vf);
+  for (int t0 = 0; t0 <= P; t0 += RPB * U) {
+    uint4 vv[U];
+    if (t0 == 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) vv[u] = vpre[u];
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vf[e] = s_v[sub * 8 + e];
+      for (int u = 0; u < U; ++u) {
+        const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
+        vv[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
+      }
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
+    for (int u = 0; u < U; ++u) {
+      const int t = t0 + u * RPB + slot;
+      if (t > P) continue;
+      const float pt = s_p[t];
+      float vf[8];
+      if (t < P) {
+        unpack8(vv[u], vf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vf[e] = s_v[sub * 8 + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
+    }
   }
-  const int slot = wave * RPW + rw;
 #pragma unroll
   for (int e = 0; e < 8; ++e) s_red[slot * HD + sub * 8 + e] = acc[e];
   __syncthreads();
