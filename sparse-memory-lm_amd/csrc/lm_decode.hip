@@ -15,9 +15,57 @@
 namespace smlm {
 namespace {
 
-constexpr int kAttnThreads = 256;
-constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kAttnUnroll = 8;    // passes of cache rows whose loads are in flight together
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// v + v[lane ^ MASK] on every lane: quad permutes (1, 2), a row rotation (8) and the gfx950 permlane swaps (16, 32:
+// swapping a register with itself leaves v[lane] in one result and v[lane ^ MASK] in the other); other masks
+// through ds_bpermute.
+template <int MASK>
+__device__ __forceinline__ float xor_add(float v) {
+  if constexpr (MASK == 1) {
+    return v + dpp<0xB1>(v);
+  } else if constexpr (MASK == 2) {
+    return v + dpp<0x4E>(v);
+  } else if constexpr (MASK == 8) {
+    return v + dpp<0x128>(v);  // row_ror:8
+  } else if constexpr (MASK == 16 || MASK == 32) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto pr = MASK == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (uint32_t)pr[0]) + __builtin_bit_cast(float, (uint32_t)pr[1]);
+  } else {
+    return v + __shfl_xor(v, MASK, kWave);
+  }
+}
+
+// Sum over aligned groups of G lanes (butterfly: after each step the lanes of a group of 2^k hold its sum, so the
+// mirrors of the DPP row act as the xor 4 and xor 8 steps); every lane ends with its group's sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v = xor_add<1>(v);
+  if constexpr (G >= 4) v = xor_add<2>(v);
+  if constexpr (G >= 8) v += dpp<0x141>(v);   // row_half_mirror
+  if constexpr (G >= 16) v += dpp<0x140>(v);  // row_mirror
+  if constexpr (G >= 32) v = xor_add<16>(v);
+  if constexpr (G >= 64) v = xor_add<32>(v);
+  return v;
+}
+
+// Sum over the lanes lane % STRIDE == this lane's (strides 2..32 in doubling steps up to 64).
+template <int STRIDE>
+__device__ __forceinline__ float strided_sum(float v) {
+  if constexpr (STRIDE < kWave) {
+    v = xor_add<STRIDE>(v);
+    return strided_sum<STRIDE * 2>(v);
+  } else {
+    return v;
+  }
+}
 
 template <bool ROPE_F32>
 __device__ __forceinline__ float table_val(const void *t, int64_t i) {
@@ -34,12 +82,13 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   }
 }
 
-template <bool ROPE_F32, int HD>
+template <bool ROPE_F32, int HD, int kAttnThreads>
 __global__ void __launch_bounds__(kAttnThreads)
     decode_attention_kernel(const uint16_t *__restrict__ qkv, int64_t qkv_stride, const void *__restrict__ rope_cos,
                             const void *__restrict__ rope_sin, int rope_len, const int64_t *__restrict__ pos_ptr,
                             uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, int H, int max_len,
                             uint16_t *__restrict__ out) {
+  constexpr int kAttnWaves = kAttnThreads / kWave;
   constexpr int LPR = HD / 8;            // lanes per cache row (8 dims, 16 bytes each)
   constexpr int RPW = kWave / LPR;       // rows per wavefront per pass
   constexpr int RPB = RPW * kAttnWaves;  // rows per workgroup per pass
@@ -47,8 +96,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   float *s_q = smem;                     // [HD]
   float *s_k = s_q + HD;                 // [HD] new token's k (bf16 values)
   float *s_v = s_k + HD;                 // [HD]
-  float *s_red = s_v + HD;               // [RPB][HD] partial sums of p * v
-  float *s_w = s_red + RPB * HD;         // [kAttnWaves] wavefront partials
+  float *s_red = s_v + HD;               // [kAttnWaves][HD] partial sums of p * v
+  float *s_w = s_red + kAttnWaves * HD;  // [kAttnWaves] wavefront partials
   float *s_p = s_w + 2 * kAttnWaves;     // [max_len] scores, then probabilities
 
   const int b = blockIdx.x / H, h = blockIdx.x % H;
@@ -99,18 +148,21 @@ __global__ void __launch_bounds__(kAttnThreads)
     uint4 kv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if (t0 + u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
       const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
       kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
     }
     if (t0 == 0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if (u * RPB > P) continue;
         const int64_t t = min((int64_t)(u * RPB + slot), last);
         vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if (t0 + u * RPB > P) continue;
       const int t = t0 + u * RPB + slot;
       float kf[8];
       if (t < P) {
@@ -122,8 +174,7 @@ __global__ void __launch_bounds__(kAttnThreads)
       float d = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
-#pragma unroll
-      for (int m = 1; m < LPR; m <<= 1) d += __shfl_xor(d, m, kWave);
+      d = group_sum<LPR>(d);
       if (sub == 0 && t <= P) s_p[t] = d * scale;
     }
   }
@@ -163,6 +214,7 @@ __global__ void __launch_bounds__(kAttnThreads)
     } else {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if (t0 + u * RPB > P) continue;
         const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
         vv[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
       }
@@ -183,35 +235,53 @@ __global__ void __launch_bounds__(kAttnThreads)
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
     }
   }
+  // the wavefront's rows summed across its lanes (lane % LPR keeps the dims), then the wavefronts through LDS
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s_red[slot * HD + sub * 8 + e] = acc[e];
+  for (int e = 0; e < 8; ++e) acc[e] = strided_sum<LPR>(acc[e]);
+  if (rw == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_red[wave * HD + sub * 8 + e] = acc[e];
+  }
   __syncthreads();
   const float inv = 1.0f / sum;
   for (int i = tid; i < HD; i += kAttnThreads) {
     float y = 0.f;
-    for (int r = 0; r < RPB; ++r) y += s_red[r * HD + i];
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
     o[i] = (uint16_t)bf16_bits_rtne(y * inv);
   }
 }
 
-template <int HD>
-int launch_attention(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
-                     int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
-                     void *out, hipStream_t stream) {
-  constexpr int RPB = (kWave / (HD / 8)) * kAttnWaves;
-  const size_t shmem = sizeof(float) * (3 * HD + RPB * HD + 2 * kAttnWaves + (size_t)max_len);
+template <int HD, int NT>
+int launch_attention_nt(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
+                        int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
+                        void *out, hipStream_t stream) {
+  const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave) + (size_t)max_len);
   if (shmem > 64 * 1024)
     return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len=%d too long for one workgroup", max_len);
   const dim3 grid((unsigned)(B * H));
   if (rope_f32)
-    hipLaunchKernelGGL((decode_attention_kernel<true, HD>), grid, dim3(kAttnThreads), shmem, stream,
+    hipLaunchKernelGGL((decode_attention_kernel<true, HD, NT>), grid, dim3(NT), shmem, stream,
                        (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
                        (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
   else
-    hipLaunchKernelGGL((decode_attention_kernel<false, HD>), grid, dim3(kAttnThreads), shmem, stream,
+    hipLaunchKernelGGL((decode_attention_kernel<false, HD, NT>), grid, dim3(NT), shmem, stream,
                        (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
                        (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
   return launch_status("smlm_decode_attention");
+}
+
+// 256 threads per (sequence, head) when those workgroups already cover the chip; otherwise (small decode batches)
+// 1024, so each workgroup's rows are spread over more lanes and its chain of loads and reductions is shorter.
+template <int HD>
+int launch_attention(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
+                     int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
+                     void *out, hipStream_t stream) {
+  if (B * H >= 256)
+    return launch_attention_nt<HD, 256>(qkv, qkv_stride, cos, sin, rope_f32, rope_len, pos, k_cache, v_cache, B, H,
+                                        max_len, out, stream);
+  return launch_attention_nt<HD, 1024>(qkv, qkv_stride, cos, sin, rope_f32, rope_len, pos, k_cache, v_cache, B, H,
+                                       max_len, out, stream);
 }
 
 }  // namespace
