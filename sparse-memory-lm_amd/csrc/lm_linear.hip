@@ -75,19 +75,26 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 // Prologue: the workgroup's rows [0, nrows) normalised into sH (bf16, row stride KP), rows [nrows, pad_rows) zero.
 // Row rr = pass * 16 + wave * 4 + quarter is handled by the 16 lanes of one quarter wavefront; lane `sub` of it owns
-// the 16-byte chunks sub, sub + 16, ... (CPQ of them, K <= 128 * CPQ).
+// the 16-byte chunks sub, sub + 16, ... (CPQ of them, K <= 128 * CPQ).  load_activations issues every load of the
+// prologue (before the weight fragments: they are the workgroup's first use), norm_activations does the arithmetic.
+template <int CPQ, int MTB>
+struct ActIn {
+  uint4 xv[MTB][CPQ], dv[MTB][CPQ], gv[CPQ];
+  bool bad[MTB];
+};
+
 template <int PRO, int CPQ, int MTB>
-__device__ __forceinline__ void build_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
-                                                  uint16_t *sH, int KP, bool first_block) {
+__device__ __forceinline__ void load_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
+                                                 ActIn<CPQ, MTB> &in) {
   const int K = a.K, CH = K / 8;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int quarter = lane >> 4, sub = lane & 15;
   const int passes = pad_rows / 16;
-  const bool write_x = a.x_out != nullptr && first_block;
   const uint16_t *nw = (const uint16_t *)a.norm_w;
-
-  uint4 xv[MTB][CPQ], dv[MTB][CPQ], gv[CPQ];
-  bool bad[MTB];
+  auto &xv = in.xv;
+  auto &dv = in.dv;
+  auto &gv = in.gv;
+  auto &bad = in.bad;
 #pragma unroll
   for (int j = 0; j < CPQ; ++j) gv[j] = *(const uint4 *)(nw + min(sub + 16 * j, CH - 1) * 8);
 #pragma unroll
@@ -114,7 +121,20 @@ __device__ __forceinline__ void build_activations(const smlm_linear_args &a, int
       }
     }
   }
+}
 
+template <int PRO, int CPQ, int MTB>
+__device__ __forceinline__ void norm_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
+                                                 uint16_t *sH, int KP, bool first_block, ActIn<CPQ, MTB> &in) {
+  const int K = a.K, CH = K / 8;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int quarter = lane >> 4, sub = lane & 15;
+  const int passes = pad_rows / 16;
+  const bool write_x = a.x_out != nullptr && first_block;
+  auto &xv = in.xv;
+  auto &dv = in.dv;
+  auto &gv = in.gv;
+  auto &bad = in.bad;
 #pragma unroll
   for (int p = 0; p < MTB; ++p) {
     if (p >= passes) continue;
@@ -199,7 +219,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int col0 = ARG ? cb * kArgCols + wave * kArgTiles * 16 : cb * 16;
   const uint16_t *W = (const uint16_t *)a.w;
 
-  // 1. weight fragments (rows past N and steps past the slice re-read valid memory; their products are unused)
+  // 1. the prologue's loads, then the weight fragments (rows past N and steps past the slice re-read valid memory;
+  // their products are unused): the prologue's arithmetic then overlaps the weights' arrival
+  ActIn<CPQ, PRO == SMLM_LIN_PLAIN ? 1 : MTB> act;
+  if constexpr (PRO != SMLM_LIN_PLAIN) load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, act);
   uint4 areg[NT][MAXS];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -228,7 +251,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       }
     }
   } else {
-    build_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0);
+    norm_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0, act);
     __syncthreads();
   }
 
@@ -238,20 +261,37 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) acc[t][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (MT == MTB && ns == MAXS) {                    // every tile and step present: straight-line code
 #pragma unroll
-  for (int s = 0; s < MAXS; ++s) {
-    if (s >= ns) continue;                          // wavefront-uniform
-    const int k = (s_lo + s) * 32 + g * 8;
+    for (int s = 0; s < MAXS; ++s) {
+      const int k = (s_lo + s) * 32 + g * 8;
 #pragma unroll
-    for (int mt = 0; mt < MTB; ++mt) {
-      if (mt >= MT) continue;
-      uint4 b;
-      if constexpr (PRO == SMLM_LIN_PLAIN) b = breg[mt][s];
-      else b = *(const uint4 *)(sH + (mt * 16 + r) * KP + k);
+      for (int mt = 0; mt < MTB; ++mt) {
+        uint4 b;
+        if constexpr (PRO == SMLM_LIN_PLAIN) b = breg[mt][s];
+        else b = *(const uint4 *)(sH + (mt * 16 + r) * KP + k);
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, areg[t][s]),
-                                                             __builtin_bit_cast(bf16x8, b), acc[t][mt], 0, 0, 0);
+        for (int t = 0; t < NT; ++t)
+          acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, areg[t][s]),
+                                                               __builtin_bit_cast(bf16x8, b), acc[t][mt], 0, 0, 0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      if (s >= ns) continue;                          // wavefront-uniform
+      const int k = (s_lo + s) * 32 + g * 8;
+#pragma unroll
+      for (int mt = 0; mt < MTB; ++mt) {
+        if (mt >= MT) continue;
+        uint4 b;
+        if constexpr (PRO == SMLM_LIN_PLAIN) b = breg[mt][s];
+        else b = *(const uint4 *)(sH + (mt * 16 + r) * KP + k);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, areg[t][s]),
+                                                               __builtin_bit_cast(bf16x8, b), acc[t][mt], 0, 0, 0);
+      }
     }
   }
 
@@ -320,35 +360,36 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       *(uint2 *)((uint16_t *)a.out + (m0 + tok) * a.out_stride + c) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
     }
   } else {  // ARGMAX
-    uint64_t *sArg = (uint64_t *)smem;  // [4 wavefronts][TB tokens]
+    // 32-bit keys inside the workgroup (order16(bf16 logit) << 16 | 0xFFFF - column in the block), maxima over the
+    // lane groups by permlane swaps, over the wavefronts through LDS; the partial is the 64-bit key of the result
+    uint32_t *sArg = (uint32_t *)smem;  // [4 wavefronts][TB tokens]
     if constexpr (PRO != SMLM_LIN_PLAIN) __syncthreads();  // activations no longer read
 #pragma unroll
     for (int mt = 0; mt < MTB; ++mt) {
       if (mt >= MT) continue;
-      uint64_t best = 0;
+      uint32_t best = 0;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int col = c + t * 16 + e;
-          if (col >= cols) continue;
-          const uint64_t key = ((uint64_t)order16(bf16_bits_rtne(acc[t][mt][e])) << 32) |
-                               (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
+          const int local = wave * kArgTiles * 16 + 4 * g + t * 16 + e;   // column - cb * kArgCols
+          if (c + t * 16 + e >= cols) continue;
+          const uint32_t key = (order16(bf16_bits_rtne(acc[t][mt][e])) << 16) | (0xFFFFu - (uint32_t)local);
           best = key > best ? key : best;
         }
-#pragma unroll
-      for (int o = 16; o < kWave; o <<= 1) {
-        const uint64_t other = __shfl_xor(best, o, kWave);
-        best = other > best ? other : best;
-      }
+      auto p16 = __builtin_amdgcn_permlane16_swap(best, best, false, false);
+      best = max((uint32_t)p16[0], (uint32_t)p16[1]);
+      auto p32 = __builtin_amdgcn_permlane32_swap(best, best, false, false);
+      best = max((uint32_t)p32[0], (uint32_t)p32[1]);
       if (g == 0) sArg[wave * TB + mt * 16 + r] = best;
     }
     __syncthreads();
     if (tid < nrows) {
-      uint64_t best = sArg[tid];
+      uint32_t best = sArg[tid];
 #pragma unroll
-      for (int w2 = 1; w2 < kLinWaves; ++w2) best = sArg[w2 * TB + tid] > best ? sArg[w2 * TB + tid] : best;
-      a.partial[(m0 + tid) * a.partial_stride + cb] = best;
+      for (int w2 = 1; w2 < kLinWaves; ++w2) best = max(best, sArg[w2 * TB + tid]);
+      const uint32_t col = (uint32_t)cb * kArgCols + (0xFFFFu - (best & 0xFFFFu));
+      a.partial[(m0 + tid) * a.partial_stride + cb] = ((uint64_t)(best >> 16) << 32) | (uint64_t)(0xFFFFFFFFu - col);
     }
   }
 }
@@ -436,7 +477,8 @@ void launch_linear_pro(const smlm_linear_args &a, const LinGrid &grid, hipStream
   }
   const int per_wave = (steps + kLinWaves - 1) / kLinWaves;
 #define SMLM_LIN_MAXS(EPI)                                                               \
-  if (per_wave <= 4) launch_linear_cpq<PRO, EPI, 4>(a, grid, stream);                     \
+  if (per_wave == 3) launch_linear_cpq<PRO, EPI, 3>(a, grid, stream);                     \
+  else if (per_wave <= 4) launch_linear_cpq<PRO, EPI, 4>(a, grid, stream);                \
   else if (PRO == SMLM_LIN_PLAIN && per_wave <= 8) launch_linear_cpq<PRO, EPI, 8>(a, grid, stream); \
   else launch_linear_cpq<PRO, EPI, 16>(a, grid, stream);
   if (a.epilogue == SMLM_LIN_STORE) {
@@ -525,7 +567,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   const int pad_rows = (int)(((A.M < tb ? A.M : tb) + 15) / 16 * 16);
   const size_t act = pro != SMLM_LIN_PLAIN ? (size_t)pad_rows * (A.K + 8) * 2 : 0;
   const size_t red = epi == SMLM_LIN_ARGMAX
-                         ? (size_t)kLinWaves * tb * 8
+                         ? (size_t)kLinWaves * tb * 4
                          : (size_t)(kLinWaves - 1) * (epi == SMLM_LIN_SWIGLU ? 2 : 1) * lg.mtb * kWave * 16;
   lg.shmem = act > red ? act : red;
   hipStream_t s = (hipStream_t)stream;
