@@ -27,7 +27,9 @@ __device__ __forceinline__ uint4 load16_or_zero(const void *p, bool ok) {
   return ok ? v : uint4{0u, 0u, 0u, 0u};
 }
 
-template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N>
+// PRE > 0 (bf16 only): when half <= 32 * PRE, every operand fragment of the workgroup is loaded before the first
+// product (decode sizes are latency-bound: one round trip instead of one per k-step).
+template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N, int PRE = 0>
 __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
     score_kernel(const void *__restrict__ q, int64_t q_stride, const void *__restrict__ keys, int N, int H, int NK,
                  int half, void *__restrict__ s1, void *__restrict__ s2) {
@@ -51,7 +53,41 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < half; k0 += KSTEP) {
+  if constexpr (!F32 && PRE > 0) {
+    if (half <= PRE * KSTEP) {
+      uint4 a[PRE][WM], b[PRE][WN];
+#pragma unroll
+      for (int st = 0; st < PRE; ++st) {
+        if (st * KSTEP >= half) continue;  // workgroup-uniform
+        const int kk = st * KSTEP + g * EPL;
+        const bool kin = kk < half;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+          const int key = key0 + i * 16 + r;
+          a[st][i] = load16_or_zero(kbase + ((int64_t)min(key, NK - 1) * half + (kin ? kk : 0)) * ESZ,
+                                    kin && key < NK);
+        }
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const int tok = tok0 + j * 16 + r;
+          b[st][j] = load16_or_zero(qbase + ((int64_t)min(tok, N - 1) * q_stride + (kin ? kk : 0)) * ESZ,
+                                    kin && tok < N);
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < PRE; ++st) {
+        if (st * KSTEP >= half) continue;
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[st][i]),
+                                                                __builtin_bit_cast(bf16x8, b[st][j]), acc[i][j], 0, 0,
+                                                                0);
+      }
+    }
+  }
+  for (int k0 = (!F32 && PRE > 0 && half <= PRE * KSTEP) ? half : 0; k0 < half; k0 += KSTEP) {
     const int kk = k0 + g * EPL;
     const bool kin = kk < half;  // half % EPL == 0: a lane's group is entirely inside or outside
     uint4 a[WM], b[WN];
@@ -357,21 +393,128 @@ __global__ void __launch_bounds__(WAVES * 64)
 #undef SMLM_STREAM_PUT
 }
 
-template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N>
+// bf16 decode sizes (N <= 64, half <= 256): a workgroup = 4 wavefronts x 32 sub-keys = 128 sub-keys against 16 * MT
+// tokens.  The query tile is loaded once per workgroup into LDS (the four wavefronts share it), each wavefront's
+// sub-key rows go straight into registers, and every load is issued before the first product.
+template <int MT>
+__global__ void __launch_bounds__(256)
+    score_decode_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
+                        int H, int NK, int half, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
+  constexpr int MAXST = 8;                 // k-steps of 32 (half <= 256)
+  constexpr int RS = MAXST * 32 + 8;       // LDS row stride (bf16)
+  __shared__ __align__(16) uint16_t sQ[16 * MT * RS];
+  const int z = blockIdx.z, h = z >> 1, p = z & 1;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, r = lane & 15, g = lane >> 4;
+  const int key0 = blockIdx.x * 128 + wave * 32;
+  const int tok0 = blockIdx.y * (16 * MT);
+  const uint16_t *kbase = keys + (int64_t)z * NK * half;
+  const uint16_t *qbase = q + (int64_t)h * 2 * half + (int64_t)p * half;
+  const int nst = (half + 31) / 32;
+
+  // 1. this wavefront's sub-key fragments (steps past half and keys past NK load valid memory, then zero)
+  uint4 a[MAXST][2];
+#pragma unroll
+  for (int st = 0; st < MAXST; ++st) {
+    if (st >= nst) continue;  // workgroup-uniform
+    const int kk = st * 32 + g * 8;
+    const bool kin = kk < half;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = key0 + i * 16 + r;
+      a[st][i] = load16_or_zero(kbase + (int64_t)min(key, NK - 1) * half + (kin ? kk : 0), kin && key < NK);
+    }
+  }
+  // 2. the query tile into LDS: row t (token tok0 + t), 16-byte chunks c < half / 8; tokens past N are zero rows
+  const int cpr = half / 8, chunks = 16 * MT * cpr;
+  constexpr int kMaxChunks = 16 * MT * MAXST * 4;
+  uint4 qv[(kMaxChunks + 255) / 256];
+#pragma unroll
+  for (int u = 0; u < (kMaxChunks + 255) / 256; ++u) {
+    const int ch = tid + u * 256;
+    if (ch >= chunks) continue;
+    const int t = ch / cpr, c = ch % cpr;
+    qv[u] = load16_or_zero(qbase + (int64_t)min(tok0 + t, N - 1) * q_stride + c * 8, tok0 + t < N);
+  }
+#pragma unroll
+  for (int u = 0; u < (kMaxChunks + 255) / 256; ++u) {
+    const int ch = tid + u * 256;
+    if (ch >= chunks) continue;
+    const int t = ch / cpr, c = ch % cpr;
+    *(uint4 *)&sQ[t * RS + c * 8] = qv[u];
+  }
+  // the steps' k groups past half read columns [half, 32 * nst) of the tile: zero them
+  for (int i = tid; i < 16 * MT * (nst * 4 - cpr); i += 256) {
+    const int t = i / (nst * 4 - cpr), c = cpr + i % (nst * 4 - cpr);
+    *(uint4 *)&sQ[t * RS + c * 8] = uint4{0u, 0u, 0u, 0u};
+  }
+  __syncthreads();
+
+  // 3. products
+  floatx4 acc[2][MT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < MAXST; ++st) {
+    if (st >= nst) continue;
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const uint4 b = *(const uint4 *)&sQ[(j * 16 + r) * RS + st * 32 + g * 8];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[st][i]),
+                                                            __builtin_bit_cast(bf16x8, b), acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // 4. scores: lane (r, g) holds sub-keys key0 + 16 i + 4g .. +3 of token tok0 + 16 j + r
+  uint16_t *out = p ? s2 : s1;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const int tok = tok0 + j * 16 + r;
+      const int key = key0 + i * 16 + g * 4;
+      if (tok >= N || key >= NK) continue;
+      uint16_t *o = out + ((int64_t)tok * H + h) * NK + key;
+      const floatx4 v = acc[i][j];
+      if ((NK & 3) == 0) {  // key % 4 == 0 and NK % 4 == 0: the 4 scores are in range and 8-byte aligned
+        *(uint2 *)o = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (key + e < NK) o[e] = (uint16_t)bf16_bits_rtne(v[e]);
+      }
+    }
+}
+
+template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N, int PRE = 0>
 void launch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                   void *s2, hipStream_t stream) {
   constexpr int BM = WAVES_M * WM * 16, BN = WAVES_N * WN * 16;
   const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((NK + BM - 1) / BM), (unsigned)(2 * H));
-  hipLaunchKernelGGL((score_kernel<F32, WM, WN, WAVES_M, WAVES_N>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream,
-                     q, q_stride, keys, (int)N, H, NK, half, s1, s2);
+  hipLaunchKernelGGL((score_kernel<F32, WM, WN, WAVES_M, WAVES_N, PRE>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
+                     stream, q, q_stride, keys, (int)N, H, NK, half, s1, s2);
 }
 
 template <bool F32>
 void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                     void *s2, hipStream_t stream) {
-  if (N <= 16) {  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
-    launch_score<F32, 2, 1, 4, 1>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
-  } else if (F32 || N <= 64 || (N / 128 + 1) * (NK / 128 + 1) * 2 * (int64_t)H >= (1LL << 30)) {
+  if (!F32 && N <= 64 && half <= 256) {  // decode: 128 sub-keys x 16 or 64 tokens, query tile shared in LDS
+    const dim3 grid((unsigned)((NK + 127) / 128), (unsigned)((N + (N <= 16 ? 15 : 63)) / (N <= 16 ? 16 : 64)),
+                    (unsigned)(2 * H));  // x: sub-key blocks, y: token blocks, z: (head, half)
+    if (N <= 16)
+      hipLaunchKernelGGL((score_decode_kernel<1>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+                         (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
+    else
+      hipLaunchKernelGGL((score_decode_kernel<4>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+                         (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
+  } else if (N <= 16) {  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
+    launch_score<F32, 2, 1, 4, 1, F32 ? 0 : 8>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
+  } else if (!F32 && N <= 64) {  // decode batches: 128 sub-keys x 64 tokens, operands preloaded
+    launch_score<F32, 4, 2, 2, 2, F32 ? 0 : 8>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
+  } else if (F32 || (N / 128 + 1) * (NK / 128 + 1) * 2 * (int64_t)H >= (1LL << 30)) {
     // 128 sub-keys x 64 tokens per workgroup, operands straight from memory
     launch_score<F32, 4, 2, 2, 2>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
   } else if (!F32 && (half == 64 || half == 128 || half == 256) && NK % 4 == 0 && N >= 256) {
