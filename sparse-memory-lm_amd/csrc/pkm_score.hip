@@ -517,7 +517,8 @@ void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N
   } else if (F32 || (N / 128 + 1) * (NK / 128 + 1) * 2 * (int64_t)H >= (1LL << 30)) {
     // 128 sub-keys x 64 tokens per workgroup, operands straight from memory
     launch_score<F32, 4, 2, 2, 2>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
-  } else if (!F32 && (half == 64 || half == 128 || half == 256) && NK % 4 == 0 && N >= 256) {
+  } else if (!F32 && (half == 64 || half == 128 || half == 256) && NK % 4 == 0 && N >= 256 &&
+             (N + 255) / 256 * 2 * (int64_t)H >= 256) {  // enough 256-token tiles to give every CU one
     // bf16, many tokens: query-stationary streaming of the sub-keys
     const int64_t tiles = (N + 255) / 256;
     const dim3 grid((unsigned)(tiles * 2 * H));

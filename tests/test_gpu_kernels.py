@@ -125,7 +125,9 @@ def test_pk_select_golden():
 # ------------------------------------------------------------------------------------------------ scoring
 SCORE_SHAPES = [(1, 4, 4096, 256), (64, 4, 4096, 256), (2048, 4, 1024, 256), (100, 4, 2048, 256),
                 (5, 2, 16, 8), (17, 3, 64, 32), (300, 1, 512, 64), (1000, 4, 2048, 256), (200, 2, 64, 40),
-                (129, 3, 16, 8), (65, 2, 384, 128), (513, 2, 192, 128), (260, 3, 100, 128)]
+                (129, 3, 16, 8), (65, 2, 384, 128), (513, 2, 192, 128), (260, 3, 100, 128),
+                # enough 256-token tiles for the streaming kernel: half 256 / 128 (ragged tile, NK % 64) / 64
+                (8192, 4, 128, 256), (8200, 4, 100, 128), (16384, 2, 64, 64)]
 
 
 def _score_inputs(N, H, NK, half, seed):
