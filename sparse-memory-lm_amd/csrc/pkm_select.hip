@@ -388,6 +388,97 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// v of lane ^ J (J < 64) on every lane: quad permutes (1, 2), row shifts by 4 either way (4), a row rotation (8),
+// and the gfx950 permlane swaps (16, 32), which given a register twice return v[lane] and v[lane ^ J] in some order.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  const int lane = lane_id();
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (J == 4) {  // row_shl:4 (lane i reads i + 4) or row_shr:4 (i - 4), both inside the row
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+    return (lane & 4) ? dn : up;
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? (uint32_t)p[0] : (uint32_t)p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? (uint32_t)p[0] : (uint32_t)p[1];
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  return (uint64_t)xor_lane<J>((uint32_t)v) | ((uint64_t)xor_lane<J>((uint32_t)(v >> 32)) << 32);
+}
+
+// One compare-exchange stage (block size K, distance J < 64) of a descending bitonic sort of the wavefront's
+// SLOTS * 64 keys, element e = s * 64 + lane.
+template <int SLOTS, int K, int J>
+__device__ __forceinline__ void bitonic_stage(uint64_t (&x)[SLOTS]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int e = s * kWave + lane;
+    const uint64_t y = xor_lane64<J>(x[s]);
+    const bool take_max = ((e & J) == 0) == ((e & K) == 0);  // the lower element of a descending block: max
+    const bool gt = x[s] > y;
+    x[s] = (gt == take_max) ? x[s] : y;
+  }
+}
+
+template <int SLOTS, int K, int J>
+__device__ __forceinline__ void bitonic_merge(uint64_t (&x)[SLOTS]) {
+  if constexpr (J >= kWave) {  // partner in the same lane: slots s and s ^ (J / 64)
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const int s2 = s ^ (J / kWave);
+      if (s2 > s) {
+        const bool desc = ((s * kWave) & K) == 0;
+        const uint64_t a = x[s], b = x[s2];
+        const uint64_t mx = a > b ? a : b, mn = a > b ? b : a;
+        x[s] = desc ? mx : mn;
+        x[s2] = desc ? mn : mx;
+      }
+    }
+  } else {
+    bitonic_stage<SLOTS, K, J>(x);
+  }
+  if constexpr (J > 1) bitonic_merge<SLOTS, K, J / 2>(x);
+}
+
+// Descending bitonic sort of SLOTS * 64 unique 64-bit keys held one per lane per slot; afterwards lane j of slot 0
+// holds the j-th largest.
+template <int SLOTS, int K = 2>
+__device__ __forceinline__ void bitonic_sort_desc(uint64_t (&x)[SLOTS]) {
+  bitonic_merge<SLOTS, K, K / 2>(x);
+  if constexpr (K < SLOTS * kWave) bitonic_sort_desc<SLOTS, K * 2>(x);
+}
+
+// The Cartesian pairs' keys (code << 32 | ~full index; 0 for a slot without a pair)
+template <bool F32, int SLOTS>
+__device__ __forceinline__ void cartesian_keys(const typename SelKey<F32>::T *top1, const typename SelKey<F32>::T *top2,
+                                               int NK, const uint32_t (&pc)[kMaxPairSlots], uint64_t (&ck)[SLOTS]) {
+  using Key = typename SelKey<F32>::T;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    ck[s] = 0;
+    if (pc[s] != kNoPair) {
+      const Key k1 = top1[pc[s] & 0xFFu];
+      const Key k2 = top2[pc[s] >> 8];
+      const float sum = key_value<F32>(k1) + key_value<F32>(k2);
+      const uint32_t code = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
+      const uint32_t full = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
+      ck[s] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
+    }
+  }
+}
+
 template <bool F32, int SLOTS>
 __device__ __forceinline__ uint64_t cartesian_threshold(const typename SelKey<F32>::T *top1,
                                                         const typename SelKey<F32>::T *top2, int NK, int knn,
@@ -437,23 +528,35 @@ __device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *to
                                                uint64_t *s_fin, float &sc, uint32_t &full, uint32_t &code,
                                                float &wt) {
   const int lane = lane_id();
-  // pairs per knn: <= 50 (one slot of 64 lanes), 119 (two), 280 (five)
-  if (knn >= 64) cartesian_threshold<F32, 5>(top1, top2, NK, knn, pc, s_fsel);
-  else if (knn >= 32) cartesian_threshold<F32, 2>(top1, top2, NK, knn, pc, s_fsel);
-  else cartesian_threshold<F32, 1>(top1, top2, NK, knn, pc, s_fsel);
-  if (lane >= knn && lane < 2) s_fsel[lane] = 0;  // pad knn = 1 to a whole 16-byte read
-  wave_lds_sync();
-  if (lane < knn) {
-    const uint64_t mine = s_fsel[lane];
-    s_fin[rank_in(s_fsel, knn < 2 ? 2 : knn, mine)] = mine;
+  // pairs per knn: <= 50 (one slot of 64 lanes), 119 (two), 280 (five).  Up to two slots: a bitonic sort in
+  // registers (keys are unique: distinct pairs have distinct table indices; pair-less slots sort last); five: the
+  // threshold search, compaction and rank through LDS.
+  uint64_t u = 0;
+  if (knn >= 64) {
+    cartesian_threshold<F32, 5>(top1, top2, NK, knn, pc, s_fsel);
+    wave_lds_sync();
+    if (lane < knn) {
+      const uint64_t mine = s_fsel[lane];
+      s_fin[rank_in(s_fsel, knn, mine)] = mine;
+    }
+    wave_lds_sync();
+    if (lane < knn) u = s_fin[lane];
+  } else if (knn >= 32) {
+    uint64_t ck[2];
+    cartesian_keys<F32, 2>(top1, top2, NK, pc, ck);
+    bitonic_sort_desc<2>(ck);
+    u = ck[0];
+  } else {
+    uint64_t ck[1];
+    cartesian_keys<F32, 1>(top1, top2, NK, pc, ck);
+    bitonic_sort_desc<1>(ck);
+    u = ck[0];
   }
-  wave_lds_sync();
 
   sc = 0.f;
   full = 0;
   code = 0;
   if (lane < knn) {
-    const uint64_t u = s_fin[lane];
     code = (uint32_t)(u >> 32);
     full = 0xFFFFFFFFu - (uint32_t)u;
     sc = F32 ? __uint_as_float(unorder32(code)) : bf16_bits_to_f32(unorder16(code));
