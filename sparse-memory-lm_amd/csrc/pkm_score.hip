@@ -18,6 +18,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // 16 bytes at p (always a valid address: callers clamp row indices into range), or zeros if !ok.  Selecting the
 // loaded value rather than the address keeps the load a plain global load (a select between a global pointer and
@@ -393,6 +394,125 @@ __global__ void __launch_bounds__(WAVES * 64)
 #undef SMLM_STREAM_PUT
 }
 
+// bf16, many tokens, NK % 64 == 0: the query-stationary stream with the wavefronts specialised.  A workgroup = 4
+// compute wavefronts (64 tokens each, query fragments in registers for the whole launch) + 4 memory wavefronts, 256
+// tokens of one (head, half).  Per 64-sub-key block kb the compute wavefronts run the MFMAs on LDS block kb and write
+// their bf16 scores to an LDS output tile; meanwhile the memory wavefronts put block kb + 1 (fetched during the
+// previous block) into the other LDS key buffer, fetch block kb + 2, and write block kb - 1's output tile to memory
+// as whole 128-byte score rows.  A wavefront that stalls on a store is then never one that has MFMAs to issue: the
+// stores (537 MB at config 2) and the products overlap.  One barrier per block.
+constexpr int kWsTok = 256;             // tokens per workgroup
+constexpr int kWsOutStride = kStreamKeys + 8;  // LDS output tile row stride (bf16)
+
+template <int KSTEPS>
+__global__ void __launch_bounds__(512)
+    score_ws_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
+                    int H, int NK, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
+  constexpr int HALF = KSTEPS * 32;
+  constexpr int RS = HALF + 8;               // LDS key row stride (bf16)
+  constexpr int PPR = HALF / 8;              // 16-byte pieces per sub-key row
+  constexpr int PPT = kStreamKeys * PPR / 256;   // key pieces per memory thread per block
+  constexpr int RPP = 256 / PPR;             // key rows per memory pass
+  constexpr int OPT = kWsTok * kStreamKeys / 8 / 256;  // 16-byte output pieces per memory thread per block (8)
+  __shared__ __align__(16) uint16_t sA[2 * kStreamKeys * RS];          // 2 key blocks of 64 rows
+  __shared__ __align__(16) uint16_t sO[2 * kWsTok * kWsOutStride];     // 2 output tiles of 256 token rows
+  const int Z = 2 * H;
+  const int z = (int)(blockIdx.x % Z), tile = (int)(blockIdx.x / Z);
+  const int h = z >> 1, p = z & 1;
+  const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+  const uint16_t *kbase = keys + (int64_t)z * NK * HALF;
+  uint16_t *out = p ? s2 : s1;
+  const int tok_base = tile * kWsTok;
+  const int nkb = NK / kStreamKeys;
+
+  if (wave < 4) {
+    // ---- compute wavefronts
+    const int r = lane & 15, g = lane >> 4;
+    const int tok0 = tok_base + wave * kStreamWaveTok;
+    const uint16_t *qbase = q + (int64_t)h * 2 * HALF + (int64_t)p * HALF;
+    bf16x8 bq[4][KSTEPS];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tok = tok0 + j * 16 + r;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+        bq[j][s] = __builtin_bit_cast(
+            bf16x8, load16_or_zero(qbase + (int64_t)min(tok, N - 1) * q_stride + s * 32 + g * 8, tok < N));
+    }
+    __syncthreads();  // block 0 is in sA[0]
+    for (int kb = 0; kb < nkb; ++kb) {
+      const uint16_t *A = sA + (kb & 1) * kStreamKeys * RS;
+      floatx4 acc[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        bf16x8 a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *(const bf16x8 *)&A[(i * 16 + r) * RS + s * 32 + g * 8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bq[j][s], acc[i][j], 0, 0, 0);
+      }
+      // lane (r, g) holds keys 16 i + 4 g .. +3 of token 16 j + r: into the output tile
+      uint16_t *O = sO + (kb & 1) * kWsTok * kWsOutStride + (wave * kStreamWaveTok) * kWsOutStride;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *(uint2 *)&O[(j * 16 + r) * kWsOutStride + i * 16 + g * 4] =
+              uint2{pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3])};
+      __syncthreads();
+    }
+    // done: the memory wavefronts write the last tile after the last barrier (1 + nkb barriers on both sides)
+  } else {
+    // ---- memory wavefronts: thread mt = 0..255
+    const int mt = tid - 256;
+    const int prow = mt / PPR, pcol = (mt % PPR) * 8;
+    u32x4 stage[PPT];  // a native vector type: an array of it stays in registers
+    // block 0 into sA[0], block 1 into registers
+#pragma unroll
+    for (int i = 0; i < PPT; ++i)
+      stage[i] = *(const u32x4 *)(kbase + ((int64_t)prow + RPP * i) * HALF + pcol);
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) *(u32x4 *)&sA[(prow + RPP * i) * RS + pcol] = stage[i];
+    if (nkb > 1) {
+#pragma unroll
+      for (int i = 0; i < PPT; ++i)
+        stage[i] = *(const u32x4 *)(kbase + ((int64_t)kStreamKeys + prow + RPP * i) * HALF + pcol);
+    }
+    __syncthreads();
+    for (int kb = 0; kb <= nkb; ++kb) {
+      if (kb + 1 < nkb) {  // block kb + 1 into the other key buffer (its last readers finished block kb - 1)
+        uint16_t *A = sA + ((kb + 1) & 1) * kStreamKeys * RS;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) *(u32x4 *)&A[(prow + RPP * i) * RS + pcol] = stage[i];
+      }
+      if (kb + 2 < nkb) {
+        const uint16_t *src = kbase + ((int64_t)(kb + 2) * kStreamKeys + prow) * HALF + pcol;
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) stage[i] = *(const u32x4 *)(src + (int64_t)RPP * i * HALF);
+      }
+      if (kb >= 1) {  // block kb - 1's scores: rows of 64 sub-keys = 8 pieces of 16 bytes
+        const uint16_t *O = sO + ((kb - 1) & 1) * kWsTok * kWsOutStride;
+        const int key0 = (kb - 1) * kStreamKeys;
+#pragma unroll
+        for (int u = 0; u < OPT; ++u) {
+          const int id = mt + 256 * u, t = id >> 3, c = id & 7;
+          const u32x4 v = *(const u32x4 *)&O[t * kWsOutStride + c * 8];
+          const int tok = tok_base + t;
+          if (tok < N) *(u32x4 *)(out + ((int64_t)tok * H + h) * NK + key0 + c * 8) = v;
+        }
+      }
+      if (kb < nkb) __syncthreads();
+    }
+  }
+}
+
 // bf16 decode sizes (N <= 64, half <= 256): a workgroup = 4 wavefronts x 32 sub-keys = 128 sub-keys against 16 * MT
 // tokens.  The query tile is loaded once per workgroup into LDS (the four wavefronts share it), each wavefront's
 // sub-key rows go straight into registers, and every load is issued before the first product.
@@ -522,6 +642,16 @@ void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N
     // bf16, many tokens: query-stationary streaming of the sub-keys
     const int64_t tiles = (N + 255) / 256;
     const dim3 grid((unsigned)(tiles * 2 * H));
+    if (NK % kStreamKeys == 0) {  // whole blocks: compute and memory wavefronts specialised
+#define SMLM_WS(KS)                                                                                           \
+  hipLaunchKernelGGL((score_ws_kernel<KS>), grid, dim3(512), 0, stream, (const uint16_t *)q, q_stride,        \
+                     (const uint16_t *)keys, (int)N, H, NK, (uint16_t *)s1, (uint16_t *)s2)
+      if (half == 256) SMLM_WS(8);
+      else if (half == 128) SMLM_WS(4);
+      else SMLM_WS(2);
+#undef SMLM_WS
+      return;
+    }
 #define SMLM_STREAM(KS)                                                                                       \
   hipLaunchKernelGGL((score_stream_kernel<KS, 4>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,  \
                      (const uint16_t *)keys, (int)N, H, NK, (uint16_t *)s1, (uint16_t *)s2)

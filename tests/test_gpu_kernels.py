@@ -126,8 +126,9 @@ def test_pk_select_golden():
 SCORE_SHAPES = [(1, 4, 4096, 256), (64, 4, 4096, 256), (2048, 4, 1024, 256), (100, 4, 2048, 256),
                 (5, 2, 16, 8), (17, 3, 64, 32), (300, 1, 512, 64), (1000, 4, 2048, 256), (200, 2, 64, 40),
                 (129, 3, 16, 8), (65, 2, 384, 128), (513, 2, 192, 128), (260, 3, 100, 128),
-                # enough 256-token tiles for the streaming kernel: half 256 / 128 (ragged tile, NK % 64) / 64
-                (8192, 4, 128, 256), (8200, 4, 100, 128), (16384, 2, 64, 64)]
+                # enough 256-token tiles for the streaming kernels: NK % 64 == 0 takes the warp-specialised one
+                # (half 256, 128 with a ragged token tile, 64 with a single sub-key block), else the plain stream
+                (8192, 4, 128, 256), (8200, 4, 192, 128), (16384, 2, 64, 64), (8200, 4, 100, 128)]
 
 
 def _score_inputs(N, H, NK, half, seed):
