@@ -335,7 +335,7 @@ def main():
         if traffic:
             roofline["physical_GBps_zipf"] = traffic / ga["ms_zipf"] / 1e6
     if lk is not None:
-        roofline_score = {"kernel": "score_stream_kernel<8, 4> (config 2 scoring)", "bound": "mfma",
+        roofline_score = {"kernel": "score_ws_kernel<8> (config 2 scoring)", "bound": "mfma",
                           "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                           "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS}
     line = {
