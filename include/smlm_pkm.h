@@ -234,6 +234,58 @@ int smlm_decode_linear(const smlm_linear_args *args, void *stream);
 int smlm_argmax_finish(const uint64_t *partial, int64_t partial_stride, int nblk, int64_t M, int64_t *pos,
                        int64_t *tok, int64_t *hist, int64_t hist_stride, int64_t hist_len, int advance, void *stream);
 
+/* ---- training side of the lookup ------------------------------------------------------------------------- */
+
+/*
+ * Backward of the selection (PKSelect.backward, smlm/kernels.py:253-266):
+ *   dl[n,h,k] = w * (g_w - sum_k' w * g_w)  (+ g_scores[n,h,k] if given),  ds = dl rounded to the scores' dtype;
+ *   ds1[n,h,:] = dense fp32 sums of ds over the selected pairs per first-half sub-key idx / NK, rounded once to
+ *   dtype; ds2 the same per second-half sub-key idx % NK.  Sums run in selection order (deterministic).
+ *   idx (N, H, knn) int64 and w (N, H, knn) fp32 from smlm_pkm_select; g_scores (N, H, knn) of dtype or NULL;
+ *   g_w (N, H, knn) fp32 or NULL; ds1, ds2 (N, H, NK) of dtype (every element written), 16-byte aligned.
+ *   NK a power of two in [8, 65536], knn <= 64.
+ */
+int smlm_pkm_select_backward(const int64_t *idx, const float *w, const void *g_scores, const float *g_w, int dtype,
+                             int64_t N, int H, int NK, int knn, void *ds1, void *ds2, void *stream);
+
+/*
+ * Row-sparse value-bag backward (smlm/kernels.py:1-104, smlm/sparse_values.py:94-113):
+ *   acc[idx[n,k], :] += w[n,k] * grad_out[n, :]   (fp32 atomic adds: the order of additions is not fixed)
+ *   touched[idx[n,k]] = 1
+ *   gw[n,k] = sum_d grad_out[n,d] * table[idx[n,k], d]   (the per-sample-weight gradient, fp32)
+ *   grad_out (N, D) fp32; idx (N, K) int64; w (N, K) fp32; table (rows, D) SMLM_F32 or SMLM_BF16; acc (rows, D)
+ *   fp32; touched (rows,) uint8; gw (N, K) fp32.  D <= 512.  An index outside [0, rows) adds nothing and gives a
+ *   NaN gw.
+ */
+int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
+                           const void *table, int table_dtype, int64_t rows, int D, float *acc, uint8_t *touched,
+                           float *gw, void *stream);
+
+/* Moment storage of smlm_lazy_adam. */
+typedef enum smlm_adam_state {
+  SMLM_ADAM_F32 = 0,   /* exp_avg, exp_avg_sq (rows, D) fp32 (smlm/kernels.py:380-433) */
+  SMLM_ADAM_BF16 = 1,  /* (rows, D) bf16, round to nearest even (smlm/kernels.py:445-492) */
+  SMLM_ADAM_INT8 = 2   /* exp_avg (rows, D) int8 codes of sign(m) sqrt(|m| / s_m) * 127, exp_avg_sq (rows, D)
+                          uint8 codes of v^(1/4) / s_v * 255 (>= 1 where v > 0), fp32 row scales s_m = max|m|,
+                          s_v = max v^(1/4) (smlm/kernels.py:445-492) */
+} smlm_adam_state;
+
+/*
+ * Lazy Adam step of the value table (LazyRowAdam, smlm/sparse_values.py:148-330, kernels.py:380-515), in place, on
+ * the rows with touched[r] != 0 only:
+ *   g = acc[r] * (*grad_scale);  m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2;
+ *   p[r] -= step_size * m / (sqrt(v) / bc2_sqrt + eps)       (step_size = lr / (1 - b1^step),
+ *                                                             bc2_sqrt = sqrt(1 - b2^step), from the host)
+ *   then acc[r] = 0 and touched[r] = 0.  SMLM_ADAM_F32 forms 1 - b on the device in fp32 (as the reference's fp32
+ *   kernel); the compact states use one_minus_beta1/2 as given (fp32 of the host's 1 - b).  IEEE division and
+ *   square root, no fused multiply-add.  param, acc (rows, D) fp32; touched (rows,) uint8; grad_scale a device
+ *   fp32 scalar; exp_avg_scale / exp_avg_sq_scale (rows,) fp32 for SMLM_ADAM_INT8 (else NULL).  D <= 512.
+ */
+int smlm_lazy_adam(float *param, void *exp_avg, void *exp_avg_sq, float *exp_avg_scale, float *exp_avg_sq_scale,
+                   int state, float *acc, uint8_t *touched, const float *grad_scale, int64_t rows, int D,
+                   float step_size, float bc2_sqrt, float beta1, float beta2, float one_minus_beta1,
+                   float one_minus_beta2, float eps, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

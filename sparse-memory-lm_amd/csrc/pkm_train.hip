@@ -1,0 +1,391 @@
+// Training side of the lookup (the gradients of the selection and of the value bag, and the lazy row Adam of the
+// value table):
+//
+//   select_backward_kernel   PKSelect.backward (smlm/kernels.py:253-266): the softmax backward of each head's knn
+//                            weights plus the scores' own gradient, rounded to the scores' dtype, scattered into
+//                            dense (N, H, NK) gradients of both halves (sums per sub-key in fp32, in selection
+//                            order, rounded once).  One wavefront per (token, head): the two dense rows are first
+//                            written as zeros with 16-byte stores, the wavefront waits until they are acknowledged,
+//                            then the lanes holding the first occurrence of a sub-key write its merged sum.
+//   bag_backward_kernel      the row-sparse bag backward (smlm/kernels.py:1-104, smlm/sparse_values.py:94-113):
+//                            acc[idx[n,k]] += w[n,k] * g[n], touched[idx[n,k]] = 1, and the per-sample-weight
+//                            gradient gw[n,k] = g[n] . table[idx[n,k]].  One workgroup per token, a wavefront per
+//                            lookup with its row's loads in flight for 4 lookups at a time; the accumulator rows
+//                            take hardware fp32 atomic adds (lane l owns columns l, l + 64, ...: each atomic
+//                            instruction covers 256 contiguous bytes), so rows read by several lookups need no
+//                            sort (the reference sorts the lookups and adds runs, with atomics at the borders).
+//   lazy_adam_kernel         the lazy Adam step of LazyRowAdam on the rows flagged in `touched` (smlm/kernels.py:
+//                            380-515): fp32 moments, or bf16 moments, or int8 companded moments with fp32 row
+//                            scales; afterwards the rows' accumulator is zero and their flag cleared.  One
+//                            wavefront per row; untouched rows cost one byte read.  No multiply-add contraction in
+//                            this file: the update is evaluated in the reference's operation order (its compact
+//                            kernel is compiled with fp fusion off), with IEEE division and square root.
+#include "pkm_common.h"
+
+#pragma clang fp contract(off)
+
+namespace smlm {
+namespace {
+
+constexpr int kTrainThreads = 256;
+constexpr int kTrainWaves = kTrainThreads / kWave;
+constexpr int kMaxD = 512;                  // columns per row: lane l owns l, l + 64, ... (at most 8 each)
+constexpr int kColsPerLane = kMaxD / kWave;
+constexpr int kBagInFlight = 4;             // lookups per wavefront whose row loads are issued together
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+template <bool F32>
+__device__ __forceinline__ float to_dtype(float x) {
+  return F32 ? x : round_bf16(x);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+template <bool F32>
+__global__ void __launch_bounds__(kTrainThreads)
+    select_backward_kernel(const int64_t *__restrict__ idx, const float *__restrict__ w, const void *__restrict__ g_scores,
+                           const float *__restrict__ g_w, int64_t rows, int NK, int knn, void *__restrict__ ds1,
+                           void *__restrict__ ds2) {
+  const int lane = lane_id();
+  const int64_t row = (int64_t)blockIdx.x * kTrainWaves + threadIdx.x / kWave;  // (n, h)
+  if (row >= rows) return;                                                       // wavefront-uniform
+  const bool have = lane < knn;
+  const int64_t o = row * knn + (have ? lane : 0);
+  const int64_t ix = have ? idx[o] : 0;
+  const float wk = have ? w[o] : 0.f;
+  float dl = 0.f;
+  if (g_w) {
+    const float gw = have ? g_w[o] : 0.f;
+    const float s = wave_sum_f32(wk * gw);
+    dl = wk * (gw - s);
+  }
+  if (g_scores) {
+    const float gs = !have ? 0.f
+                     : F32 ? ((const float *)g_scores)[o]
+                           : bf16_bits_to_f32(((const uint16_t *)g_scores)[o]);
+    dl = dl + gs;
+  }
+  const float ds = to_dtype<F32>(dl);
+  const int i1 = (int)(ix / NK), i2 = (int)(ix % NK);
+
+  // 1. both dense rows as zeros, 16 bytes per store
+  constexpr int EPV = F32 ? 4 : 8;            // elements per 16 bytes
+  const int chunks = NK / EPV;
+  char *r1 = (char *)ds1 + row * (int64_t)NK * (F32 ? 4 : 2);
+  char *r2 = (char *)ds2 + row * (int64_t)NK * (F32 ? 4 : 2);
+  for (int c = lane; c < chunks; c += kWave) {
+    *(uint4 *)(r1 + (int64_t)c * 16) = uint4{0u, 0u, 0u, 0u};
+    *(uint4 *)(r2 + (int64_t)c * 16) = uint4{0u, 0u, 0u, 0u};
+  }
+  // every zero store acknowledged before the first value store: the value then lands after the zero
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // 2. per sub-key: the sum of its selected pairs' gradients in selection order, by its first occurrence
+  float sum1 = 0.f, sum2 = 0.f;
+  bool first1 = have, first2 = have;
+  for (int j = 0; j < knn; ++j) {
+    const int j1 = __builtin_amdgcn_readlane(i1, j), j2 = __builtin_amdgcn_readlane(i2, j);
+    const float dj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ds), j));
+    if (j1 == i1) {
+      sum1 = sum1 + dj;
+      if (j < lane) first1 = false;
+    }
+    if (j2 == i2) {
+      sum2 = sum2 + dj;
+      if (j < lane) first2 = false;
+    }
+  }
+  // an index outside [0, NK^2) (not a selection's output) writes nothing
+  first1 = first1 && (unsigned)i1 < (unsigned)NK && ix >= 0;
+  first2 = first2 && (unsigned)i2 < (unsigned)NK && ix >= 0;
+  if constexpr (F32) {
+    if (first1) ((float *)r1)[i1] = sum1;
+    if (first2) ((float *)r2)[i2] = sum2;
+  } else {
+    if (first1) ((uint16_t *)r1)[i1] = (uint16_t)bf16_bits_rtne(sum1);
+    if (first2) ((uint16_t *)r2)[i2] = (uint16_t)bf16_bits_rtne(sum2);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+template <bool TABLE_F32>
+__device__ __forceinline__ float table_at(const void *table, int64_t off) {
+  if constexpr (TABLE_F32) return ((const float *)table)[off];
+  else return bf16_bits_to_f32(((const uint16_t *)table)[off]);
+}
+
+template <bool TABLE_F32, int CPL>
+__global__ void __launch_bounds__(kTrainThreads)
+    bag_backward_kernel(const float *__restrict__ grad_out, const int64_t *__restrict__ idx,
+                        const float *__restrict__ w, int K, const void *__restrict__ table, int64_t rows, int D,
+                        float *__restrict__ acc, uint8_t *__restrict__ touched, float *__restrict__ gw) {
+  const int64_t n = blockIdx.x;
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  float g[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    const int d = lane + kWave * e;
+    g[e] = d < D ? grad_out[n * D + d] : 0.f;
+  }
+  for (int k0 = wave * kBagInFlight; k0 < K; k0 += kTrainWaves * kBagInFlight) {
+    int64_t r[kBagInFlight];
+    float wk[kBagInFlight], t[kBagInFlight][CPL];
+    bool ok[kBagInFlight];
+#pragma unroll
+    for (int u = 0; u < kBagInFlight; ++u) {
+      const int k = k0 + u;
+      const bool live = k < K;                         // wavefront-uniform
+      const int64_t rr = live ? idx[n * K + k] : 0;
+      ok[u] = live && rr >= 0 && rr < rows;
+      r[u] = ok[u] ? rr : 0;
+      wk[u] = live ? w[n * K + k] : 0.f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int d = lane + kWave * e;
+        t[u][e] = d < D ? table_at<TABLE_F32>(table, r[u] * D + d) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBagInFlight; ++u) {
+      const int k = k0 + u;
+      if (k >= K) continue;
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) dot = fmaf(g[e], t[u][e], dot);
+      dot = wave_sum_f32(dot);
+      if (lane == 0) gw[n * K + k] = ok[u] ? dot : __builtin_nanf("");  // an index outside the table: NaN
+      if (!ok[u]) continue;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int d = lane + kWave * e;
+        if (d < D) unsafeAtomicAdd(acc + r[u] * D + d, wk[u] * g[e]);
+      }
+      if (lane == 0) touched[r[u]] = 1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// state: 0 fp32 moments, 1 bf16 moments, 2 int8 / uint8 codes + fp32 row scales
+template <int STATE, int CPL>
+__global__ void __launch_bounds__(kTrainThreads)
+    lazy_adam_kernel(float *__restrict__ p, void *__restrict__ m_ptr, void *__restrict__ v_ptr,
+                     float *__restrict__ m_scale, float *__restrict__ v_scale, float *__restrict__ acc,
+                     uint8_t *__restrict__ touched, const float *__restrict__ grad_scale, int64_t rows, int D,
+                     float step_size, float bc2_sqrt, float beta1, float beta2, float omb1, float omb2, float eps) {
+  const int lane = lane_id();
+  const float scale = *grad_scale;
+  for (int64_t row = (int64_t)blockIdx.x * kTrainWaves + threadIdx.x / kWave; row < rows;
+       row += (int64_t)gridDim.x * kTrainWaves) {
+    if (touched[row] == 0) continue;                   // wavefront-uniform: one wavefront per row
+    float g[CPL], m[CPL], v[CPL], pv[CPL];
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      const int d = lane + kWave * e;
+      const bool in = d < D;
+      const int64_t off = row * D + (in ? d : 0);
+      g[e] = in ? acc[off] * scale : 0.f;
+      pv[e] = in ? p[off] : 0.f;
+      if constexpr (STATE == 0) {
+        m[e] = in ? ((const float *)m_ptr)[off] : 0.f;
+        v[e] = in ? ((const float *)v_ptr)[off] : 0.f;
+      } else if constexpr (STATE == 1) {
+        m[e] = in ? bf16_bits_to_f32(((const uint16_t *)m_ptr)[off]) : 0.f;
+        v[e] = in ? bf16_bits_to_f32(((const uint16_t *)v_ptr)[off]) : 0.f;
+      } else {
+        m[e] = in ? (float)((const int8_t *)m_ptr)[off] : 0.f;
+        v[e] = in ? (float)((const uint8_t *)v_ptr)[off] : 0.f;
+      }
+    }
+    if constexpr (STATE == 2) {  // decode: m = sign * (c / 127)^2 * scale, v = ((c / 255) * scale)^4
+      const float ms = m_scale[row], vs = v_scale[row];
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        float mm = m[e] / 127.0f;
+        mm = (mm < 0.f ? -1.0f : 1.0f) * mm * mm * ms;
+        float vv = v[e] / 255.0f * vs;
+        vv = vv * vv;
+        vv = vv * vv;
+        m[e] = mm;
+        v[e] = vv;
+      }
+    }
+    float mq[CPL], vroot[CPL];
+    float mmax = 0.f, vmax = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      if constexpr (STATE == 0) {  // the fp32 kernel forms 1 - beta on the device
+        m[e] = beta1 * m[e] + (1.0f - beta1) * g[e];
+        v[e] = beta2 * v[e] + (1.0f - beta2) * g[e] * g[e];
+        pv[e] = pv[e] - step_size * m[e] / (sqrtf(v[e]) / bc2_sqrt + eps);
+      } else {
+        m[e] = beta1 * m[e] + omb1 * g[e];
+        v[e] = beta2 * v[e] + omb2 * g[e] * g[e];
+        const float denom = sqrtf(v[e]) / bc2_sqrt + eps;
+        pv[e] = pv[e] - (step_size * m[e]) / denom;
+      }
+      if constexpr (STATE == 2) {
+        const int d = lane + kWave * e;
+        vroot[e] = sqrtf(sqrtf(v[e]));
+        if (d < D) {
+          mmax = fmaxf(mmax, fabsf(m[e]));
+          vmax = fmaxf(vmax, vroot[e]);
+        }
+      }
+    }
+    if constexpr (STATE == 2) {  // encode against the row's largest |m| and v^(1/4)
+      mmax = wave_max_f32(mmax);
+      vmax = wave_max_f32(vmax);
+      const float md = mmax > 0.f ? mmax : 1.0f, vd = vmax > 0.f ? vmax : 1.0f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        float a = sqrtf(fabsf(m[e]) / md);
+        a = (m[e] < 0.f ? -1.0f : 1.0f) * a * 127.0f;
+        float b = vroot[e] / vd * 255.0f;
+        a = rintf(fminf(fmaxf(a, -127.0f), 127.0f));
+        b = rintf(fminf(fmaxf(b, 0.0f), 255.0f));
+        b = v[e] > 0.f ? fmaxf(b, 1.0f) : 0.0f;  // a positive second moment never gets a zero code
+        mq[e] = a;
+        vroot[e] = b;
+      }
+      if (lane == 0) {
+        m_scale[row] = mmax;
+        v_scale[row] = vmax;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      const int d = lane + kWave * e;
+      if (d >= D) continue;
+      const int64_t off = row * D + d;
+      p[off] = pv[e];
+      acc[off] = 0.f;
+      if constexpr (STATE == 0) {
+        ((float *)m_ptr)[off] = m[e];
+        ((float *)v_ptr)[off] = v[e];
+      } else if constexpr (STATE == 1) {
+        ((uint16_t *)m_ptr)[off] = (uint16_t)bf16_bits_rtne(m[e]);
+        ((uint16_t *)v_ptr)[off] = (uint16_t)bf16_bits_rtne(v[e]);
+      } else {
+        ((int8_t *)m_ptr)[off] = (int8_t)(int)mq[e];
+        ((uint8_t *)v_ptr)[off] = (uint8_t)(int)vroot[e];
+      }
+    }
+    if (lane == 0) touched[row] = 0;
+  }
+}
+
+template <int CPL>
+void launch_bag_backward(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
+                         const void *table, bool f32, int64_t rows, int D, float *acc, uint8_t *touched, float *gw,
+                         hipStream_t stream) {
+  if (f32)
+    hipLaunchKernelGGL((bag_backward_kernel<true, CPL>), dim3((unsigned)N), dim3(kTrainThreads), 0, stream, grad_out,
+                       idx, w, K, table, rows, D, acc, touched, gw);
+  else
+    hipLaunchKernelGGL((bag_backward_kernel<false, CPL>), dim3((unsigned)N), dim3(kTrainThreads), 0, stream,
+                       grad_out, idx, w, K, table, rows, D, acc, touched, gw);
+}
+
+template <int STATE>
+void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, uint8_t *touched,
+                 const float *grad_scale, int64_t rows, int D, float step_size, float bc2_sqrt, float b1, float b2,
+                 float omb1, float omb2, float eps, hipStream_t stream) {
+  int64_t blocks = (rows + kTrainWaves - 1) / kTrainWaves;
+  if (blocks > 65536) blocks = 65536;   // grid-stride beyond 262,144 rows at a time
+  const dim3 grid((unsigned)blocks), block(kTrainThreads);
+#define SMLM_ADAM(CPL)                                                                                         \
+  hipLaunchKernelGGL((lazy_adam_kernel<STATE, CPL>), grid, block, 0, stream, p, m, v, ms, vs, acc, touched,     \
+                     grad_scale, rows, D, step_size, bc2_sqrt, b1, b2, omb1, omb2, eps)
+  if (D <= 128) SMLM_ADAM(2);
+  else if (D <= 256) SMLM_ADAM(4);
+  else if (D <= 384) SMLM_ADAM(6);
+  else SMLM_ADAM(8);
+#undef SMLM_ADAM
+}
+
+bool aligned(const void *p, int a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+}  // namespace smlm
+
+extern "C" int smlm_pkm_select_backward(const int64_t *idx, const float *w, const void *g_scores, const float *g_w,
+                                        int dtype, int64_t N, int H, int NK, int knn, void *ds1, void *ds2,
+                                        void *stream) {
+  using namespace smlm;
+  if (!idx || !w || !ds1 || !ds2) return fail(SMLM_EINVAL, "smlm_pkm_select_backward: null idx, w, ds1 or ds2");
+  if (dtype != SMLM_BF16 && dtype != SMLM_F32)
+    return fail(SMLM_EINVAL, "smlm_pkm_select_backward: dtype must be SMLM_BF16 or SMLM_F32, got %d", dtype);
+  if (N < 0 || H < 1 || knn < 1 || knn > kWave || !is_pow2(NK) || NK > 65536 || NK < (dtype == SMLM_F32 ? 4 : 8))
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_backward: N=%lld H=%d NK=%d knn=%d (NK a power of two in "
+                "[8, 65536], knn <= 64)", (long long)N, H, NK, knn);
+  if (!aligned(ds1, 16) || !aligned(ds2, 16))
+    return fail(SMLM_EINVAL, "smlm_pkm_select_backward: ds1 and ds2 must be 16-byte aligned");
+  const int64_t rows = N * H;
+  if (rows == 0) return SMLM_OK;
+  const dim3 grid((unsigned)((rows + kTrainWaves - 1) / kTrainWaves)), block(kTrainThreads);
+  if (dtype == SMLM_F32)
+    hipLaunchKernelGGL((select_backward_kernel<true>), grid, block, 0, (hipStream_t)stream, idx, w, g_scores, g_w,
+                       rows, NK, knn, ds1, ds2);
+  else
+    hipLaunchKernelGGL((select_backward_kernel<false>), grid, block, 0, (hipStream_t)stream, idx, w, g_scores, g_w,
+                       rows, NK, knn, ds1, ds2);
+  return launch_status("smlm_pkm_select_backward");
+}
+
+extern "C" int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
+                                      const void *table, int table_dtype, int64_t rows, int D, float *acc,
+                                      uint8_t *touched, float *gw, void *stream) {
+  using namespace smlm;
+  if (!grad_out || !idx || !w || !table || !acc || !touched || !gw)
+    return fail(SMLM_EINVAL, "smlm_bag_backward_rows: null pointer argument");
+  if (table_dtype != SMLM_F32 && table_dtype != SMLM_BF16)
+    return fail(SMLM_EINVAL, "smlm_bag_backward_rows: the table must be SMLM_F32 or SMLM_BF16, got %d", table_dtype);
+  if (N < 0 || N > 0x7FFFFFFFLL || K < 1 || rows < 1 || D < 1 || D > kMaxD)
+    return fail(SMLM_EUNSUPPORTED, "smlm_bag_backward_rows: N=%lld K=%d rows=%lld D=%d (1 <= D <= %d)",
+                (long long)N, K, (long long)rows, D, kMaxD);
+  if (N == 0) return SMLM_OK;
+  const bool f32 = table_dtype == SMLM_F32;
+  hipStream_t s = (hipStream_t)stream;
+  if (D <= 128) launch_bag_backward<2>(grad_out, idx, w, N, K, table, f32, rows, D, acc, touched, gw, s);
+  else if (D <= 256) launch_bag_backward<4>(grad_out, idx, w, N, K, table, f32, rows, D, acc, touched, gw, s);
+  else if (D <= 384) launch_bag_backward<6>(grad_out, idx, w, N, K, table, f32, rows, D, acc, touched, gw, s);
+  else launch_bag_backward<8>(grad_out, idx, w, N, K, table, f32, rows, D, acc, touched, gw, s);
+  return launch_status("smlm_bag_backward_rows");
+}
+
+extern "C" int smlm_lazy_adam(float *param, void *exp_avg, void *exp_avg_sq, float *exp_avg_scale,
+                              float *exp_avg_sq_scale, int state, float *acc, uint8_t *touched,
+                              const float *grad_scale, int64_t rows, int D, float step_size, float bc2_sqrt,
+                              float beta1, float beta2, float one_minus_beta1, float one_minus_beta2, float eps,
+                              void *stream) {
+  using namespace smlm;
+  if (!param || !exp_avg || !exp_avg_sq || !acc || !touched || !grad_scale)
+    return fail(SMLM_EINVAL, "smlm_lazy_adam: null pointer argument");
+  if (state != SMLM_ADAM_F32 && state != SMLM_ADAM_BF16 && state != SMLM_ADAM_INT8)
+    return fail(SMLM_EINVAL, "smlm_lazy_adam: unknown moment storage %d", state);
+  if (state == SMLM_ADAM_INT8 && (!exp_avg_scale || !exp_avg_sq_scale))
+    return fail(SMLM_EINVAL, "smlm_lazy_adam: int8 moments need exp_avg_scale and exp_avg_sq_scale");
+  if (rows < 0 || D < 1 || D > kMaxD)
+    return fail(SMLM_EUNSUPPORTED, "smlm_lazy_adam: rows=%lld D=%d (1 <= D <= %d)", (long long)rows, D, kMaxD);
+  if (rows == 0) return SMLM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (state == SMLM_ADAM_F32)
+    launch_adam<0>(param, exp_avg, exp_avg_sq, exp_avg_scale, exp_avg_sq_scale, acc, touched, grad_scale, rows, D,
+                   step_size, bc2_sqrt, beta1, beta2, one_minus_beta1, one_minus_beta2, eps, s);
+  else if (state == SMLM_ADAM_BF16)
+    launch_adam<1>(param, exp_avg, exp_avg_sq, exp_avg_scale, exp_avg_sq_scale, acc, touched, grad_scale, rows, D,
+                   step_size, bc2_sqrt, beta1, beta2, one_minus_beta1, one_minus_beta2, eps, s);
+  else
+    launch_adam<2>(param, exp_avg, exp_avg_sq, exp_avg_scale, exp_avg_sq_scale, acc, touched, grad_scale, rows, D,
+                   step_size, bc2_sqrt, beta1, beta2, one_minus_beta1, one_minus_beta2, eps, s);
+  return launch_status("smlm_lazy_adam");
+}

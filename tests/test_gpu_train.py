@@ -1,0 +1,188 @@
+"""Training-side kernels against the CPU oracle (oracle/train_oracle.py, pinned in tests/test_train_oracle.py):
+selection backward (smlm_pkm_select_backward), row-sparse bag backward (smlm_bag_backward_rows) and the lazy row
+Adam (smlm_lazy_adam) with fp32, bf16 and int8 moments.
+
+Bars: the lazy Adam is bit-exact (same operation order, IEEE division and square root, no fused multiply-add).
+The selection backward is bit-exact up to the softmax backward's wavefront sum (the oracle sums w * g_w in
+numpy's order): bf16 outputs within one bf16 ulp and fp32 outputs within 1e-5 relative, and every element whose
+sub-key is not selected is exactly zero.  The bag backward's accumulator takes fp32 atomic adds in no fixed order:
+within 1e-5 of the summed magnitudes; the per-sample-weight gradient within 1e-5; the flags exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.train_oracle as T
+from smlm_hip import kernels as KR
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def _ulp_bf16(x):
+    return np.abs(T.round_to(x, True)) * 2.0 ** -7 + 2.0 ** -133
+
+
+@pytest.mark.parametrize("N,H,NK,knn,dtype,gs,gw", [
+    (5, 4, 2048, 32, torch.bfloat16, True, True),
+    (9, 4, 4096, 32, torch.bfloat16, False, True),
+    (3, 2, 64, 64, torch.float32, True, True),
+    (7, 3, 8, 8, torch.bfloat16, True, False),
+    (4, 4, 1024, 16, torch.float32, False, True),
+])
+def test_select_backward_matches_oracle(N, H, NK, knn, dtype, gs, gw):
+    note(f"select backward N={N} H={H} NK={NK} knn={knn} {dtype} g_scores={gs} g_w={gw}")
+    g = torch.Generator().manual_seed(N * NK + knn)
+    s1 = torch.randn(N, H, NK, generator=g).to(dtype).to(DEV)
+    s2 = torch.randn(N, H, NK, generator=g).to(dtype).to(DEV)
+    _, idx, w = KR.pk_select(s1, s2, knn)
+    G_s = torch.randn(N, H, knn, generator=g).to(dtype) if gs else None
+    G_w = torch.randn(N, H, knn, generator=g) if gw else None
+    ds1, ds2 = KR.pk_select_backward(idx, w, None if G_s is None else G_s.to(DEV),
+                                    None if G_w is None else G_w.to(DEV), NK, dtype)
+    torch.cuda.synchronize()
+    bf16 = dtype == torch.bfloat16
+    r1, r2 = T.select_backward(idx.cpu().numpy(), w.cpu().numpy(), None if G_s is None else G_s.float().numpy(),
+                               None if G_w is None else G_w.numpy(), NK, bf16)
+    i = idx.cpu().numpy()
+    for got, ref, sub in ((ds1, r1, i // NK), (ds2, r2, i % NK)):
+        got = got.float().cpu().numpy()
+        mask = np.zeros(got.shape, dtype=bool)
+        np.put_along_axis(mask, sub, True, axis=-1)
+        assert not got[~mask].any()                       # every unselected sub-key: exactly zero
+        if bf16:
+            assert np.all(np.abs(got - ref) <= _ulp_bf16(ref))
+            assert (got == ref).mean() > 0.97
+        else:
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-7)
+
+
+def test_pkselect_autograd_matches_oracle():
+    note("PKSelect autograd")
+    N, H, NK, knn = 6, 4, 512, 32
+    g = torch.Generator().manual_seed(11)
+    s1 = torch.randn(N, H, NK, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    s2 = torch.randn(N, H, NK, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    scores, idx, w = KR.PKSelect.apply(s1, s2, knn)
+    Gs = torch.randn(N, H, knn, generator=g).to(torch.bfloat16)
+    Gw = torch.randn(N, H, knn, generator=g)
+    ((scores.float() * Gs.float().to(DEV)).sum() + (w * Gw.to(DEV)).sum()).backward()
+    r1, r2 = T.select_backward(idx.cpu().numpy(), w.detach().cpu().numpy(), Gs.float().numpy(), Gw.numpy(), NK,
+                               True)
+    for got, ref in ((s1.grad, r1), (s2.grad, r2)):
+        assert got.dtype == torch.bfloat16
+        got = got.float().cpu().numpy()
+        assert np.all(np.abs(got - ref) <= _ulp_bf16(ref))
+
+
+@pytest.mark.parametrize("N,K,D,rows,tdtype", [(33, 128, 384, 1000, torch.float32), (5, 7, 100, 50, torch.float32),
+                                               (17, 64, 384, 300, torch.bfloat16), (3, 40, 512, 20, torch.float32)])
+def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype):
+    note(f"bag backward N={N} K={K} D={D} rows={rows} {tdtype}")
+    g = torch.Generator().manual_seed(N + K + D)
+    idx = torch.randint(0, rows, (N, K), generator=g)
+    idx[0, : min(K, 5)] = 1                                # a row read several times in a bag and across bags
+    idx[-1, 0] = 1
+    w = torch.rand(N, K, generator=g)
+    table = torch.randn(rows, D, generator=g).to(tdtype)
+    G = torch.randn(N, D, generator=g)
+    acc0 = torch.randn(rows, D, generator=g) * 0.1
+    t0 = torch.zeros(rows, dtype=torch.bool)
+    t0[rows - 1] = True
+    acc, touched = acc0.to(DEV), t0.to(DEV)
+    gw = KR.bag_backward_rows(G.to(DEV), idx.to(DEV), w.to(DEV), table.to(DEV), acc, touched)
+    torch.cuda.synchronize()
+    rgw, racc, rt = T.bag_backward_rows(G.numpy(), idx.numpy(), w.numpy(), table.float().numpy(), acc0.numpy(),
+                                        t0.numpy())
+    mag_gw = np.abs(G.numpy()) @ np.abs(table.float().numpy()).T
+    np.testing.assert_array_less(np.abs(gw.cpu().numpy() - rgw), 1e-5 * np.take_along_axis(mag_gw, idx.numpy(), 1)
+                                 + 1e-6)
+    mag = np.zeros((rows, D))
+    np.add.at(mag, idx.reshape(-1).numpy(), (np.abs(w.numpy())[..., None] * np.abs(G.numpy())[:, None]).reshape(
+        N * K, D))
+    np.testing.assert_array_less(np.abs(acc.cpu().numpy() - racc), 1e-5 * (mag + np.abs(acc0.numpy())) + 1e-7)
+    np.testing.assert_array_equal(touched.cpu().numpy(), rt)
+
+
+def test_bag_backward_rows_index_outside_table():
+    note("bag backward: index outside the table")
+    N, K, D, rows = 2, 3, 64, 10
+    idx = torch.tensor([[0, 10, 2], [3, -1, 3]])
+    acc = torch.zeros(rows, D, device=DEV)
+    touched = torch.zeros(rows, dtype=torch.bool, device=DEV)
+    gw = KR.bag_backward_rows(torch.ones(N, D, device=DEV), idx.to(DEV), torch.ones(N, K, device=DEV),
+                             torch.ones(rows, D, device=DEV), acc, touched)
+    gw = gw.cpu()
+    assert torch.isnan(gw[0, 1]) and torch.isnan(gw[1, 1]) and not torch.isnan(gw[:, [0, 2]]).any()
+    assert touched.cpu().nonzero().view(-1).tolist() == [0, 2, 3]
+    np.testing.assert_array_equal(acc.cpu().sum(1).numpy(), [64, 0, 64, 128, 0, 0, 0, 0, 0, 0])
+
+
+def _adam_case(rows, D, seed):
+    rng = np.random.default_rng(seed)
+    p = rng.standard_normal((rows, D)).astype(np.float32)
+    return rng, p
+
+
+@pytest.mark.parametrize("rows,D", [(300, 384), (40, 100), (64, 512)])
+def test_lazy_adam_fp32_bit_exact(rows, D):
+    note(f"lazy adam fp32 rows={rows} D={D}")
+    rng, p = _adam_case(rows, D, rows + D)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    P, M, V = (torch.from_numpy(a.copy()).to(DEV) for a in (p, m, v))
+    for step in range(1, 4):
+        acc = (rng.standard_normal((rows, D)) * 1e-2).astype(np.float32)
+        touched = rng.random(rows) < 0.6
+        scale = 0.7 if step == 2 else 1.0
+        A, Tt = torch.from_numpy(acc.copy()).to(DEV), torch.from_numpy(touched.copy()).to(DEV)
+        KR.lazy_adam_step(P, M, V, A, Tt, torch.tensor(scale), step, 1e-3, 0.9, 0.95, 1e-8)
+        p, m, v, acc_r, t_r = T.lazy_adam(p, m, v, acc, touched, scale, step, 1e-3, 0.9, 0.95, 1e-8)
+        torch.cuda.synchronize()
+        for got, ref in ((P, p), (M, m), (V, v), (A, acc_r)):
+            np.testing.assert_array_equal(got.cpu().numpy(), ref)
+        assert not Tt.cpu().any()
+
+
+@pytest.mark.parametrize("state,rows,D", [("bf16", 200, 384), ("int8", 200, 384), ("int8", 33, 100)])
+def test_lazy_adam_lowmem_bit_exact(state, rows, D):
+    note(f"lazy adam {state} rows={rows} D={D}")
+    rng, p = _adam_case(rows, D, 7 * rows + D)
+    int8 = state == "int8"
+    if int8:
+        m, v = np.zeros((rows, D), np.int8), np.zeros((rows, D), np.uint8)
+        ms, vs = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+        M = torch.zeros(rows, D, dtype=torch.int8, device=DEV)
+        V = torch.zeros(rows, D, dtype=torch.uint8, device=DEV)
+        MS, VS = torch.zeros(rows, device=DEV), torch.zeros(rows, device=DEV)
+    else:
+        m, v = np.zeros((rows, D), np.float32), np.zeros((rows, D), np.float32)
+        ms = vs = None
+        M = torch.zeros(rows, D, dtype=torch.bfloat16, device=DEV)
+        V = torch.zeros(rows, D, dtype=torch.bfloat16, device=DEV)
+        MS = VS = None
+    P = torch.from_numpy(p.copy()).to(DEV)
+    for step in range(1, 5):
+        acc = (rng.standard_normal((rows, D)) * 1e-2).astype(np.float32)
+        acc[0] = 0.0                                       # a touched row with a zero gradient
+        touched = rng.random(rows) < 0.7
+        touched[0] = True
+        A, Tt = torch.from_numpy(acc.copy()).to(DEV), torch.from_numpy(touched.copy()).to(DEV)
+        KR.lazy_adam_step_lowmem(P, M, V, A, Tt, 1.0, step, 1e-3, 0.9, 0.95, 1e-8, state, MS, VS)
+        p, m, v, ms, vs, acc_r, _ = T.lazy_adam_lowmem(p, m, v, ms, vs, acc, touched, 1.0, step, 1e-3, 0.9, 0.95,
+                                                       1e-8, int8)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(P.cpu().numpy(), p)
+        np.testing.assert_array_equal(A.cpu().numpy(), acc_r)
+        if int8:
+            np.testing.assert_array_equal(M.cpu().numpy(), m)
+            np.testing.assert_array_equal(V.cpu().numpy(), v)
+            np.testing.assert_array_equal(MS.cpu().numpy(), ms)
+            np.testing.assert_array_equal(VS.cpu().numpy(), vs)
+        else:
+            np.testing.assert_array_equal(M.float().cpu().numpy(), m)
+            np.testing.assert_array_equal(V.float().cpu().numpy(), v)
+        assert not Tt.cpu().any()
