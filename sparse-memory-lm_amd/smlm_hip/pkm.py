@@ -6,7 +6,13 @@ graph switch), whose lookup runs on the gfx950 kernels of smlm_hip.kernels:
     -> bag_infer (value gather, swilu epilogue, bf16 out) -> value_proj
 
 impl="hip" is the only implementation here; the reference's "torch" and "triton" implementations stay in the
-reference package.  The module is inference-only: a forward that autograd would record raises.
+reference package.
+
+A forward that autograd records (training) takes the reference's differentiable path with the HIP kernels where the
+reference uses its Triton ones (smlm/pkm.py:186-228): torch query projection and BatchNorm, sub-key scores by
+torch.einsum (its backward is two library GEMMs), the selection and its backward on the kernels (kernels.PKSelect),
+and the values through the row-sparse bag (smlm_hip.sparse_values: fp32 accumulator + touched flags for
+LazyRowAdam) or, with value_grad="dense", F.embedding_bag.
 """
 import math
 
@@ -15,6 +21,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import kernels
+from .sparse_values import row_sparse_embedding_bag
 
 
 def _pow2(n):
@@ -204,10 +211,43 @@ class ProductKeyMemory(nn.Module):
             self._bn_cache = (tag, scale, shift)
         return self._bn_cache[1], self._bn_cache[2]
 
+    def _train_forward(self, x):
+        """The differentiable lookup (smlm/pkm.py:186-228 with impl="triton"): the kernels' selection with its
+        backward (kernels.PKSelect), row-sparse or dense value gradients."""
+        N = x.shape[0]
+        q = self.query_proj(x)
+        if self.query_norm is not None:
+            q = self.query_norm(q.to(self.query_norm.weight.dtype))     # BN in fp32 under autocast
+        q = q.view(N, self.heads, self.k_dim)
+        if _autocast_bf16(x):
+            q = q.to(torch.bfloat16)
+        half = self.k_dim // 2
+        k1, k2 = self.keys[:, 0], self.keys[:, 1]
+        s1 = torch.einsum("nhd,hkd->nhk", q[..., :half], k1)
+        s2 = torch.einsum("nhd,hkd->nhk", q[..., half:], k2)
+        if s1.dtype not in (torch.bfloat16, torch.float32):
+            s1, s2 = s1.float(), s2.float()
+        scores, indices, weights = kernels.PKSelect.apply(s1, s2, self.knn)
+        if self.log_score_scale is not None:
+            logits = scores.float() * self.log_score_scale.float().exp().view(1, self.heads, 1)
+            weights = torch.softmax(logits, dim=-1)
+        if self.record:
+            self.last_indices = indices.detach()
+            self.last_scores = scores.detach()
+            self.last_weights = weights.detach()
+        idx, w = indices.view(N, -1), weights.view(N, -1)
+        table = self.values.weight
+        if self.value_grad == "row_sparse":
+            out = row_sparse_embedding_bag(idx, w, table, "hip")
+        else:
+            out = F.embedding_bag(idx, table, per_sample_weights=w.to(table.dtype), mode="sum")
+        if self.swilu:
+            out = self.value_proj(out * F.silu(self.swilu_proj(x)).to(out.dtype))
+        return out
+
     def _forward(self, x):
         if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())):
-            raise NotImplementedError("smlm_hip implements the inference lookup only: run the forward under "
-                                      "torch.no_grad() / torch.inference_mode()")
+            return self._train_forward(x)
         N = x.shape[0]
         bf16 = _autocast_bf16(x) or x.dtype == torch.bfloat16
         sdt = torch.bfloat16 if (bf16 or self.keys.dtype == torch.bfloat16) else torch.float32

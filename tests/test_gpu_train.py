@@ -186,3 +186,69 @@ def test_lazy_adam_lowmem_bit_exact(state, rows, D):
             np.testing.assert_array_equal(M.float().cpu().numpy(), m)
             np.testing.assert_array_equal(V.float().cpu().numpy(), v)
         assert not Tt.cpu().any()
+
+
+def _ref_grads(mem, x, G, idx):
+    """fp64 CPU autograd of the layer given the kernels' selection idx: q = x Wq^T + b, s1/s2 = einsum, scores =
+    gathered sums, softmax, embedding_bag (smlm/pkm.py:117-148, 186-228)."""
+    sd = {k: v.detach().double().cpu().requires_grad_(True) for k, v in mem.named_parameters()}
+    xd = x.double().cpu()
+    N = xd.shape[0]
+    H, kd, NK = mem.heads, mem.k_dim, mem.n_keys
+    q = (xd @ sd["query_proj.weight"].T + sd["query_proj.bias"]).view(N, H, kd)
+    s1 = torch.einsum("nhd,hkd->nhk", q[..., :kd // 2], sd["keys"][:, 0])
+    s2 = torch.einsum("nhd,hkd->nhk", q[..., kd // 2:], sd["keys"][:, 1])
+    i = idx.cpu()
+    scores = s1.gather(-1, i // NK) + s2.gather(-1, i % NK)
+    w = torch.softmax(scores, -1)
+    out = torch.nn.functional.embedding_bag(i.view(N, -1), sd["values.weight"], per_sample_weights=w.view(N, -1),
+                                            mode="sum")
+    (out * G.double().cpu()).sum().backward()
+    return {k: v.grad for k, v in sd.items()}
+
+
+@pytest.mark.parametrize("value_grad", ["row_sparse", "dense"])
+def test_layer_training_step_matches_fp64_autograd(value_grad):
+    """A training forward + backward of ProductKeyMemory (fp32, no BatchNorm, no swilu) on the kernels: query /
+    key gradients through the selection backward and the einsum, value gradients in the row store (row_sparse) or
+    as a dense .grad, against fp64 autograd on the CPU given the same selection; then one LazyRowAdam step equals
+    the oracle on the accumulated rows."""
+    from smlm_hip.pkm import ProductKeyMemory
+    from smlm_hip.sparse_values import LazyRowAdam, row_store
+    note(f"layer training step value_grad={value_grad}")
+    torch.manual_seed(0)
+    N, d, H, kd, NK, knn = 48, 32, 2, 32, 64, 8
+    mem = ProductKeyMemory(d, d, n_keys=NK, heads=H, knn=knn, k_dim=kd, query_norm="none", swilu=False,
+                           value_grad=value_grad).to(DEV).train()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(N, d, generator=g).to(DEV)
+    G = torch.randn(N, d, generator=g)
+    mem.record = True
+    out = mem(x)
+    (out * G.to(DEV)).sum().backward()
+    idx = mem.last_indices
+    ref = _ref_grads(mem, x, G, idx)
+    for name in ("query_proj.weight", "query_proj.bias", "keys"):
+        got = dict(mem.named_parameters())[name].grad.double().cpu()
+        scale = ref[name].abs().max()
+        assert float((got - ref[name]).abs().max()) <= 1e-5 * float(scale), name
+    table = mem.values.weight
+    if value_grad == "dense":
+        assert float((table.grad.double().cpu() - ref["values.weight"]).abs().max()) <= 1e-6
+        return
+    assert table.grad is None
+    st = row_store(table)
+    acc = st.acc.double().cpu()
+    assert float((acc - ref["values.weight"]).abs().max()) <= 1e-6
+    expect = torch.zeros(NK * NK, dtype=torch.bool)
+    expect[idx.reshape(-1).cpu()] = True
+    assert torch.equal(st.touched.cpu(), expect)
+    p0, acc0, t0 = table.detach().cpu().numpy().copy(), st.acc.cpu().numpy().copy(), st.touched.cpu().numpy()
+    opt = LazyRowAdam([table], lr=1e-2)
+    opt.step()
+    torch.cuda.synchronize()
+    z = np.zeros_like(p0)
+    p1, m1, v1, _, _ = T.lazy_adam(p0, z, z, acc0, t0, 1.0, 1, 1e-2, 0.9, 0.95, 1e-8)
+    np.testing.assert_array_equal(table.detach().cpu().numpy(), p1)
+    np.testing.assert_array_equal(opt.state[table]["exp_avg"].cpu().numpy(), m1)
+    assert not st.touched.any() and not st.acc.any()
