@@ -16,6 +16,9 @@ HBM GB/s".
   pkm_lookup     config 2 (B-4M, 8 x 2048 tokens): scoring + selection + value bag kernels, tokens / time.
   gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out;
                  algorithmic bytes 3,439,329,280 per call; plus a uniform-index control.
+  train_kernels  the training side at the reference's training shape (4,096 tokens x 128 lookups per micro-batch,
+                 B-1M fp32 table): row-sparse bag backward, lazy row Adam (fp32 / bf16 / int8 moments) on the
+                 rows of a 32,768-token step, selection backward at config 2; algorithmic GB/s each.
   roofline       the config-4 gather kernel against HBM peak (8 TB/s), timed with HIP events on the stream it
                  is launched on; roofline_score: the config-2 scoring kernel against the bf16 MFMA peak.
   cpu_baseline   the reference's PyTorch path on the host CPU (oracle/torch_path.py), config 3 at batch 64,
@@ -194,6 +197,88 @@ def lookup_prefill(dev, reps):
     return res
 
 
+def event_time_each_ms(prep, fn, reps):
+    """Average device time of fn() in ms over `reps` calls, each bracketed by its own HIP events so that prep()
+    (state reset between calls) stays outside the timed intervals."""
+    import torch
+    prep()
+    fn()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in pairs:
+        prep()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / reps
+
+
+def train_kernels(dev, reps):
+    """The training side of the lookup at the reference's training shape (one micro-batch = 4 x 1024 tokens, 4
+    heads x top-32 = 128 lookups per token, B-1M fp32 value table 1,048,576 x 384): the row-sparse bag backward on
+    uniform and Zipf(1.1) indices, the lazy row Adam (fp32 / bf16 / int8 moments) on the rows a 32,768-token step
+    (8 micro-batches) reads, and the selection backward at config 2 (8 x 2048 tokens, NK 2048, bf16 scores).
+    Algorithmic bytes are the least any implementation moves: every distinct row read or written once."""
+    import torch
+    from smlm_hip import kernels as K
+    rows, D, N, Kl = 1 << 20, 384, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    table = torch.empty(rows, D, device=dev).normal_(0.0, 0.02, generator=g)
+    acc = torch.zeros(rows, D, device=dev)
+    touched = torch.zeros(rows, dtype=torch.bool, device=dev)
+    gout = torch.randn(N, D, generator=g, device=dev)
+    w = torch.softmax(torch.randn(N, 4, 32, generator=g, device=dev), -1).view(N, Kl)
+    res = {"shape": "4,096 tokens x 128 lookups, table 1,048,576 x 384 fp32 (B-1M)"}
+    for name, idx in (("uniform", torch.randint(0, rows, (N, Kl), generator=g, device=dev)),
+                      ("zipf", zipf_rows(N * Kl, rows, 1.1, g, dev).view(N, Kl))):
+        distinct = int(torch.unique(idx).numel())
+        alg = N * Kl * (8 + 4 + 4) + N * D * 4 + distinct * (3 * D * 4 + 1)
+        ms = event_time_ms(lambda: K.bag_backward_rows(gout, idx, w, table, acc, touched), reps)
+        res[f"bag_backward_{name}"] = {"ms": ms, "distinct_rows": distinct, "alg_bytes": alg,
+                                       "alg_GBps": alg / ms / 1e6}
+    del acc, gout, w
+    # rows read by a 32,768-token step: 8 micro-batches of uniform lookups
+    mask = torch.zeros(rows, dtype=torch.bool, device=dev)
+    mask[torch.randint(0, rows, (8 * N * Kl,), generator=g, device=dev)] = True
+    hot = int(mask.sum())
+    acc = torch.randn(rows, D, generator=g, device=dev) * 1e-3
+    per_row = {"fp32": 8 * D * 4, "bf16": D * (8 + 4 + 4 + 8), "int8": D * (8 + 2 + 2 + 8) + 16}
+    for sd in ("fp32", "bf16", "int8"):
+        if sd == "fp32":
+            m, v = torch.zeros_like(table), torch.zeros_like(table)
+            step = lambda: K.lazy_adam_step(table, m, v, acc, touched, 1.0, 1, 1e-3, 0.9, 0.95, 1e-8)
+        elif sd == "bf16":
+            m = torch.zeros(rows, D, dtype=torch.bfloat16, device=dev)
+            v = torch.zeros_like(m)
+            step = lambda: K.lazy_adam_step_lowmem(table, m, v, acc, touched, 1.0, 1, 1e-3, 0.9, 0.95, 1e-8, "bf16")
+        else:
+            m = torch.zeros(rows, D, dtype=torch.int8, device=dev)
+            v = torch.zeros(rows, D, dtype=torch.uint8, device=dev)
+            ms_, vs_ = torch.zeros(rows, device=dev), torch.zeros(rows, device=dev)
+            step = lambda: K.lazy_adam_step_lowmem(table, m, v, acc, touched, 1.0, 1, 1e-3, 0.9, 0.95, 1e-8, "int8",
+                                                   ms_, vs_)
+        ms = event_time_each_ms(lambda: touched.copy_(mask), step, reps)
+        alg = rows + hot * (per_row[sd] + 1)
+        res[f"lazy_adam_{sd}"] = {"ms": ms, "touched_rows": hot, "alg_bytes": alg, "alg_GBps": alg / ms / 1e6}
+        del m, v
+    del table, acc, touched, mask
+    torch.cuda.empty_cache()
+    Ns, H, NK, knn = 8 * 2048, 4, 2048, 32
+    s1 = torch.randn(Ns, H, NK, generator=g, device=dev).to(torch.bfloat16)
+    s2 = torch.randn(Ns, H, NK, generator=g, device=dev).to(torch.bfloat16)
+    _, idx, wsel = K.pk_select(s1, s2, knn)
+    del s1, s2
+    gs = torch.randn(Ns, H, knn, generator=g, device=dev).to(torch.bfloat16)
+    gw = torch.randn(Ns, H, knn, generator=g, device=dev)
+    ms = event_time_ms(lambda: K.pk_select_backward(idx, wsel, gs, gw, NK, torch.bfloat16), reps)
+    alg = Ns * H * knn * (8 + 4 + 2 + 4) + 2 * Ns * H * NK * 2
+    res["select_backward_config2"] = {"ms": ms, "alg_bytes": alg, "alg_GBps": alg / ms / 1e6}
+    del idx, wsel, gs, gw
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(model, B, max_steps, budget_s):
     """The reference's torch path (oracle/torch_path.py) on the host cores: config 3 at batch B, 128-token
     prompts, then greedy decode steps (fp32 weights, the bf16 table read by row gather), timed until
@@ -261,8 +346,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,cpu",
-                    help="subset of decode,config1,prefill,lookup,gather,cpu,calibrate (profiling runs); the JSON "
+    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,cpu",
+                    help="subset of decode,config1,prefill,lookup,gather,train,cpu,calibrate (profiling runs); the JSON "
                          "line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -312,13 +397,19 @@ def main():
         log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
         del m2
         torch.cuda.empty_cache()
-    lk = ga = cpu = None
+    lk = ga = tr = cpu = None
     if "lookup" in phases:
         lk = lookup_prefill(dev, args.reps)
         log(f"lookup config 2: {lk}")
     if "gather" in phases:
         ga = gather_stress(dev, args.reps)
         log(f"gather config 4: {ga}")
+    if "train" in phases:
+        tr = train_kernels(dev, args.reps)
+        for k, v in tr.items():
+            if isinstance(v, dict):
+                v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
+        log(f"training kernels: {tr}")
     if "cpu" in phases:
         t0 = time.perf_counter()
         cpu = cpu_baseline(model, 64, args.cpu_steps, args.cpu_seconds)
@@ -349,7 +440,7 @@ def main():
                    "new_tokens": args.steps},
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
         "decode_config1_bs1": c1, "prefill_config2": pf,
-        "pkm_lookup_config2": lk, "gather_config4": ga,
+        "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
         "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -59,4 +59,33 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v of lane ^ J (J < 64) on every lane: quad permutes (1, 2), row shifts by 4 either way (4), a row rotation (8),
+// and the gfx950 permlane swaps (16, 32), which given a register twice return v[lane] and v[lane ^ J] in some order.
+template <int J>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+  const int lane = lane_id();
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  } else if constexpr (J == 4) {  // row_shl:4 (lane i reads i + 4) or row_shr:4 (i - 4), both inside the row
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
+    return (lane & 4) ? dn : up;
+  } else if constexpr (J == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? (uint32_t)p[0] : (uint32_t)p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? (uint32_t)p[0] : (uint32_t)p[1];
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+  return (uint64_t)xor_lane<J>((uint32_t)v) | ((uint64_t)xor_lane<J>((uint32_t)(v >> 32)) << 32);
+}
+
 }  // namespace smlm

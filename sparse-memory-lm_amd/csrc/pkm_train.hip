@@ -174,41 +174,253 @@ __global__ void __launch_bounds__(kTrainThreads)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// state: 0 fp32 moments, 1 bf16 moments, 2 int8 / uint8 codes + fp32 row scales
-template <int STATE, int CPL>
+// The bag backward with the lookups of a few tokens grouped by table row first: 512 lookups per workgroup (T = 512
+// / K tokens, fewer where T x D gradients exceed the LDS stage), sorted in the workgroup by (row, lookup) with a
+// bitonic network over its 512 threads (distances below 64 by lane exchange, the rest through LDS).  Each
+// wavefront then owns 64 consecutive sorted lookups and walks the runs of equal rows among them: one table-row read
+// per run, the run's sum of w x g in registers and ONE set of atomic adds per run, so a row read by many tokens
+// (Zipf-skewed indices) costs one atomic per run instead of one per lookup.  Runs keep the lookups' order, so
+// the in-register sum adds the products in lookup order.
+constexpr int kSortEntries = 512;
+constexpr int kSortThreads = kSortEntries;  // one key per thread
+constexpr int kSortShift = 9;               // key = row << 9 | lookup slot
+constexpr int kStageFloats = 4096;          // LDS for the T x D staged token gradients (16 KB)
+constexpr int kRunsInFlight = 4;            // runs per wavefront whose table-row loads are issued together
+constexpr uint64_t kNoKey = ~0ull;          // padding and lookups outside the table sort last
+
+// one compare-exchange of an ascending bitonic sort over the workgroup's threads (block K, distance J)
+template <int K, int J>
+__device__ __forceinline__ uint64_t sort_step(uint64_t key, uint64_t *sKey, int t) {
+  uint64_t other;
+  if constexpr (J >= kWave) {
+    sKey[t] = key;
+    __syncthreads();
+    other = sKey[t ^ J];
+    __syncthreads();
+  } else {
+    other = xor_lane64<J>(key);
+  }
+  const bool keep_min = ((t & J) == 0) == ((t & K) == 0);
+  const uint64_t lo = key < other ? key : other, hi = key < other ? other : key;
+  return keep_min ? lo : hi;
+}
+
+template <int K, int J>
+__device__ __forceinline__ uint64_t sort_merge(uint64_t key, uint64_t *sKey, int t) {
+  key = sort_step<K, J>(key, sKey, t);
+  if constexpr (J > 1) return sort_merge<K, J / 2>(key, sKey, t);
+  else return key;
+}
+
+template <int K>
+__device__ __forceinline__ uint64_t sort_keys(uint64_t key, uint64_t *sKey, int t) {
+  key = sort_merge<K, K / 2>(key, sKey, t);
+  if constexpr (K < kSortEntries) return sort_keys<K * 2>(key, sKey, t);
+  else return key;
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+template <bool TABLE_F32, int CPL>
+__global__ void __launch_bounds__(kSortThreads)
+    bag_backward_sorted_kernel(const float *__restrict__ grad_out, const int64_t *__restrict__ idx,
+                               const float *__restrict__ w, int64_t N, int K, int T,
+                               const void *__restrict__ table, int64_t rows, int D, float *__restrict__ acc,
+                               uint8_t *__restrict__ touched, float *__restrict__ gw) {
+  __shared__ float sG[kStageFloats];
+  __shared__ uint64_t sKey[kSortEntries];
+  __shared__ float sW[kSortEntries], sGW[kSortEntries];
+  const int t = threadIdx.x, lane = lane_id();
+  const int64_t n0 = (int64_t)blockIdx.x * T;
+  const int nT = (int)(N - n0 < T ? N - n0 : T);
+  const int E = nT * K;                       // <= 512
+  const int64_t e0 = n0 * K;
+  for (int i = t; i < nT * D; i += kSortThreads) sG[i] = grad_out[n0 * D + i];
+  uint64_t key = kNoKey;
+  if (t < E) {
+    const int64_t r = idx[e0 + t];
+    sW[t] = w[e0 + t];
+    if (r >= 0 && r < rows) key = ((uint64_t)r << kSortShift) | (uint64_t)t;
+    else sGW[t] = __builtin_nanf("");         // an index outside the table: NaN weight gradient, no update
+  }
+  key = sort_keys<2>(key, sKey, t);
+  __syncthreads();                            // staged gradients and weights visible to every wavefront
+
+  const bool valid = key != kNoKey;
+  const int64_t row = (int64_t)(key >> kSortShift);
+  const int slot = (int)(key & (kSortEntries - 1));
+  // the previous lane's row (lane 0 starts a run by definition)
+  const uint32_t plo = (uint32_t)__shfl_up((int)(uint32_t)row, 1, kWave);
+  const uint32_t phi = (uint32_t)__shfl_up((int)(uint32_t)((uint64_t)row >> 32), 1, kWave);
+  const int64_t prow = (int64_t)(((uint64_t)phi << 32) | plo);
+  uint64_t heads = ballot(valid && (lane == 0 || prow != row));
+  const int nvalid = __popcll(ballot(valid));  // valid keys precede the padding
+  const int my_n = valid ? slot / K : 0;
+  const float my_w = valid ? sW[slot] : 0.f;
+
+  while (heads) {
+    int h[kRunsInFlight], end[kRunsInFlight];
+    int64_t r[kRunsInFlight];
+    float tv[kRunsInFlight][CPL];
+#pragma unroll
+    for (int u = 0; u < kRunsInFlight; ++u) {
+      h[u] = heads ? __builtin_ctzll(heads) : kWave;
+      heads = heads ? heads & (heads - 1) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kRunsInFlight; ++u) {
+      const int nxt = u + 1 < kRunsInFlight ? h[u + 1] : (heads ? __builtin_ctzll(heads) : kWave);
+      end[u] = nxt < kWave ? nxt : nvalid;
+      r[u] = h[u] < kWave ? readlane64(row, h[u]) : 0;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int d = lane + kWave * e;
+        tv[u][e] = (h[u] < kWave && d < D) ? table_at<TABLE_F32>(table, r[u] * D + d) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRunsInFlight; ++u) {
+      if (h[u] >= kWave) break;               // wavefront-uniform
+      float s[CPL];
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) s[e] = 0.f;
+      for (int j = h[u]; j < end[u]; ++j) {
+        const int nj = __builtin_amdgcn_readlane(my_n, j);
+        const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_w), j));
+        const float *g = sG + nj * D;
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) {
+          const int d = lane + kWave * e;
+          const float gv = d < D ? g[d] : 0.f;
+          dot = fmaf(gv, tv[u][e], dot);
+          s[e] = s[e] + wj * gv;
+        }
+        dot = wave_sum_f32(dot);
+        if (lane == 0) sGW[__builtin_amdgcn_readlane(slot, j)] = dot;
+      }
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int d = lane + kWave * e;
+        if (d < D) unsafeAtomicAdd(acc + r[u] * D + d, s[e]);
+      }
+      if (lane == 0) touched[r[u]] = 1;
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < E; i += kSortThreads) gw[e0 + i] = sGW[i];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// state: 0 fp32 moments, 1 bf16 moments, 2 int8 / uint8 codes + fp32 row scales.  Column layout of a row in its
+// wavefront: chunk c, lane l, element i holds column c * 64 * V + l * V + i.  V = 4 (D a multiple of 4) gives each
+// lane 16-byte fp32, 8-byte bf16 and 4-byte int8 accesses; V = 1 is the fallback for other widths.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+template <int V>
+__device__ __forceinline__ void load_f32v(const float *q, bool in, float *x) {
+  if constexpr (V == 4) {
+    const f32x4 t = in ? *(const f32x4 *)q : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = t[i];
+  } else {
+    x[0] = in ? *q : 0.f;
+  }
+}
+template <int V>
+__device__ __forceinline__ void store_f32v(float *q, const float *x) {
+  if constexpr (V == 4) *(f32x4 *)q = f32x4{x[0], x[1], x[2], x[3]};
+  else *q = x[0];
+}
+template <int V>
+__device__ __forceinline__ void load_bf16v(const uint16_t *q, bool in, float *x) {
+  if constexpr (V == 4) {
+    const u32x2 t = in ? *(const u32x2 *)q : u32x2{0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = bf16_bits_to_f32((t[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
+  } else {
+    x[0] = in ? bf16_bits_to_f32(*q) : 0.f;
+  }
+}
+template <int V>
+__device__ __forceinline__ void store_bf16v(uint16_t *q, const float *x) {
+  if constexpr (V == 4) {
+    *(u32x2 *)q = u32x2{bf16_bits_rtne(x[0]) | (bf16_bits_rtne(x[1]) << 16),
+                        bf16_bits_rtne(x[2]) | (bf16_bits_rtne(x[3]) << 16)};
+  } else {
+    *q = (uint16_t)bf16_bits_rtne(x[0]);
+  }
+}
+// int8 first-moment codes (signed) or uint8 second-moment codes, as floats
+template <int V, bool SIGNED>
+__device__ __forceinline__ void load_codes(const uint8_t *q, bool in, float *x) {
+  if constexpr (V == 4) {
+    const uint32_t t = in ? *(const uint32_t *)q : 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = (t >> (8 * i)) & 0xFFu;
+      x[i] = SIGNED ? (float)(int8_t)c : (float)c;
+    }
+  } else {
+    x[0] = !in ? 0.f : SIGNED ? (float)*(const int8_t *)q : (float)*q;
+  }
+}
+template <int V>
+__device__ __forceinline__ void store_codes(uint8_t *q, const float *x) {
+  if constexpr (V == 4) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t |= ((uint32_t)(int)x[i] & 0xFFu) << (8 * i);
+    *(uint32_t *)q = t;
+  } else {
+    *q = (uint8_t)(int)x[0];
+  }
+}
+
+template <int STATE, int V, int NC>
 __global__ void __launch_bounds__(kTrainThreads)
     lazy_adam_kernel(float *__restrict__ p, void *__restrict__ m_ptr, void *__restrict__ v_ptr,
                      float *__restrict__ m_scale, float *__restrict__ v_scale, float *__restrict__ acc,
                      uint8_t *__restrict__ touched, const float *__restrict__ grad_scale, int64_t rows, int D,
                      float step_size, float bc2_sqrt, float beta1, float beta2, float omb1, float omb2, float eps) {
+  constexpr int L = V * NC;                   // columns per lane
   const int lane = lane_id();
   const float scale = *grad_scale;
   for (int64_t row = (int64_t)blockIdx.x * kTrainWaves + threadIdx.x / kWave; row < rows;
        row += (int64_t)gridDim.x * kTrainWaves) {
     if (touched[row] == 0) continue;                   // wavefront-uniform: one wavefront per row
-    float g[CPL], m[CPL], v[CPL], pv[CPL];
+    float g[L], m[L], v[L], pv[L];
+    bool in[NC];
+    int64_t off[NC];
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-      const int d = lane + kWave * e;
-      const bool in = d < D;
-      const int64_t off = row * D + (in ? d : 0);
-      g[e] = in ? acc[off] * scale : 0.f;
-      pv[e] = in ? p[off] : 0.f;
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = c * kWave * V + lane * V;
+      in[c] = d0 < D;                                  // D % V == 0: all V columns in or all out
+      off[c] = row * D + (in[c] ? d0 : 0);
+      load_f32v<V>(acc + off[c], in[c], g + c * V);
+      load_f32v<V>(p + off[c], in[c], pv + c * V);
       if constexpr (STATE == 0) {
-        m[e] = in ? ((const float *)m_ptr)[off] : 0.f;
-        v[e] = in ? ((const float *)v_ptr)[off] : 0.f;
+        load_f32v<V>((const float *)m_ptr + off[c], in[c], m + c * V);
+        load_f32v<V>((const float *)v_ptr + off[c], in[c], v + c * V);
       } else if constexpr (STATE == 1) {
-        m[e] = in ? bf16_bits_to_f32(((const uint16_t *)m_ptr)[off]) : 0.f;
-        v[e] = in ? bf16_bits_to_f32(((const uint16_t *)v_ptr)[off]) : 0.f;
+        load_bf16v<V>((const uint16_t *)m_ptr + off[c], in[c], m + c * V);
+        load_bf16v<V>((const uint16_t *)v_ptr + off[c], in[c], v + c * V);
       } else {
-        m[e] = in ? (float)((const int8_t *)m_ptr)[off] : 0.f;
-        v[e] = in ? (float)((const uint8_t *)v_ptr)[off] : 0.f;
+        load_codes<V, true>((const uint8_t *)m_ptr + off[c], in[c], m + c * V);
+        load_codes<V, false>((const uint8_t *)v_ptr + off[c], in[c], v + c * V);
       }
     }
+#pragma unroll
+    for (int e = 0; e < L; ++e) g[e] = g[e] * scale;
     if constexpr (STATE == 2) {  // decode: m = sign * (c / 127)^2 * scale, v = ((c / 255) * scale)^4
       const float ms = m_scale[row], vs = v_scale[row];
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) {
+      for (int e = 0; e < L; ++e) {
         float mm = m[e] / 127.0f;
         mm = (mm < 0.f ? -1.0f : 1.0f) * mm * mm * ms;
         float vv = v[e] / 255.0f * vs;
@@ -218,10 +430,10 @@ __global__ void __launch_bounds__(kTrainThreads)
         v[e] = vv;
       }
     }
-    float mq[CPL], vroot[CPL];
+    float mq[L], vroot[L];
     float mmax = 0.f, vmax = 0.f;
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) {
+    for (int e = 0; e < L; ++e) {
       if constexpr (STATE == 0) {  // the fp32 kernel forms 1 - beta on the device
         m[e] = beta1 * m[e] + (1.0f - beta1) * g[e];
         v[e] = beta2 * v[e] + (1.0f - beta2) * g[e] * g[e];
@@ -233,9 +445,8 @@ __global__ void __launch_bounds__(kTrainThreads)
         pv[e] = pv[e] - (step_size * m[e]) / denom;
       }
       if constexpr (STATE == 2) {
-        const int d = lane + kWave * e;
         vroot[e] = sqrtf(sqrtf(v[e]));
-        if (d < D) {
+        if (in[e / V]) {
           mmax = fmaxf(mmax, fabsf(m[e]));
           vmax = fmaxf(vmax, vroot[e]);
         }
@@ -246,7 +457,7 @@ __global__ void __launch_bounds__(kTrainThreads)
       vmax = wave_max_f32(vmax);
       const float md = mmax > 0.f ? mmax : 1.0f, vd = vmax > 0.f ? vmax : 1.0f;
 #pragma unroll
-      for (int e = 0; e < CPL; ++e) {
+      for (int e = 0; e < L; ++e) {
         float a = sqrtf(fabsf(m[e]) / md);
         a = (m[e] < 0.f ? -1.0f : 1.0f) * a * 127.0f;
         float b = vroot[e] / vd * 255.0f;
@@ -261,22 +472,21 @@ __global__ void __launch_bounds__(kTrainThreads)
         v_scale[row] = vmax;
       }
     }
+    const float zero[V] = {};
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-      const int d = lane + kWave * e;
-      if (d >= D) continue;
-      const int64_t off = row * D + d;
-      p[off] = pv[e];
-      acc[off] = 0.f;
+    for (int c = 0; c < NC; ++c) {
+      if (!in[c]) continue;
+      store_f32v<V>(p + off[c], pv + c * V);
+      store_f32v<V>(acc + off[c], zero);
       if constexpr (STATE == 0) {
-        ((float *)m_ptr)[off] = m[e];
-        ((float *)v_ptr)[off] = v[e];
+        store_f32v<V>((float *)m_ptr + off[c], m + c * V);
+        store_f32v<V>((float *)v_ptr + off[c], v + c * V);
       } else if constexpr (STATE == 1) {
-        ((uint16_t *)m_ptr)[off] = (uint16_t)bf16_bits_rtne(m[e]);
-        ((uint16_t *)v_ptr)[off] = (uint16_t)bf16_bits_rtne(v[e]);
+        store_bf16v<V>((uint16_t *)m_ptr + off[c], m + c * V);
+        store_bf16v<V>((uint16_t *)v_ptr + off[c], v + c * V);
       } else {
-        ((int8_t *)m_ptr)[off] = (int8_t)(int)mq[e];
-        ((uint8_t *)v_ptr)[off] = (uint8_t)(int)vroot[e];
+        store_codes<V>((uint8_t *)m_ptr + off[c], mq + c * V);
+        store_codes<V>((uint8_t *)v_ptr + off[c], vroot + c * V);
       }
     }
     if (lane == 0) touched[row] = 0;
@@ -287,6 +497,17 @@ template <int CPL>
 void launch_bag_backward(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
                          const void *table, bool f32, int64_t rows, int D, float *acc, uint8_t *touched, float *gw,
                          hipStream_t stream) {
+  if (K <= kSortEntries) {  // T tokens per workgroup: T x K <= 512 lookups, T x D <= 4096 staged floats
+    const int T = std::min(kSortEntries / K, kStageFloats / D);
+    const dim3 grid((unsigned)((N + T - 1) / T)), block(kSortThreads);
+    if (f32)
+      hipLaunchKernelGGL((bag_backward_sorted_kernel<true, CPL>), grid, block, 0, stream, grad_out, idx, w, N, K, T,
+                         table, rows, D, acc, touched, gw);
+    else
+      hipLaunchKernelGGL((bag_backward_sorted_kernel<false, CPL>), grid, block, 0, stream, grad_out, idx, w, N, K,
+                         T, table, rows, D, acc, touched, gw);
+    return;
+  }
   if (f32)
     hipLaunchKernelGGL((bag_backward_kernel<true, CPL>), dim3((unsigned)N), dim3(kTrainThreads), 0, stream, grad_out,
                        idx, w, K, table, rows, D, acc, touched, gw);
@@ -295,6 +516,8 @@ void launch_bag_backward(const float *grad_out, const int64_t *idx, const float 
                        grad_out, idx, w, K, table, rows, D, acc, touched, gw);
 }
 
+bool aligned(const void *p, int a) { return ((uintptr_t)p % a) == 0; }
+
 template <int STATE>
 void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, uint8_t *touched,
                  const float *grad_scale, int64_t rows, int D, float step_size, float bc2_sqrt, float b1, float b2,
@@ -302,17 +525,21 @@ void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, u
   int64_t blocks = (rows + kTrainWaves - 1) / kTrainWaves;
   if (blocks > 65536) blocks = 65536;   // grid-stride beyond 262,144 rows at a time
   const dim3 grid((unsigned)blocks), block(kTrainThreads);
-#define SMLM_ADAM(CPL)                                                                                         \
-  hipLaunchKernelGGL((lazy_adam_kernel<STATE, CPL>), grid, block, 0, stream, p, m, v, ms, vs, acc, touched,     \
+  constexpr int kMomentBytes = STATE == 0 ? 4 : STATE == 1 ? 2 : 1;
+  const bool vec = D % 4 == 0 && aligned(p, 16) && aligned(acc, 16) && aligned(m, 4 * kMomentBytes) &&
+                   aligned(v, 4 * kMomentBytes);
+#define SMLM_ADAM(V, NC)                                                                                       \
+  hipLaunchKernelGGL((lazy_adam_kernel<STATE, V, NC>), grid, block, 0, stream, p, m, v, ms, vs, acc, touched,   \
                      grad_scale, rows, D, step_size, bc2_sqrt, b1, b2, omb1, omb2, eps)
-  if (D <= 128) SMLM_ADAM(2);
-  else if (D <= 256) SMLM_ADAM(4);
-  else if (D <= 384) SMLM_ADAM(6);
-  else SMLM_ADAM(8);
+  if (vec && D <= 256) SMLM_ADAM(4, 1);
+  else if (vec) SMLM_ADAM(4, 2);
+  else if (D <= 128) SMLM_ADAM(1, 2);
+  else if (D <= 256) SMLM_ADAM(1, 4);
+  else if (D <= 384) SMLM_ADAM(1, 6);
+  else SMLM_ADAM(1, 8);
 #undef SMLM_ADAM
 }
 
-bool aligned(const void *p, int a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
 }  // namespace smlm
@@ -349,7 +576,7 @@ extern "C" int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx,
     return fail(SMLM_EINVAL, "smlm_bag_backward_rows: null pointer argument");
   if (table_dtype != SMLM_F32 && table_dtype != SMLM_BF16)
     return fail(SMLM_EINVAL, "smlm_bag_backward_rows: the table must be SMLM_F32 or SMLM_BF16, got %d", table_dtype);
-  if (N < 0 || N > 0x7FFFFFFFLL || K < 1 || rows < 1 || D < 1 || D > kMaxD)
+  if (N < 0 || N > 0x7FFFFFFFLL || K < 1 || rows < 1 || rows >= (1LL << (63 - kSortShift)) || D < 1 || D > kMaxD)
     return fail(SMLM_EUNSUPPORTED, "smlm_bag_backward_rows: N=%lld K=%d rows=%lld D=%d (1 <= D <= %d)",
                 (long long)N, K, (long long)rows, D, kMaxD);
   if (N == 0) return SMLM_OK;

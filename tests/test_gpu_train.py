@@ -79,7 +79,11 @@ def test_pkselect_autograd_matches_oracle():
 
 
 @pytest.mark.parametrize("N,K,D,rows,tdtype", [(33, 128, 384, 1000, torch.float32), (5, 7, 100, 50, torch.float32),
-                                               (17, 64, 384, 300, torch.bfloat16), (3, 40, 512, 20, torch.float32)])
+                                               (17, 64, 384, 300, torch.bfloat16), (3, 40, 512, 20, torch.float32),
+                                               # runs longer than a wavefront and across workgroups
+                                               (64, 128, 384, 3, torch.float32),
+                                               # K = 1: 64 tokens per workgroup; K > 512: one token per workgroup
+                                               (700, 1, 64, 50, torch.float32), (3, 600, 64, 500, torch.bfloat16)])
 def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype):
     note(f"bag backward N={N} K={K} D={D} rows={rows} {tdtype}")
     g = torch.Generator().manual_seed(N + K + D)
@@ -127,7 +131,8 @@ def _adam_case(rows, D, seed):
     return rng, p
 
 
-@pytest.mark.parametrize("rows,D", [(300, 384), (40, 100), (64, 512)])
+# D % 4 == 0 takes 4 adjacent columns per lane (one or two chunks of 256); other widths one column per lane
+@pytest.mark.parametrize("rows,D", [(300, 384), (40, 100), (64, 512), (50, 98), (20, 510)])
 def test_lazy_adam_fp32_bit_exact(rows, D):
     note(f"lazy adam fp32 rows={rows} D={D}")
     rng, p = _adam_case(rows, D, rows + D)
@@ -147,7 +152,8 @@ def test_lazy_adam_fp32_bit_exact(rows, D):
         assert not Tt.cpu().any()
 
 
-@pytest.mark.parametrize("state,rows,D", [("bf16", 200, 384), ("int8", 200, 384), ("int8", 33, 100)])
+@pytest.mark.parametrize("state,rows,D", [("bf16", 200, 384), ("int8", 200, 384), ("int8", 33, 100),
+                                          ("bf16", 30, 130), ("int8", 30, 98), ("int8", 40, 512)])
 def test_lazy_adam_lowmem_bit_exact(state, rows, D):
     note(f"lazy adam {state} rows={rows} D={D}")
     rng, p = _adam_case(rows, D, 7 * rows + D)
