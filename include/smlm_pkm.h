@@ -45,6 +45,16 @@ const char *smlm_pkm_version(void);
 const char *smlm_pkm_last_error(void);
 
 /*
+ * Device address of a value table (or its scales) kept in pinned host memory (hipHostMalloc).  Replaces the
+ * staging path of OffloadTable.bag (smlm/offload.py:57-76: unique rows -> CPU fetch -> pinned staging -> compact
+ * device table) for tables held in host RAM (HostTable, smlm/offload.py:79-92): the table-reading entry points
+ * (smlm_pkm_bag, smlm_pkm_select_bag) accept the returned address and read the rows over the host link, with no
+ * synchronisation, so the call can be captured in a graph.  Host-side only (no device work); fails with
+ * SMLM_EINVAL for pageable, device or unknown memory.
+ */
+int smlm_host_table_pointer(const void *host, void **device);
+
+/*
  * Sub-key scores.  Replaces ProductKeyMemory.subkey_scores (smlm/pkm.py:117-123), the two
  *   s1 = einsum("nhd,hkd->nhk", q[..., :half], keys[:, 0]);  s2 = einsum(..., q[..., half:], keys[:, 1])
  * calls that feed pk_select (smlm/pkm.py:197).

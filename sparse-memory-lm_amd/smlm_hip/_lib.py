@@ -37,6 +37,7 @@ class LinearArgs(ctypes.Structure):
 EXPORTS = {
     "smlm_pkm_version": (ctypes.c_char_p, []),
     "smlm_pkm_last_error": (ctypes.c_char_p, []),
+    "smlm_host_table_pointer": (_i, [_p, ctypes.POINTER(ctypes.c_void_p)]),
     "smlm_pkm_score": (_i, [_p, _i64, _p, _i, _i64, _i, _i, _i, _p, _p, _p]),
     "smlm_pkm_select": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "smlm_pkm_bag": (_i, [_p, _i, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p]),
@@ -98,3 +99,10 @@ def check(rc, what):
 def stream_handle(device):
     """hipStream_t (as int) of torch's current stream on `device`."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def host_device_pointer(host_ptr):
+    """Device address of pinned host memory (smlm_host_table_pointer); raises SmlmError for anything else."""
+    out = ctypes.c_void_p()
+    check(lib().smlm_host_table_pointer(host_ptr, ctypes.byref(out)), "smlm_host_table_pointer")
+    return out.value

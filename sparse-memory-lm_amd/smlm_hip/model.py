@@ -16,7 +16,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import kernels
-from .pkm import ProductKeyMemory
+from .pkm import ProductKeyMemory, inference_tables
 
 
 @dataclass
@@ -380,7 +380,10 @@ class _FusedDecodeStep:
                 return False
             if blk.is_memory:
                 m = blk.ffn
-                table = (getattr(m.values, "infer_table", None) or (m.values.weight, None))[0]
+                tables = inference_tables(m.values)
+                if tables is None:          # staged table tier: every call synchronises, no fused step
+                    return False
+                table = tables[0]
                 if (not m.swilu or m.log_score_scale is not None or m.record or m.heads > 4
                         or (m.heads * m.k_dim) % 16 or (m.k_dim // 2) % 8 or m.v_dim % 32
                         or m.query_proj.weight.dtype != torch.bfloat16
@@ -434,7 +437,7 @@ class _FusedDecodeStep:
                 x, (q, pre) = kernels.decode_linear(w, x, delta=delta, norm=blk.ffn_norm, write_x=True, bias=b,
                                                     affine=affine, n_split=nq)
                 s1, s2 = kernels.pk_scores(q.view(B, m.heads, m.k_dim), m._keys_as(torch.bfloat16))
-                table, scales = getattr(m.values, "infer_table", None) or (m.values.weight.detach(), None)
+                table, scales = inference_tables(m.values)
                 if record is None:
                     out = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True)
                 else:
@@ -527,6 +530,8 @@ class _StepDecoder:
 
     def run(self, prompt, new_tokens, use_graph, sync_every_step):
         B, P = prompt.shape
+        if any(inference_tables(m.values) is None for m in self.model.memory_layers()):
+            use_graph = False               # a staged table tier synchronises in every call: no capture
         if use_graph and self.graph is None:
             self._capture()
         logits = self.model(prompt, kv_caches=self.caches, pos0=0)

@@ -32,6 +32,18 @@ def _autocast_bf16(x):
     return x.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
 
 
+def inference_tables(values):
+    """(table, scales) that the inference kernels read for this values module: its inference table (a tuple, or
+    the device / pinned-host tensors of a smlm_hip.offload table), else the weights; None when the table stages
+    every call through the host (then infer_table.bag() runs the value bag)."""
+    t = getattr(values, "infer_table", None)
+    if t is None:
+        return values.weight.detach(), None
+    if hasattr(t, "bag"):
+        return t.device_tables()
+    return t
+
+
 class ProductKeyMemory(nn.Module):
     """Same constructor as smlm/pkm.py:33-92 (impl defaults to "hip")."""
 
@@ -156,7 +168,7 @@ class ProductKeyMemory(nn.Module):
         shape = x.shape
         x = x.reshape(-1, self.d_in)
         if (self.decode_graph and not self.record and not torch.is_grad_enabled() and x.is_cuda
-                and not torch.cuda.is_current_stream_capturing()):
+                and not torch.cuda.is_current_stream_capturing() and inference_tables(self.values) is not None):
             return self._graph_forward(x).view(*shape[:-1], self.d_out)
         return self._forward(x).view(*shape[:-1], self.d_out)
 
@@ -264,8 +276,11 @@ class ProductKeyMemory(nn.Module):
         if self.swilu and bf16:
             # fused inference bag: value rows (bf16 / fp32 / int8 / q4 table) * bf16(silu(pre)), bf16 out
             pre = self.swilu_proj(x).to(torch.bfloat16)
-            table, scales = getattr(self.values, "infer_table", None) or (self.values.weight.detach(), None)
-            out = kernels.bag_infer(idx, w, table, scales, pre=pre, out_bf16=True)
+            tables = inference_tables(self.values)
+            if tables is None:                  # a table tier that stages every call (smlm_hip.offload)
+                out = self.values.infer_table.bag(idx, w, pre)
+            else:
+                out = kernels.bag_infer(idx, w, tables[0], tables[1], pre=pre, out_bf16=True)
             return self.value_proj(out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
         out = self.read_values(idx, w)
         if self.swilu:
