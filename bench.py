@@ -19,6 +19,8 @@ HBM GB/s".
   train_kernels  the training side at the reference's training shape (4,096 tokens x 128 lookups per micro-batch,
                  B-1M fp32 table): row-sparse bag backward, lazy row Adam (fp32 / bf16 / int8 moments) on the
                  rows of a 32,768-token step, selection backward at config 2; algorithmic GB/s each.
+  offload        config 3 decode with the B-16M table as q4 in HBM, q4 / bf16 in pinned host RAM read over the
+                 host link (zero-copy, graphs), and bs1 from a q4 file through mmap (staged, no graphs).
   roofline       the config-4 gather kernel against HBM peak (8 TB/s), timed with HIP events on the stream it
                  is launched on; roofline_score: the config-2 scoring kernel against the bf16 MFMA peak.
   cpu_baseline   the reference's PyTorch path on the host CPU (oracle/torch_path.py), config 3 at batch 64,
@@ -197,6 +199,96 @@ def lookup_prefill(dev, reps):
     return res
 
 
+def time_decode_eager(model, B, steps, dev, seed=1, prompt_len=128):
+    """Decode steps run one by one without graphs (tables that stage every call synchronise inside the step)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    P = prompt_len
+    prompt = torch.randint(0, model.cfg.vocab_size, (B, P), generator=g, device=dev)
+    with torch.no_grad():
+        dec = model._decoder(B, P + steps + 3, dev)
+        logits = model(prompt, kv_caches=dec.caches, pos0=0)
+        dec.hist[:, :P] = prompt
+        dec.hist[:, P] = logits[:, -1].argmax(-1)
+        dec.tok.copy_(dec.hist[:, P:P + 1])
+        dec.pos.fill_(P)
+        for _ in range(2):
+            dec._step()
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dec._step()
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+    return B * steps / dt, 1000.0 * dt / steps
+
+
+def offload_tiers(model, steps, warmup, dev, reps, staged_steps=32):
+    """Config 3 (B-16M) decode with the value table in each tier of smlm_hip.offload: q4 in HBM, q4 and bf16 in
+    pinned host RAM read by the kernels over the host link (zero-copy, whole-step graphs), and bs1 from a q4 file
+    through mmap (staged: one synchronisation and host fetch per memory-layer call, no graphs); plus the
+    zero-copy q4 gather's host-link bandwidth (4,096 tokens x 128 uniform lookups)."""
+    import tempfile
+    import torch
+    from smlm_hip import kernels as K
+    from smlm_hip.offload import HostTable, MmapQ4Table
+    mem = model.memory_layers()
+    bf16_table = mem[0].values.infer_table
+    res = {}
+
+    def use(table, name, graphs=True):
+        for m in mem:
+            m.values.infer_table = table
+            m._graph = None
+        model._decoders.clear()
+        for B in (1, 64):
+            if not graphs and B > 1:
+                continue
+            if graphs:
+                tok_s, ms = time_decode(model, B, steps, warmup, dev)
+            else:
+                tok_s, ms = time_decode_eager(model, B, staged_steps, dev)
+            res[f"{name}_bs{B}"] = {"tok_s": tok_s, "ms_per_step": ms}
+            log(f"offload {name} bs{B}: {tok_s:.1f} tok/s ({ms:.3f} ms/step)")
+
+    codes, scales = K.quantize_q4(mem[0].values.weight.detach())
+    use((codes, scales), "q4_hbm")
+    t0 = time.perf_counter()
+    host_q4 = HostTable(codes.cpu(), scales.cpu())
+    res["q4_host_pin_s"] = time.perf_counter() - t0
+    use(host_q4, "q4_host_zero_copy")
+    g = torch.Generator(device=dev).manual_seed(9)
+    N, Kl = 4096, 128
+    idx = torch.randint(0, codes.shape[0], (N, Kl), generator=g, device=dev)
+    w = torch.softmax(torch.randn(N, Kl, generator=g, device=dev), -1)
+    ms = event_time_ms(lambda: K.bag_infer(idx, w, host_q4.table, host_q4.scales), reps)
+    alg = N * Kl * (codes.shape[1] + 2)
+    res["q4_host_gather"] = {"tokens": N, "lookups_per_token": Kl, "ms": ms, "row_bytes_GBps": alg / ms / 1e6}
+    log(f"offload zero-copy q4 gather: {res['q4_host_gather']}")
+    del idx, w
+    with tempfile.TemporaryDirectory() as d:
+        codes.cpu().numpy().tofile(os.path.join(d, "values_q4.bin"))
+        scales.cpu().numpy().tofile(os.path.join(d, "scales_q4.bin"))
+        rows, D = codes.shape[0], codes.shape[1] * 2
+        mm = MmapQ4Table(os.path.join(d, "values_q4.bin"), os.path.join(d, "scales_q4.bin"), rows, D)
+        use(mm, "q4_mmap_staged", graphs=False)
+        res["q4_mmap_staged_stats"] = dict(mm.stats)
+        mm.close()
+    del host_q4
+    t0 = time.perf_counter()
+    host_bf16 = HostTable(bf16_table[0].cpu())
+    res["bf16_host_pin_s"] = time.perf_counter() - t0
+    use(host_bf16, "bf16_host_zero_copy")
+    del host_bf16
+    for m in mem:
+        m.values.infer_table = bf16_table
+        m._graph = None
+    model._decoders.clear()
+    del codes, scales
+    torch.cuda.empty_cache()
+    return res
+
+
 def event_time_each_ms(prep, fn, reps):
     """Average device time of fn() in ms over `reps` calls, each bracketed by its own HIP events so that prep()
     (state reset between calls) stays outside the timed intervals."""
@@ -346,9 +438,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,cpu",
-                    help="subset of decode,config1,prefill,lookup,gather,train,cpu,calibrate (profiling runs); the JSON "
-                         "line is complete only with the default")
+    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,offload,cpu",
+                    help="subset of decode,config1,prefill,lookup,gather,train,offload,cpu,calibrate (profiling "
+                         "runs); the JSON line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
@@ -368,7 +460,7 @@ def main():
         log("calibration copy of 1 GiB done")
     model = None
     tok_s64 = ms64 = tok_s1 = ms1 = None
-    if "decode" in phases or "cpu" in phases:
+    if "decode" in phases or "cpu" in phases or "offload" in phases:
         cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
         t0 = time.perf_counter()
         model = build_lm(cfg, dev)
@@ -404,6 +496,9 @@ def main():
     if "gather" in phases:
         ga = gather_stress(dev, args.reps)
         log(f"gather config 4: {ga}")
+    off = None
+    if "offload" in phases:
+        off = offload_tiers(model, args.steps, args.warmup, dev, args.reps)
     if "train" in phases:
         tr = train_kernels(dev, args.reps)
         for k, v in tr.items():
@@ -441,6 +536,7 @@ def main():
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
         "decode_config1_bs1": c1, "prefill_config2": pf,
         "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
+        "offload_config3": off,
         "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
