@@ -21,6 +21,8 @@ HBM GB/s".
                  rows of a 32,768-token step, selection backward at config 2; algorithmic GB/s each.
   offload        config 3 decode with the B-16M table as q4 in HBM, q4 / bf16 in pinned host RAM read over the
                  host link (zero-copy, graphs), and bs1 from a q4 file through mmap (staged, no graphs).
+  engram_lookup  the Engram n-gram hash, row gather (fp32 / bf16) and row-sparse backward over 8 x 2048 tokens x
+                 16 lookups of 24-wide rows (524,287 rows per head); algorithmic GB/s each.
   roofline       the config-4 gather kernel against HBM peak (8 TB/s), timed with HIP events on the stream it
                  is launched on; roofline_score: the config-2 scoring kernel against the bf16 MFMA peak.
   cpu_baseline   the reference's PyTorch path on the host CPU (oracle/torch_path.py), config 3 at batch 64,
@@ -289,6 +291,41 @@ def offload_tiers(model, steps, warmup, dev, reps, staged_steps=32):
     return res
 
 
+def engram_lookup(dev, reps):
+    """The Engram row lookup at the reference's default shape (orders 2 and 3, 8 heads each = 16 lookups per token,
+    524,287 rows per head, head_dim 24) over 8 x 2048 tokens: the hash kernel, the row gather (fp32 and bf16
+    tables) and the row-sparse backward (weight 1 per lookup) into an fp32 accumulator."""
+    import torch
+    from smlm_hip import kernels as K
+    from smlm_hip.engram import NgramHash
+    B, T, vocab = 8, 2048, 50304
+    ng = NgramHash(vocab, (2, 3), 8, 524287, seed=0, canon=torch.arange(vocab)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    c = torch.randint(0, ng.pad, (B, ng.history + T), generator=g, device=dev)
+    rows = ng(c)
+    M = rows.numel()
+    res = {"tokens": B * T, "lookups_per_token": ng.n_lookups, "ms_hash": event_time_ms(lambda: ng(c), reps)}
+    res["hash_alg_GBps"] = (B * (ng.history + T) * 8 + M * 8) / res["ms_hash"] / 1e6
+    for dt, name in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        table = (torch.randn(ng.n_lookups * ng.rows, 24, generator=g, device=dev) * 0.2).to(dt)
+        ms = event_time_ms(lambda: K.row_gather(rows, table), reps)
+        alg = M * (8 + 2 * 24 * table.element_size())
+        res[f"gather_{name}"] = {"ms": ms, "alg_GBps": alg / ms / 1e6}
+        if dt == torch.float32:
+            acc = torch.zeros_like(table)
+            touched = torch.zeros(table.shape[0], dtype=torch.bool, device=dev)
+            grad = torch.randn(M, 24, generator=g, device=dev)
+            flat, ones = rows.reshape(-1, 1), torch.ones(M, 1, device=dev)
+            ms_b = event_time_ms(lambda: K.bag_backward_rows(grad, flat, ones, table, acc, touched), reps)
+            distinct = int(torch.unique(flat).numel())
+            alg_b = M * 16 + M * 24 * 4 + distinct * (3 * 24 * 4 + 1)
+            res["backward_fp32"] = {"ms": ms_b, "distinct_rows": distinct, "alg_GBps": alg_b / ms_b / 1e6}
+            del acc, touched, grad
+        del table
+    torch.cuda.empty_cache()
+    return res
+
+
 def event_time_each_ms(prep, fn, reps):
     """Average device time of fn() in ms over `reps` calls, each bracketed by its own HIP events so that prep()
     (state reset between calls) stays outside the timed intervals."""
@@ -438,8 +475,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,offload,cpu",
-                    help="subset of decode,config1,prefill,lookup,gather,train,offload,cpu,calibrate (profiling "
+    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,offload,engram,cpu",
+                    help="subset of decode,config1,prefill,lookup,gather,train,offload,engram,cpu,calibrate (profiling "
                          "runs); the JSON line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -496,7 +533,10 @@ def main():
     if "gather" in phases:
         ga = gather_stress(dev, args.reps)
         log(f"gather config 4: {ga}")
-    off = None
+    off = eng = None
+    if "engram" in phases:
+        eng = engram_lookup(dev, args.reps)
+        log(f"engram lookup: {eng}")
     if "offload" in phases:
         off = offload_tiers(model, args.steps, args.warmup, dev, args.reps)
     if "train" in phases:
@@ -536,7 +576,7 @@ def main():
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
         "decode_config1_bs1": c1, "prefill_config2": pf,
         "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
-        "offload_config3": off,
+        "offload_config3": off, "engram_lookup": eng,
         "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -296,6 +296,27 @@ int smlm_lazy_adam(float *param, void *exp_avg, void *exp_avg_sq, float *exp_avg
                    float step_size, float bc2_sqrt, float beta1, float beta2, float one_minus_beta1,
                    float one_minus_beta2, float eps, void *stream);
 
+/*
+ * Engram n-gram hash.  Replaces NgramHash.forward (smlm/engram.py:60-73): for every position t of B sequences of
+ * T tokens, n-gram order o (orders[o] tokens) and hash head h, x = XOR_{i < n} c[t - i] * mult[o, h, i] (64-bit
+ * wrap-around), x ^= x >> 17, rows[b, t, o * heads + h] = (x mod rows_per_head) + (o * heads + h) * rows_per_head.
+ *   c        (B, c_len) int64 compressed token ids, c_len = T + max(orders) - 1 (the leading columns are the
+ *            previous chunk's last tokens, or the pad id)
+ *   mult     (n_orders, heads, max_order) int64 odd multipliers
+ *   orders   HOST array of n_orders n-gram lengths (1 <= n <= max_order <= 8, n_orders <= 4)
+ *   rows_out (B, T, n_orders * heads) int64
+ */
+int smlm_engram_hash(const int64_t *c, int64_t B, int64_t T, int64_t c_len, const int64_t *mult, const int *orders,
+                     int n_orders, int heads, int max_order, int64_t rows_per_head, int64_t *rows_out, void *stream);
+
+/*
+ * Row gather out[m] = table[rows[m]] for M int64 row indices (F.embedding), table (table_rows, D) of table_dtype
+ * (SMLM_F32 / SMLM_BF16), out (M, D) of the same dtype.  Replaces the Engram row lookup (smlm/engram.py:111-118,
+ * F.embedding / row_sparse_embedding_bag with weights 1); a row outside the table gives a NaN output row.
+ */
+int smlm_row_gather(const int64_t *rows, int64_t M, const void *table, int table_dtype, int64_t table_rows, int D,
+                    void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

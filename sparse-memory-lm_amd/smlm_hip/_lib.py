@@ -53,6 +53,8 @@ EXPORTS = {
     "smlm_pkm_select_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _p]),
     "smlm_bag_backward_rows": (_i, [_p, _p, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _p]),
     "smlm_lazy_adam": (_i, [_p, _p, _p, _p, _p, _i, _p, _p, _p, _i64, _i, _f, _f, _f, _f, _f, _f, _f, _p]),
+    "smlm_engram_hash": (_i, [_p, _i64, _i64, _i64, _p, _p, _i, _i, _i, _i64, _p, _p]),
+    "smlm_row_gather": (_i, [_p, _i64, _p, _i, _i64, _i, _p, _p]),
 }
 ADAM_F32, ADAM_BF16, ADAM_INT8 = 0, 1, 2
 

@@ -16,6 +16,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import kernels
+from .engram import EngramMemory, NgramHash
 from .pkm import ProductKeyMemory, inference_tables
 
 
@@ -93,6 +94,16 @@ class StaticKVCache:
         self.v = torch.zeros_like(self.k)
         self.slots = torch.arange(max_len, device=device)
         self.max_len = max_len
+        self.extra = {}                     # per-layer decode state of other modules (Engram: "eng_u", "eng_hist")
+
+    def get(self, key, default=None):
+        return self.extra.get(key, default)
+
+    def __getitem__(self, key):
+        return self.extra[key]
+
+    def __setitem__(self, key, value):
+        self.extra[key] = value
 
 
 class Attention(nn.Module):
@@ -207,8 +218,15 @@ class Block(nn.Module):
                 raise ValueError("a second read needs a memory layer with a shared value table")
             self.ffn_norm_r2 = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
             self.ffn_r2 = _memory(cfg, shared_values)
+        self.engram = None
+        if layer_id in cfg.eng_layers:
+            self.engram = EngramMemory(cfg.d_model, len(cfg.eng_orders) * cfg.eng_heads, cfg.eng_head_dim,
+                                       cfg.eng_rows, conv_kernel=cfg.eng_conv_kernel, dilation=max(cfg.eng_orders),
+                                       eps=cfg.norm_eps, impl=cfg.eng_impl, value_grad=cfg.eng_value_grad)
 
-    def forward(self, x, kv_cache=None, pos0=0):
+    def forward(self, x, kv_cache=None, pos0=0, eng_rows=None):
+        if self.engram is not None:
+            x = x + self.engram(x, eng_rows, kv_cache)
         x = x + self.attn(self.attn_norm(x), kv_cache, pos0)
         x = x + self.ffn(self.ffn_norm(x))
         if self.ffn_r2 is not None:
@@ -217,10 +235,10 @@ class Block(nn.Module):
 
 
 class Transformer(nn.Module):
-    def __init__(self, cfg):
+    def __init__(self, cfg, ngram_canon=None):
+        """ngram_canon: the token compression table of the Engram hash ((vocab_size,) int64), needed for Engram
+        layers where the GPT-2 tokenizer (tiktoken) is not installed; None computes it with canonical_ids."""
         super().__init__()
-        if cfg.eng_layers:
-            raise NotImplementedError("Engram layers are not part of the product-key lookup build")
         self.cfg = cfg
         self.tok_emb = nn.Embedding(cfg.vocab_size, cfg.d_model)
         shared = None
@@ -230,6 +248,8 @@ class Transformer(nn.Module):
         self.norm = nn.RMSNorm(cfg.d_model, eps=cfg.norm_eps)
         self.lm_head = nn.Linear(cfg.d_model, cfg.vocab_size, bias=False)
         self.lm_head.weight = self.tok_emb.weight
+        self.ngram = (NgramHash(cfg.vocab_size, cfg.eng_orders, cfg.eng_heads, cfg.eng_rows, cfg.eng_hash_seed,
+                                canon=ngram_canon) if cfg.eng_layers else None)
         self._decoders = {}
         self._init_weights()
 
@@ -255,6 +275,9 @@ class Transformer(nn.Module):
                 if b.ffn_r2 is not None:
                     out.append(b.ffn_r2)
         return out
+
+    def engram_layers(self):
+        return [b.engram for b in self.layers if b.engram is not None]
 
     def memory_sites(self):
         out = []
@@ -299,16 +322,30 @@ class Transformer(nn.Module):
     def forward(self, idx, targets=None, kv_caches=None, pos0=0):
         """Logits (B, T, vocab), or (logits, loss) with targets (smlm/model.py:266-293)."""
         x = self.tok_emb(idx)
-        if x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_autocast_enabled("cuda"):
+        rows = self._ngram_rows(idx, kv_caches) if self.ngram is not None else None
+        if (x.is_cuda and x.dtype == torch.bfloat16 and not torch.is_autocast_enabled("cuda")
+                and self.ngram is None):
             logits = self.lm_head(self._blocks_fused_norms(x, kv_caches, pos0))
         else:
             for i, blk in enumerate(self.layers):
-                x = blk(x, None if kv_caches is None else kv_caches[i], pos0)
+                x = blk(x, None if kv_caches is None else kv_caches[i], pos0, rows)
             logits = self.lm_head(self.norm(x))
         if targets is None:
             return logits
         loss = F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.reshape(-1))
         return logits, loss
+
+    def _ngram_rows(self, idx, kv_caches):
+        """Engram rows of this chunk (smlm/model.py:270-279): the hash sees the last history tokens before the
+        chunk, the pad id at the start of a sequence, else the ones kept in the first layer's cache."""
+        c = self.ngram.canon[idx]
+        hist = kv_caches[0].get("eng_hist") if kv_caches is not None else None
+        if hist is None:
+            hist = torch.full((c.shape[0], self.ngram.history), self.ngram.pad, dtype=c.dtype, device=c.device)
+        c = torch.cat([hist, c], 1)
+        if kv_caches is not None:
+            kv_caches[0]["eng_hist"] = c[:, -self.ngram.history:]
+        return self.ngram(c)
 
     def _blocks_fused_norms(self, x, kv_caches, pos0):
         """The blocks of forward() on bf16 GPU tensors with every residual add fused into the RMSNorm that follows
@@ -369,7 +406,7 @@ class _FusedDecodeStep:
         Transformer.forward)."""
         cfg = model.cfg
         w = model.tok_emb.weight
-        if dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not w.is_cuda:
+        if dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or not w.is_cuda or model.ngram is not None:
             return False
         C, hd = cfg.d_model, cfg.d_model // cfg.n_heads
         if C % 32 or C > 480 or C % cfg.n_heads or hd not in (16, 32, 64, 128) or cfg.ffn_hidden % 16 \
@@ -532,6 +569,10 @@ class _StepDecoder:
         B, P = prompt.shape
         if any(inference_tables(m.values) is None for m in self.model.memory_layers()):
             use_graph = False               # a staged table tier synchronises in every call: no capture
+        if self.model.ngram is not None:
+            use_graph = False               # Engram's conv and hash histories are new tensors every step
+        for cache in self.caches:
+            cache.extra.clear()             # no state of an earlier sequence
         if use_graph and self.graph is None:
             self._capture()
         logits = self.model(prompt, kv_caches=self.caches, pos0=0)
