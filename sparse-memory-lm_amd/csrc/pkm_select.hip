@@ -371,10 +371,6 @@ __device__ __forceinline__ void half_topk_reg(const void *row, int NK, int knn, 
   }
 }
 
-// Cartesian step of one head, by one wavefront: candidates (i, j) with (i+1)(j+1) <= knn of the two halves'
-// descending top lists, scored dtype(v1[i] + v2[j]), top-knn by (score, lowest table index), softmax in fp32.
-// Lane j < knn ends with the j-th best pair: its score `sc` (code = order code of its bits), table index `full`
-// and weight `wt`.  pc: the lane's pairs from load_pairs; s_fsel, s_fin: kMaxKnn entries of LDS scratch.
 // Sum over the wavefront: DPP sums within each 16-lane row, then the four row totals.  All lanes active.
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
