@@ -9,6 +9,8 @@ HBM GB/s".
                  prompts, then K greedy steps; each step is one replay of the captured whole-step HIP graph
                  (embedding, 6 blocks, lm_head, argmax, KV write).  value = 64 * K / time of the K steps.
   decode_bs1     the same at batch 1.
+  config0        config 0: the B-1M PKM layer forward alone in fp32 over 8 x 256 tokens, on the GPU and as the
+                 reference's torch path on the host cores.
   config1        config 1: the same LM with the B-1M memory (1024^2 rows), 512-token prompt, greedy decode at
                  batch 1 (whole-step graph).
   prefill        config 2: the LM with the B-4M memory (2048^2 rows) forward over 8 x 2048 prompt tokens (no
@@ -195,6 +197,7 @@ def lookup_prefill(dev, reps):
     total = ms_score + ms_select + ms_bag
     res = {"tokens": N, "ms_score": ms_score, "ms_select": ms_select, "ms_bag": ms_bag,
            "tok_s": N / total * 1e3, "score_TFLOPs": flops / ms_score / 1e9,
+           "score_write_GBps": 2 * N * H * NK * 2 / ms_score / 1e6,
            "bag_alg_GBps": N * 128 * (2 * D + 12) / ms_bag / 1e6}
     del q, keys, table, pre, s1, s2, sc, idx, w
     torch.cuda.empty_cache()
@@ -324,6 +327,53 @@ def engram_lookup(dev, reps):
         del table
     torch.cuda.empty_cache()
     return res
+
+
+def layer_config0(dev, reps, cpu_reps=3):
+    """Config 0: the B-1M PKM layer forward alone in fp32 (8 x 256 tokens of N(0,1) hidden states, d 384, query
+    384 -> 4 heads x 512, sub-keys N(0, 1/256) of 1024 x 256 per half, top-32 twice, softmax, 1,048,576 x 384 fp32
+    values N(0, 0.02), no query norm, no swilu, seed 0): median synchronised forward time on the GPU, and the
+    reference's torch path (oracle/torch_path.py) on the host cores for the same layer and inputs."""
+    import torch
+    import oracle.torch_path as TP
+    from smlm_hip.pkm import ProductKeyMemory
+    g = torch.Generator().manual_seed(0)
+    N, d, H, kd, NK, knn = 2048, 384, 4, 512, 1024, 32
+    x = torch.randn(N, d, generator=g)
+    mem = ProductKeyMemory(d, d, n_keys=NK, heads=H, knn=knn, k_dim=kd, query_norm="none", swilu=False)
+    with torch.no_grad():
+        mem.query_proj.weight.copy_(torch.randn(H * kd, d, generator=g) * 0.02)
+        mem.query_proj.bias.zero_()
+        mem.keys.copy_(torch.randn(H, 2, NK, kd // 2, generator=g) / 16)
+        mem.values.weight.copy_(torch.randn(NK * NK, d, generator=g) * 0.02)
+    sd = {k: v.detach().clone() for k, v in mem.state_dict().items()}
+    mem = mem.to(dev).eval()
+    xd = x.to(dev)
+    times = []
+    with torch.no_grad():
+        for i in range(3 + reps):
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            mem(xd)
+            torch.cuda.synchronize(dev)
+            if i >= 3:
+                times.append(time.perf_counter() - t0)
+    times.sort()
+    ms = 1000.0 * times[len(times) // 2]
+    mcfg = {"heads": H, "knn": knn, "k_dim": kd, "n_keys": NK, "query_norm": "none", "swilu": False}
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    cpu = []
+    with torch.no_grad():
+        for _ in range(cpu_reps):
+            t0 = time.perf_counter()
+            TP.pkm_forward(sd, "", x, mcfg)
+            cpu.append(time.perf_counter() - t0)
+    cpu.sort()
+    cpu_ms = 1000.0 * cpu[len(cpu) // 2]
+    del mem, xd
+    torch.cuda.empty_cache()
+    return {"tokens": N, "ms": ms, "tok_s": N / ms * 1e3, "cpu_ms": cpu_ms, "cpu_tok_s": N / cpu_ms * 1e3,
+            "cpu_cores": torch.get_num_threads(), "cpu_kind": "port (reference torch path)"}
 
 
 def event_time_each_ms(prep, fn, reps):
@@ -475,9 +525,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,config1,prefill,lookup,gather,train,offload,engram,cpu",
-                    help="subset of decode,config1,prefill,lookup,gather,train,offload,engram,cpu,calibrate (profiling "
-                         "runs); the JSON line is complete only with the default")
+    ap.add_argument("--phases", default="decode,config0,config1,prefill,lookup,gather,train,offload,engram,cpu",
+                    help="subset of decode,config0,config1,prefill,lookup,gather,train,offload,engram,cpu,calibrate "
+                         "(profiling runs); the JSON line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
@@ -507,7 +557,10 @@ def main():
         log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
         tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
         log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
-    c1 = pf = None
+    c0 = c1 = pf = None
+    if "config0" in phases:
+        c0 = layer_config0(dev, args.reps)
+        log(f"layer config 0 (B-1M, fp32, 8 x 256 tokens): {c0}")
     if "config1" in phases:
         t0 = time.perf_counter()
         m1 = build_lm(lm_config(1024, 512 + args.warmup + args.steps + 2), dev)
@@ -561,9 +614,13 @@ def main():
         if traffic:
             roofline["physical_GBps_zipf"] = traffic / ga["ms_zipf"] / 1e6
     if lk is not None:
+        # the launch also writes 537 MB of bf16 scores, which sets its pace: the write rate is reported beside
+        # the MFMA rate
         roofline_score = {"kernel": "score_ws_kernel<8> (config 2 scoring)", "bound": "mfma",
                           "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                          "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS}
+                          "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS,
+                          "score_write_GBps": lk["score_write_GBps"],
+                          "score_write_frac": lk["score_write_GBps"] / HBM_PEAK_GBS}
     line = {
         "metric": "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather HBM GB/s",
         "value": tok_s64, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -574,7 +631,7 @@ def main():
                                "whole-step hipGraph", "global_batch": 64, "prompt_len": 128,
                    "new_tokens": args.steps},
         "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
-        "decode_config1_bs1": c1, "prefill_config2": pf,
+        "layer_config0": c0, "decode_config1_bs1": c1, "prefill_config2": pf,
         "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
         "offload_config3": off, "engram_lookup": eng,
         "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
