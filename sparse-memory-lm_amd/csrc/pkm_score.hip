@@ -28,6 +28,28 @@ __device__ __forceinline__ uint4 load16_or_zero(const void *p, bool ok) {
   return ok ? v : uint4{0u, 0u, 0u, 0u};
 }
 
+// One k-step's operand fragments of score_kernel: key rows key0 + 16 i + r and token rows tok0 + 16 j + r, the
+// g-th group of EPL dims from k0 (zeros outside the rows or past half).
+template <int ESZ, int EPL, int WM, int WN>
+__device__ __forceinline__ void score_load_step(const char *kbase, const char *qbase, int64_t q_stride, int N, int NK,
+                                                int half, int key0, int tok0, int r, int g, int k0, u32x4 (&a)[WM],
+                                                u32x4 (&b)[WN]) {
+  const int kk = k0 + g * EPL;
+  const bool kin = kk < half;  // half % EPL == 0: a lane's group is entirely inside or outside
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int key = key0 + i * 16 + r;
+    a[i] = __builtin_bit_cast(u32x4, load16_or_zero(kbase + ((int64_t)min(key, NK - 1) * half + (kin ? kk : 0)) * ESZ,
+                                                     kin && key < NK));
+  }
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int tok = tok0 + j * 16 + r;
+    b[j] = __builtin_bit_cast(u32x4, load16_or_zero(qbase + ((int64_t)min(tok, N - 1) * q_stride + (kin ? kk : 0)) * ESZ,
+                                                     kin && tok < N));
+  }
+}
+
 // PRE > 0 (bf16 only): when half <= 32 * PRE, every operand fragment of the workgroup is loaded before the first
 // product (decode sizes are latency-bound: one round trip instead of one per k-step).
 template <bool F32, int WM, int WN, int WAVES_M, int WAVES_N, int PRE = 0>
@@ -88,35 +110,42 @@ __global__ void __launch_bounds__(WAVES_M *WAVES_N * 64)
       }
     }
   }
-  for (int k0 = (!F32 && PRE > 0 && half <= PRE * KSTEP) ? half : 0; k0 < half; k0 += KSTEP) {
-    const int kk = k0 + g * EPL;
-    const bool kin = kk < half;  // half % EPL == 0: a lane's group is entirely inside or outside
-    uint4 a[WM], b[WN];
+  // Operands of step k0 + KSTEP are in flight while the MFMAs of step k0 run.  fp32: the four products of a
+  // 16-byte group are issued group-slot outer, so consecutive MFMAs feed different accumulators; each
+  // accumulator still adds its products in the same order (slot 0..3 of step 0, of step 1, ...).
+  const int kbeg = (!F32 && PRE > 0 && half <= PRE * KSTEP) ? half : 0;
+  u32x4 a[WM], b[WN];
+  if (kbeg < half)
+    score_load_step<ESZ, EPL, WM, WN>(kbase, qbase, q_stride, N, NK, half, key0, tok0, r, g, kbeg, a, b);
+  for (int k0 = kbeg; k0 < half; k0 += KSTEP) {
+    const bool more = k0 + KSTEP < half;  // workgroup-uniform
+    u32x4 an[WM], bn[WN];
+    if (more)
+      score_load_step<ESZ, EPL, WM, WN>(kbase, qbase, q_stride, N, NK, half, key0, tok0, r, g, k0 + KSTEP, an, bn);
+    if constexpr (F32) {
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const int key = key0 + i * 16 + r;
-      a[i] = load16_or_zero(kbase + ((int64_t)min(key, NK - 1) * half + (kin ? kk : 0)) * ESZ, kin && key < NK);
-    }
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int tok = tok0 + j * 16 + r;
-      b[j] = load16_or_zero(qbase + ((int64_t)min(tok, N - 1) * q_stride + (kin ? kk : 0)) * ESZ, kin && tok < N);
-    }
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(floatx4, a[i])[s],
+                                                             __builtin_bit_cast(floatx4, b[j])[s], acc[i][j], 0, 0,
+                                                             0);
+    } else {
 #pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        if constexpr (F32) {
-          const floatx4 fa = __builtin_bit_cast(floatx4, a[i]);
-          const floatx4 fb = __builtin_bit_cast(floatx4, b[j]);
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s], fb[s], acc[i][j], 0, 0, 0);
-        } else {
+        for (int j = 0; j < WN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[i]),
                                                               __builtin_bit_cast(bf16x8, b[j]), acc[i][j], 0, 0, 0);
-        }
-      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < WM; ++i) a[i] = an[i];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) b[j] = bn[j];
+    }
   }
 
   char *out = (char *)(p ? s2 : s1);
