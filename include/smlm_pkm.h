@@ -169,6 +169,20 @@ int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float
                      void *h_out, void *stream);
 
 /*
+ * Causal attention of a prompt / prefill pass (several new tokens at once), flash-style on the matrix cores.
+ * Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True) and the masked form for new tokens after a filled
+ * cache (mask = ones(T, S).tril(S - T)) of smlm/model.py:97-105:
+ *   y[b, t, h, :] = sum_{s <= S-T+t} softmax_s(q[b,h,t] . k[b,h,s] / sqrt(head_dim)) v[b,h,s]
+ * bf16 operands, fp32 scores / softmax statistics / accumulation, probabilities rounded to bf16 for the value
+ * product, y rounded to bf16.  Element (b, h, t, d) of q is at q + b*q_strides[0] + h*q_strides[1] + t*q_strides[2]
+ * + d (d contiguous); likewise k, v (t < S) and y with its own strides.  q, k, v 16-byte aligned with strides that
+ * are multiples of 8 elements; y 8-byte aligned, strides multiples of 4.  head_dim in {32, 64, 128}; S >= T.
+ */
+int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *k, const int64_t *k_strides,
+                           const void *v, const int64_t *v_strides, void *y, const int64_t *y_strides, int64_t B,
+                           int H, int T, int S, int head_dim, void *stream);
+
+/*
  * Fused linear layer of the single-token decode step (M = decode batch rows):  y = h W^T on the matrix cores with
  * the op in front of it and the op after it in one launch.  Replaces, per decode step, the nn.Linear calls of
  * smlm/model.py:90-118 and 266-293 (wqkv, wo, w13, w2, lm_head) and smlm/pkm.py:188-191, 213-224 (query_proj,

@@ -1,0 +1,268 @@
+// Causal attention of a prefill / prompt pass on the matrix cores (flash-style: the (T, S) score matrix never
+// leaves the workgroup).  Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True) and its masked form
+// for new tokens after a filled cache (smlm/model.py:97-105): query t of T sits at position S - T + t and sees
+// keys 0 .. S - T + t; y = softmax(q k^T / sqrt(hd)) v, bf16 in and out, fp32 statistics and accumulation.
+//
+// One workgroup = 128 queries of one (batch, head), 4 wavefronts x 32 queries; the keys go by in tiles of 64,
+// staged in LDS (keys row-major, values transposed).  Per tile each wavefront computes S^T = K Q^T on
+// v_mfma_f32_16x16x32_bf16 with the keys as the M operand and its queries as N, so a lane (r, g) holds keys
+// 4g..4g+3 of each 16-key tile for ONE query (r): the online softmax (running max m, sum l, rescale of the
+// output) is per lane, with the cross-lane max / sum over the four lane groups by permlane swaps.  Then
+// O^T = V^T P^T with P^T straight from the score registers (rounded to bf16): the k slots of a 32-key step are
+// keys {4g..4g+3, 16+4g..16+4g+3} in lane group g for both operands, so the lane's own exp-scores ARE its B
+// operand, and V^T's A operand is two 8-byte reads of the transposed value tile.  The output fragment holds
+// d = 4g..4g+3 of query r, the same query as the statistics, so the final 1/l is per lane too.
+#include "pkm_common.h"
+
+namespace smlm {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFaBM = 128;  // queries per workgroup
+constexpr int kFaBN = 64;   // keys per tile
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return bf16_bits_rtne(lo) | (bf16_bits_rtne(hi) << 16);
+}
+
+__device__ __forceinline__ float xor_lane_f(float v, int j) {
+  const uint32_t u = __float_as_uint(v);
+  return __uint_as_float(j == 16 ? xor_lane<16>(u) : xor_lane<32>(u));
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256)
+    flash_attn_kernel(const uint16_t *__restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
+                      const uint16_t *__restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
+                      const uint16_t *__restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
+                      uint16_t *__restrict__ y, int64_t ysb, int64_t ysh, int64_t yst, int B, int H, int T, int S,
+                      float scale_log2) {
+  constexpr int KS = HD / 32;           // k-steps of the score product
+  constexpr int MT = HD / 16;           // 16-wide d tiles of the output
+  constexpr int CPR = HD / 8;           // 16-byte chunks per key / value row
+  constexpr int LPT = kFaBN * CPR / 256;  // chunks per thread per tile (of K, and of V)
+  constexpr int RS = HD + 8;            // sK row stride (bf16)
+  constexpr int VS = kFaBN + 8;         // sVt row stride (bf16)
+  __shared__ __align__(16) uint16_t sK[kFaBN * RS];
+  __shared__ __align__(16) uint16_t sVt[HD * VS];
+
+  const int BH = B * H;
+  const int ntq = (T + kFaBM - 1) / kFaBM;
+  const int qt = ntq - 1 - (int)(blockIdx.x / BH);  // the longest query tiles first
+  const int bh = (int)(blockIdx.x % BH), b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+  const int offset = S - T;
+  const int q0 = qt * kFaBM;
+  const int qw = q0 + wave * 32;  // this wavefront's first query
+  const uint16_t *qb = q + b * qsb + h * qsh;
+  const uint16_t *kb = k + b * ksb + h * ksh;
+  const uint16_t *vb = v + b * vsb + h * vsh;
+
+  // this wavefront's queries as B fragments: query qw + 16 j + r, dims 32 s + 8 g .. +7 (zeros past T)
+  bf16x8 bq[2][KS];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = qw + 16 * j + r;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint4 val = *(const uint4 *)(qb + (int64_t)min(t, T - 1) * qst + 32 * s + 8 * g);
+      bq[j][s] = __builtin_bit_cast(bf16x8, t < T ? val : uint4{0u, 0u, 0u, 0u});
+    }
+  }
+
+  // keys this workgroup needs: up to the position of its last query
+  const int kv_end = offset + min(T, q0 + kFaBM);
+  const int ntk = (kv_end + kFaBN - 1) / kFaBN;
+  const bool wave_on = qw < T;
+  const int qpos_lo = offset + qw;                 // position of the wavefront's first query
+  const int qpos_hi = offset + min(T - 1, qw + 31);  // ... and of its last
+
+  float m[2] = {-__builtin_inff(), -__builtin_inff()};
+  float l[2] = {0.f, 0.f};
+  floatx4 oacc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) oacc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // tile loads: chunk id = tid + 256 u -> row id / CPR, 16-byte chunk id % CPR (rows past S load as zeros)
+  uint4 kr[LPT], vr[LPT];
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
+      const int key = kv0 + row;
+      const int64_t kk = min(key, S - 1);
+      const uint4 kv = *(const uint4 *)(kb + kk * kst + 8 * c);
+      const uint4 vv = *(const uint4 *)(vb + kk * vst + 8 * c);
+      kr[u] = key < S ? kv : uint4{0u, 0u, 0u, 0u};
+      vr[u] = key < S ? vv : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  load_tile(0);
+
+  for (int tk = 0; tk < ntk; ++tk) {
+    const int kv0 = tk * kFaBN;
+    __syncthreads();  // every wavefront is done with the previous tile
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
+      *(uint4 *)&sK[row * RS + 8 * c] = kr[u];
+      const uint32_t w4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sVt[(8 * c + 2 * e) * VS + row] = (uint16_t)(w4[e] & 0xFFFFu);
+        sVt[(8 * c + 2 * e + 1) * VS + row] = (uint16_t)(w4[e] >> 16);
+      }
+    }
+    if (tk + 1 < ntk) load_tile(kv0 + kFaBN);  // in flight during this tile's products
+    __syncthreads();
+
+    // wavefront-uniform: skip tiles none of this wavefront's queries reaches
+    if (!wave_on || kv0 > qpos_hi) continue;
+    const bool masked = kv0 + kFaBN - 1 > qpos_lo;
+
+    // S^T tile: sacc[kt][j][i] = q(query qw + 16 j + r) . k(key kv0 + 16 kt + 4 g + i)
+    floatx4 sacc[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) sacc[kt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 a[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) a[kt] = *(const bf16x8 *)&sK[(16 * kt + r) * RS + 32 * s + 8 * g];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          sacc[kt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kt], bq[j][s], sacc[kt][j], 0, 0, 0);
+    }
+
+    // online softmax per query (lane), in the log2 domain
+    bf16x8 bp[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int qpos = offset + qw + 16 * j + r;
+      if (masked) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kv0 + 16 * kt + 4 * g + i;
+            if (key > qpos || key >= S) sacc[kt][j][i] = -__builtin_inff();
+          }
+      }
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][j][i]);
+      mx = fmaxf(mx, xor_lane_f(mx, 16));
+      mx = fmaxf(mx, xor_lane_f(mx, 32));
+      const float mnew = fmaxf(m[j], mx * scale_log2);  // finite: every query sees key 0 in tile 0
+      const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
+      float ls = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - mnew);
+          sacc[kt][j][i] = p;
+          ls += p;
+        }
+      ls += xor_lane_f(ls, 16);
+      ls += xor_lane_f(ls, 32);
+      l[j] = l[j] * alpha + ls;
+      m[j] = mnew;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
+      // P^T as B fragments: 32-key step ks = key tiles 2 ks and 2 ks + 1
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const floatx4 lo = sacc[2 * ks][j], hi = sacc[2 * ks + 1][j];
+        const uint4 pk{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
+                       pack_bf16x2(hi[2], hi[3])};
+        bp[j][ks] = __builtin_bit_cast(bf16x8, pk);
+      }
+    }
+
+    // O^T += V^T P^T: A fragment of d tile mt = values of d = 16 mt + r at the step's keys (same slot order)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const uint16_t *row = &sVt[(16 * mt + r) * VS + 32 * ks + 4 * g];
+        const uint2 lo = *(const uint2 *)row, hi = *(const uint2 *)(row + 16);
+        const bf16x8 a = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          oacc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[j][ks], oacc[mt][j], 0, 0, 0);
+      }
+  }
+
+  // y[query][d]: lane (r, g) holds d = 16 mt + 4 g .. +3 of query qw + 16 j + r
+  if (!wave_on) return;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = qw + 16 * j + r;
+    if (t >= T) continue;
+    const float inv = 1.0f / l[j];
+    uint16_t *yr = y + b * ysb + h * ysh + (int64_t)t * yst;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const floatx4 o = oacc[mt][j];
+      *(uint2 *)(yr + 16 * mt + 4 * g) = uint2{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+    }
+  }
+}
+
+template <int HD>
+int launch_flash(const void *q, const int64_t *qs, const void *k, const int64_t *ks, const void *v, const int64_t *vs,
+                 void *y, const int64_t *ys, int B, int H, int T, int S, hipStream_t stream) {
+  const int ntq = (T + kFaBM - 1) / kFaBM;
+  const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
+  hipLaunchKernelGGL((flash_attn_kernel<HD>), dim3((unsigned)((int64_t)ntq * B * H)), dim3(256), 0, stream,
+                     (const uint16_t *)q, qs[0], qs[1], qs[2], (const uint16_t *)k, ks[0], ks[1], ks[2],
+                     (const uint16_t *)v, vs[0], vs[1], vs[2], (uint16_t *)y, ys[0], ys[1], ys[2], B, H, T, S,
+                     scale_log2);
+  return launch_status("smlm_prefill_attention");
+}
+
+}  // namespace
+}  // namespace smlm
+
+extern "C" int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *k, const int64_t *k_strides,
+                                      const void *v, const int64_t *v_strides, void *y, const int64_t *y_strides,
+                                      int64_t B, int H, int T, int S, int head_dim, void *stream) {
+  using namespace smlm;
+  if (!q || !k || !v || !y || !q_strides || !k_strides || !v_strides || !y_strides)
+    return fail(SMLM_EINVAL, "smlm_prefill_attention: null pointer argument");
+  if (B < 0 || H < 1 || T < 0 || S < T || (T > 0 && S < 1))
+    return fail(SMLM_EINVAL, "smlm_prefill_attention: bad shape B=%lld H=%d T=%d S=%d", (long long)B, H, T, S);
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(SMLM_EUNSUPPORTED, "smlm_prefill_attention: head_dim %d not in {32, 64, 128}", head_dim);
+  const int64_t ntq = ((int64_t)T + kFaBM - 1) / kFaBM;
+  if (ntq * B * H > 0x7FFFFFFFLL)
+    return fail(SMLM_EINVAL, "smlm_prefill_attention: B*H*ceil(T/128)=%lld workgroups is too many",
+                (long long)(ntq * B * H));
+  const int64_t *st[4] = {q_strides, k_strides, v_strides, y_strides};
+  for (int a = 0; a < 4; ++a)
+    for (int i = 0; i < 3; ++i)
+      if (st[a][i] < 0 || st[a][i] % (a == 3 ? 4 : 8))
+        return fail(SMLM_EINVAL, "smlm_prefill_attention: strides must be non-negative multiples of 8 elements (4 "
+                                 "for y); got %lld", (long long)st[a][i]);
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 || (uintptr_t)y % 8)
+    return fail(SMLM_EINVAL, "smlm_prefill_attention: q, k, v must be 16-byte and y 8-byte aligned");
+  if (B == 0 || T == 0) return SMLM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int b = (int)B;
+  switch (head_dim) {
+    case 32: return launch_flash<32>(q, q_strides, k, k_strides, v, v_strides, y, y_strides, b, H, T, S, s);
+    case 64: return launch_flash<64>(q, q_strides, k, k_strides, v, v_strides, y, y_strides, b, H, T, S, s);
+    default: return launch_flash<128>(q, q_strides, k, k_strides, v, v_strides, y, y_strides, b, H, T, S, s);
+  }
+}

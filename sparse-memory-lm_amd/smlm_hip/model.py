@@ -133,8 +133,8 @@ class Attention(nn.Module):
                     k = torch.cat([kv_cache["k"], k], dim=2)
                     v = torch.cat([kv_cache["v"], v], dim=2)
                 kv_cache["k"], kv_cache["v"] = k, v
-            y = _attention(q, k, v, _causal_mask(q.shape[2], k.shape[2], q.device))
-        return self.wo(y.transpose(1, 2).reshape(B, T, C))
+            y = _causal_attention(q, k, v)
+        return self.wo(y.reshape(B, T, C))
 
     def _static(self, q, k, v, cache, pos0):
         T = q.shape[2]
@@ -144,11 +144,11 @@ class Attention(nn.Module):
                 raise ValueError("a device-side position is for single-token decode steps")
             cache.k.index_copy_(2, pos0.view(1), k)
             cache.v.index_copy_(2, pos0.view(1), v)
-            return _attention(q, cache.k, cache.v, (cache.slots <= pos0).view(1, 1, 1, -1))
+            return _attention(q, cache.k, cache.v, (cache.slots <= pos0).view(1, 1, 1, -1)).transpose(1, 2)
         cache.k[:, :, pos0:pos0 + T] = k
         cache.v[:, :, pos0:pos0 + T] = v
         S = pos0 + T
-        return _attention(q, cache.k[:, :, :S], cache.v[:, :, :S], _causal_mask(T, S, q.device))
+        return _causal_attention(q, cache.k[:, :, :S], cache.v[:, :, :S])
 
 
 def _causal_mask(T, S, device):
@@ -156,6 +156,17 @@ def _causal_mask(T, S, device):
     if T == 1:
         return None
     return torch.ones(T, S, dtype=torch.bool, device=device).tril(S - T)
+
+
+def _causal_attention(q, k, v):
+    """Token i of the T new tokens (q) after S - T earlier ones sees keys 0 .. S - T + i; returns (B, T, H, hd).
+    bf16 on the GPU without an autograd graph: the flash-attention kernel (smlm_prefill_attention), which reads the
+    permuted / sliced views as they are; otherwise (training, fp32) the torch ops of _attention."""
+    if (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == v.dtype == torch.bfloat16
+            and q.shape[-1] in (32, 64, 128)
+            and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad))):
+        return kernels.prefill_attention(q, k, v)
+    return _attention(q, k, v, _causal_mask(q.shape[2], k.shape[2], q.device)).transpose(1, 2)
 
 
 def _attention(q, k, v, mask):

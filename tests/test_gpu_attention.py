@@ -1,0 +1,127 @@
+"""Prefill attention kernel (smlm_prefill_attention) against fp64 / fp32 CPU attention of the same bf16 inputs:
+the causal F.scaled_dot_product_attention of smlm/model.py:97-105 (S == T) and its masked form for new tokens
+after a filled cache (mask ones(T, S).tril(S - T)).
+
+Tolerance: the north star's 1e-2 relative for bf16 outputs, i.e. |y - ref| <= 1e-2 * max|ref| per element, and
+the mean error within 5e-3 of the mean |ref| (the kernel rounds the probabilities to bf16 for the value product and
+the output to bf16, about 0.2% of an output that averages hundreds of values; a dropped key tile, a wrong mask or a
+transposed operand is off by several percent).
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from smlm_hip import kernels as K
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def ref_attention(q, k, v):
+    """fp64 causal attention with the query offset S - T, (B, H, T, hd) -> (B, T, H, hd)."""
+    q, k, v = q.double().cpu(), k.double().cpu(), v.double().cpu()
+    T, S, hd = q.shape[2], k.shape[2], q.shape[3]
+    s = q @ k.transpose(-1, -2) / math.sqrt(hd)
+    mask = torch.ones(T, S, dtype=torch.bool).tril(S - T)
+    s = s.masked_fill(~mask, float("-inf"))
+    return (torch.softmax(s, -1) @ v).transpose(1, 2)
+
+
+def check(got, ref, what):
+    got = got.float().cpu().double()
+    scale = float(ref.abs().max())
+    worst = float((got - ref).abs().max())
+    mean_err = float((got - ref).abs().mean())
+    assert worst <= 1e-2 * scale, f"{what}: worst error {worst:.3e} vs scale {scale:.3e}"
+    assert mean_err <= 5e-3 * float(ref.abs().mean()), f"{what}: mean error {mean_err:.3e}"
+
+
+def rand_qkv(B, H, T, S, hd, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, H, T, hd, generator=g) * scale).to(torch.bfloat16)
+    k = (torch.randn(B, H, S, hd, generator=g) * scale).to(torch.bfloat16)
+    v = torch.randn(B, H, S, hd, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,H,T,S,hd", [
+    (2, 3, 1, 1, 64),        # one token
+    (1, 2, 37, 37, 64),      # one partial query tile, partial key tile
+    (2, 6, 300, 300, 64),    # several query tiles, ragged
+    (1, 2, 130, 700, 64),    # new tokens after 570 cached ones
+    (1, 1, 1, 513, 64),      # one new token after a long prefix
+    (3, 2, 256, 256, 32),
+    (1, 3, 200, 333, 128),
+])
+def test_prefill_attention_matches_fp64(B, H, T, S, hd):
+    note(f"prefill_attention B={B} H={H} T={T} S={S} hd={hd}")
+    q, k, v = rand_qkv(B, H, T, S, hd, seed=B * 1000 + T + S + hd)
+    y = K.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (B, T, H, hd) and y.dtype == torch.bfloat16
+    check(y, ref_attention(q, k, v), f"B={B} H={H} T={T} S={S} hd={hd}")
+
+
+def test_prefill_attention_sharp_scores():
+    """Large logits (softmax close to one-hot, the running max moves a lot between tiles): the online rescaling."""
+    note("prefill_attention sharp scores")
+    q, k, v = rand_qkv(1, 2, 257, 257, 64, seed=7, scale=4.0)
+    y = K.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    check(y, ref_attention(q, k, v), "sharp")
+
+
+def test_prefill_attention_strided_views():
+    """q, k, v as the model passes them: permuted views of one (B, T, 3, H, hd) projection, and keys / values as a
+    prefix slice of a larger static cache."""
+    note("prefill_attention strided views")
+    B, T, H, hd = 2, 160, 6, 64
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn(B, T, 3, H, hd, generator=g).to(torch.bfloat16)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4)
+    y = K.prefill_attention(*(t for t in qkv.to(DEV).permute(2, 0, 3, 1, 4)))
+    torch.cuda.synchronize()
+    check(y, ref_attention(q, k, v), "permuted qkv")
+
+    cache_k = torch.zeros(B, H, 512, hd, dtype=torch.bfloat16)
+    cache_v = torch.zeros_like(cache_k)
+    cache_k[:, :, :T] = k
+    cache_v[:, :, :T] = v
+    ck, cv = cache_k.to(DEV), cache_v.to(DEV)
+    y2 = K.prefill_attention(q.to(DEV), ck[:, :, :T], cv[:, :, :T])
+    torch.cuda.synchronize()
+    check(y2, ref_attention(q, k, v), "cache slice")
+    assert torch.equal(y2.cpu(), y.cpu())   # same values, same order of operations
+
+
+def test_prefill_attention_against_sdpa_config2_shape():
+    """One (batch, head) slice pair at the config-2 prefill length (2048 tokens, head_dim 64) against torch's own
+    fp32 F.scaled_dot_product_attention (is_causal=True) on the CPU."""
+    note("prefill_attention 2048 tokens vs CPU SDPA")
+    q, k, v = rand_qkv(1, 2, 2048, 2048, 64, seed=11)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True).transpose(1, 2).double()
+    y = K.prefill_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    check(y, ref, "2048 tokens")
+
+
+def test_prefill_attention_out_argument_and_errors():
+    note("prefill_attention out= and argument checks")
+    q, k, v = rand_qkv(1, 2, 64, 64, 64, seed=5)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = torch.empty(1, 64, 2, 64, dtype=torch.bfloat16, device=DEV)
+    assert K.prefill_attention(qd, kd, vd, out=out) is out
+    torch.cuda.synchronize()
+    check(out, ref_attention(q, k, v), "out=")
+    with pytest.raises(ValueError):
+        K.prefill_attention(qd.float(), kd, vd)
+    with pytest.raises(ValueError):
+        K.prefill_attention(qd, kd[:, :, :32], vd[:, :, :32])          # S < T
+    with pytest.raises(ValueError):
+        K.prefill_attention(qd[..., :48], kd[..., :48], vd[..., :48])  # head_dim 48
