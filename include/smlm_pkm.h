@@ -169,6 +169,20 @@ int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float
                      void *h_out, void *stream);
 
 /*
+ * RoPE of a prompt pass in one launch: replaces the chunk / multiply / add / cat ops of smlm/model.py:63-78 applied
+ * to q and k of `q, k, v = wqkv(x).view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4)` (smlm/model.py:92-93).  Token t of
+ * the (B*T, 3*H*hd) bf16 projection (row b*T + t at qkv + (b*T + t)*qkv_row_stride) is at position pos0 + t:
+ *   out[i] = bf16(x[i] c - x[i + hd/2] s),  out[i + hd/2] = bf16(x[i] s + x[i + hd/2] c),  i < hd/2,
+ *   c, s = rope_cos / rope_sin[pos0 + t, i] (fp32 or bf16 tables of rope_len rows), fp32 arithmetic;
+ * q and k go to q_out / k_out (element (b, h, t, d) at base + b*strides[0] + h*strides[1] + t*strides[2] + d), v is
+ * copied to v_out when it is not NULL (e.g. the slots [pos0, pos0 + T) of a static KV cache).  head_dim in
+ * {16, 32, 64, 128}; pos0 + T <= rope_len; pointers 16-byte aligned, strides multiples of 8 elements.
+ */
+int smlm_rope_qkv(const void *qkv, int64_t qkv_row_stride, const void *rope_cos, const void *rope_sin, int rope_dtype,
+                  int rope_len, int pos0, void *q_out, const int64_t *q_strides, void *k_out, const int64_t *k_strides,
+                  void *v_out, const int64_t *v_strides, int64_t B, int T, int H, int head_dim, void *stream);
+
+/*
  * Causal attention of a prompt / prefill pass (several new tokens at once), flash-style on the matrix cores.
  * Replaces F.scaled_dot_product_attention(q, k, v, is_causal=True) and the masked form for new tokens after a filled
  * cache (mask = ones(T, S).tril(S - T)) of smlm/model.py:97-105:

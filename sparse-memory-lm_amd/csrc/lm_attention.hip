@@ -12,6 +12,8 @@
 // keys {4g..4g+3, 16+4g..16+4g+3} in lane group g for both operands, so the lane's own exp-scores ARE its B
 // operand, and V^T's A operand is two 8-byte reads of the transposed value tile.  The output fragment holds
 // d = 4g..4g+3 of query r, the same query as the statistics, so the final 1/l is per lane too.
+#include <algorithm>
+
 #include "pkm_common.h"
 
 namespace smlm {
@@ -232,8 +234,140 @@ int launch_flash(const void *q, const int64_t *qs, const void *k, const int64_t 
   return launch_status("smlm_prefill_attention");
 }
 
+// ---- RoPE of a prompt pass: the (B*T, 3*H*hd) qkv projection -> rotated q and k (and v) in the layouts attention
+// reads, one pass instead of the chunk / multiply / add / cat ops of smlm/model.py:63-78.  Token t is at position
+// pos0 + t; out1 = bf16(x1 c - x2 s), out2 = bf16(x1 s + x2 c) in fp32 with one rounding each (the formula of the
+// decode step's attention kernel, so prompt and decode keys come from the same arithmetic).  One thread per 8
+// rotation pairs of a (token, head, q | k), or per 8 dims of v.
+__device__ __forceinline__ void unpack8f(const uint4 v, float *f) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(u[e] << 16);
+    f[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
+  }
+}
+
+template <bool ROPE_F32>
+__device__ __forceinline__ void load8_table(const void *t, int64_t i, float *f) {
+  if constexpr (ROPE_F32) {
+    const float4 a = *(const float4 *)((const float *)t + i), b = *(const float4 *)((const float *)t + i + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    unpack8f(*(const uint4 *)((const uint16_t *)t + i), f);
+  }
+}
+
+template <bool ROPE_F32, int HD>
+__global__ void __launch_bounds__(256)
+    rope_qkv_kernel(const uint16_t *__restrict__ qkv, int64_t qkv_stride, const void *__restrict__ rope_cos,
+                    const void *__restrict__ rope_sin, int pos0, uint16_t *__restrict__ q_out, int64_t qsb,
+                    int64_t qsh, int64_t qst, uint16_t *__restrict__ k_out, int64_t ksb, int64_t ksh, int64_t kst,
+                    uint16_t *__restrict__ v_out, int64_t vsb, int64_t vsh, int64_t vst, int B, int T, int H) {
+  constexpr int CQ = HD / 16;  // 8-pair chunks of a q or k head
+  constexpr int CV = HD / 8;   // 8-dim chunks of a v head
+  const int per_head = 2 * CQ + (v_out ? CV : 0);
+  const int64_t total = (int64_t)B * T * H * per_head;
+  for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < total;
+       it += (int64_t)gridDim.x * blockDim.x) {
+    int64_t rest = it;
+    const int u = (int)(rest % per_head);
+    rest /= per_head;
+    const int h = (int)(rest % H);
+    rest /= H;
+    const int t = (int)(rest % T);
+    const int b = (int)(rest / T);
+    const uint16_t *row = qkv + ((int64_t)b * T + t) * qkv_stride;
+    if (u < 2 * CQ) {
+      const int part = u / CQ, c = u % CQ;  // part 0: q, 1: k
+      const uint16_t *src = row + (int64_t)part * H * HD + h * HD;
+      float x1[8], x2[8], cs[8], sn[8];
+      unpack8f(*(const uint4 *)(src + 8 * c), x1);
+      unpack8f(*(const uint4 *)(src + HD / 2 + 8 * c), x2);
+      const int64_t ti = (int64_t)(pos0 + t) * (HD / 2) + 8 * c;
+      load8_table<ROPE_F32>(rope_cos, ti, cs);
+      load8_table<ROPE_F32>(rope_sin, ti, sn);
+      uint32_t o1[4], o2[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i0 = 2 * e, i1 = 2 * e + 1;
+        o1[e] = bf16_bits_rtne(x1[i0] * cs[i0] - x2[i0] * sn[i0]) |
+                (bf16_bits_rtne(x1[i1] * cs[i1] - x2[i1] * sn[i1]) << 16);
+        o2[e] = bf16_bits_rtne(x1[i0] * sn[i0] + x2[i0] * cs[i0]) |
+                (bf16_bits_rtne(x1[i1] * sn[i1] + x2[i1] * cs[i1]) << 16);
+      }
+      uint16_t *dst = part == 0 ? q_out + b * qsb + h * qsh + (int64_t)t * qst
+                                : k_out + b * ksb + h * ksh + (int64_t)t * kst;
+      *(uint4 *)(dst + 8 * c) = uint4{o1[0], o1[1], o1[2], o1[3]};
+      *(uint4 *)(dst + HD / 2 + 8 * c) = uint4{o2[0], o2[1], o2[2], o2[3]};
+    } else {
+      const int c = u - 2 * CQ;
+      *(uint4 *)(v_out + b * vsb + h * vsh + (int64_t)t * vst + 8 * c) =
+          *(const uint4 *)(row + 2LL * H * HD + h * HD + 8 * c);
+    }
+  }
+}
+
+template <int HD>
+int launch_rope(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int f32, int pos0, void *q,
+                const int64_t *qs, void *k, const int64_t *ks, void *v, const int64_t *vs, int B, int T, int H,
+                hipStream_t stream) {
+  const int64_t per_head = 2 * (HD / 16) + (v ? HD / 8 : 0);
+  const int64_t items = (int64_t)B * T * H * per_head;
+  const unsigned grid = (unsigned)std::min<int64_t>((items + 255) / 256, 1 << 16);
+  const int64_t z3[3] = {0, 0, 0};
+  const int64_t *vv = v ? vs : z3;
+  if (f32)
+    hipLaunchKernelGGL((rope_qkv_kernel<true, HD>), dim3(grid), dim3(256), 0, stream, (const uint16_t *)qkv,
+                       qkv_stride, cos, sin, pos0, (uint16_t *)q, qs[0], qs[1], qs[2], (uint16_t *)k, ks[0], ks[1],
+                       ks[2], (uint16_t *)v, vv[0], vv[1], vv[2], B, T, H);
+  else
+    hipLaunchKernelGGL((rope_qkv_kernel<false, HD>), dim3(grid), dim3(256), 0, stream, (const uint16_t *)qkv,
+                       qkv_stride, cos, sin, pos0, (uint16_t *)q, qs[0], qs[1], qs[2], (uint16_t *)k, ks[0], ks[1],
+                       ks[2], (uint16_t *)v, vv[0], vv[1], vv[2], B, T, H);
+  return launch_status("smlm_rope_qkv");
+}
+
 }  // namespace
 }  // namespace smlm
+
+extern "C" int smlm_rope_qkv(const void *qkv, int64_t qkv_row_stride, const void *rope_cos, const void *rope_sin,
+                             int rope_dtype, int rope_len, int pos0, void *q_out, const int64_t *q_strides,
+                             void *k_out, const int64_t *k_strides, void *v_out, const int64_t *v_strides, int64_t B,
+                             int T, int H, int head_dim, void *stream) {
+  using namespace smlm;
+  if (!qkv || !rope_cos || !rope_sin || !q_out || !q_strides || !k_out || !k_strides || (v_out && !v_strides))
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: null pointer argument");
+  if (rope_dtype != SMLM_F32 && rope_dtype != SMLM_BF16)
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: rope tables must be SMLM_F32 or SMLM_BF16");
+  if (B < 0 || T < 0 || H < 1 || pos0 < 0 || B * (int64_t)T > 0x7FFFFFFFLL)
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: bad shape B=%lld T=%d H=%d pos0=%d", (long long)B, T, H, pos0);
+  if ((int64_t)pos0 + T > rope_len)
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: positions %d..%d are past the rope table (%d rows)", pos0,
+                pos0 + T - 1, rope_len);
+  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(SMLM_EUNSUPPORTED, "smlm_rope_qkv: head_dim %d not in {16, 32, 64, 128}", head_dim);
+  if (qkv_row_stride < 3LL * H * head_dim || qkv_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: qkv_row_stride %lld must be >= 3*H*head_dim and a multiple of 8",
+                (long long)qkv_row_stride);
+  const int64_t *st[3] = {q_strides, k_strides, v_out ? v_strides : q_strides};
+  for (int a = 0; a < 3; ++a)
+    for (int i = 0; i < 3; ++i)
+      if (st[a][i] < 0 || st[a][i] % 8)
+        return fail(SMLM_EINVAL, "smlm_rope_qkv: output strides must be non-negative multiples of 8 elements");
+  if (((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)k_out | (uintptr_t)v_out | (uintptr_t)rope_cos |
+       (uintptr_t)rope_sin) % 16)
+    return fail(SMLM_EINVAL, "smlm_rope_qkv: qkv, the outputs and the rope tables must be 16-byte aligned");
+  if (B == 0 || T == 0) return SMLM_OK;
+  const int f32 = rope_dtype == SMLM_F32, b = (int)B;
+  hipStream_t s = (hipStream_t)stream;
+  switch (head_dim) {
+    case 16: return launch_rope<16>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, pos0, q_out, q_strides, k_out, k_strides, v_out, v_strides, b, T, H, s);
+    case 32: return launch_rope<32>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, pos0, q_out, q_strides, k_out, k_strides, v_out, v_strides, b, T, H, s);
+    case 64: return launch_rope<64>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, pos0, q_out, q_strides, k_out, k_strides, v_out, v_strides, b, T, H, s);
+    default: return launch_rope<128>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, pos0, q_out, q_strides, k_out, k_strides, v_out, v_strides, b, T, H, s);
+  }
+}
 
 extern "C" int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *k, const int64_t *k_strides,
                                       const void *v, const int64_t *v_strides, void *y, const int64_t *y_strides,

@@ -123,7 +123,10 @@ class Attention(nn.Module):
             qkv = self.wqkv(x).view(B, 3 * C).to(torch.bfloat16)
             y = kernels.decode_attention(qkv, self.rope.cos, self.rope.sin, pos0, kv_cache.k, kv_cache.v)
             return self.wo(y.view(B, 1, C).to(x.dtype))
-        q, k, v = self.wqkv(x).view(B, T, 3, self.n_heads, self.head_dim).permute(2, 0, 3, 1, 4)
+        qkv = self.wqkv(x)
+        if not torch.is_tensor(pos0) and _use_attention_kernels(qkv, self.head_dim):
+            return self.wo(self._prefill_kernels(qkv, kv_cache, pos0).reshape(B, T, C))
+        q, k, v = qkv.view(B, T, 3, self.n_heads, self.head_dim).permute(2, 0, 3, 1, 4)
         q, k = self.rope(q, pos0), self.rope(k, pos0)
         if isinstance(kv_cache, StaticKVCache):
             y = self._static(q, k, v, kv_cache, pos0)
@@ -135,6 +138,29 @@ class Attention(nn.Module):
                 kv_cache["k"], kv_cache["v"] = k, v
             y = _causal_attention(q, k, v)
         return self.wo(y.reshape(B, T, C))
+
+    def _prefill_kernels(self, qkv, kv_cache, pos0):
+        """RoPE (smlm_rope_qkv, written straight into the static cache's slots when there is one) and causal
+        attention (smlm_prefill_attention) of T new tokens at positions pos0.. -> (B, T, H, hd)."""
+        B, T, _ = qkv.shape
+        H, hd = self.n_heads, self.head_dim
+        q = torch.empty(B, H, T, hd, dtype=qkv.dtype, device=qkv.device)
+        if isinstance(kv_cache, StaticKVCache):
+            S = pos0 + T
+            if S > kv_cache.max_len:
+                raise ValueError(f"{T} new tokens at position {pos0} overflow the static cache ({kv_cache.max_len})")
+            kernels.rope_qkv(qkv, self.rope.cos, self.rope.sin, pos0, q, kv_cache.k[:, :, pos0:S],
+                             kv_cache.v[:, :, pos0:S])
+            return kernels.prefill_attention(q, kv_cache.k[:, :, :S], kv_cache.v[:, :, :S])
+        k = torch.empty_like(q)
+        kernels.rope_qkv(qkv, self.rope.cos, self.rope.sin, pos0, q, k)
+        v = qkv.view(B, T, 3, H, hd)[:, :, 2].transpose(1, 2)
+        if kv_cache is not None:
+            if kv_cache.get("k") is not None:
+                k = torch.cat([kv_cache["k"], k], dim=2)
+                v = torch.cat([kv_cache["v"], v], dim=2)
+            kv_cache["k"], kv_cache["v"] = k, v
+        return kernels.prefill_attention(q, k, v)
 
     def _static(self, q, k, v, cache, pos0):
         T = q.shape[2]
@@ -158,13 +184,18 @@ def _causal_mask(T, S, device):
     return torch.ones(T, S, dtype=torch.bool, device=device).tril(S - T)
 
 
+def _use_attention_kernels(t, head_dim):
+    """bf16 on the GPU without an autograd graph to record: the prompt-pass kernels (forward only) apply."""
+    return (t.is_cuda and t.dtype == torch.bfloat16 and head_dim in (32, 64, 128)
+            and not (torch.is_grad_enabled() and t.requires_grad))
+
+
 def _causal_attention(q, k, v):
     """Token i of the T new tokens (q) after S - T earlier ones sees keys 0 .. S - T + i; returns (B, T, H, hd).
     bf16 on the GPU without an autograd graph: the flash-attention kernel (smlm_prefill_attention), which reads the
     permuted / sliced views as they are; otherwise (training, fp32) the torch ops of _attention."""
-    if (q.is_cuda and q.dtype == torch.bfloat16 and k.dtype == v.dtype == torch.bfloat16
-            and q.shape[-1] in (32, 64, 128)
-            and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad))):
+    if (_use_attention_kernels(q, q.shape[-1]) and k.dtype == v.dtype == torch.bfloat16
+            and not (torch.is_grad_enabled() and (k.requires_grad or v.requires_grad))):
         return kernels.prefill_attention(q, k, v)
     return _attention(q, k, v, _causal_mask(q.shape[2], k.shape[2], q.device)).transpose(1, 2)
 

@@ -125,3 +125,85 @@ def test_prefill_attention_out_argument_and_errors():
         K.prefill_attention(qd, kd[:, :, :32], vd[:, :, :32])          # S < T
     with pytest.raises(ValueError):
         K.prefill_attention(qd[..., :48], kd[..., :48], vd[..., :48])  # head_dim 48
+
+
+def rope_ref(x, cos, sin, pos0):
+    """fp64 rotation of the halves of x (B, H, T, hd) at positions pos0.. (smlm/model.py:63-78), tables as given."""
+    T, hd = x.shape[2], x.shape[3]
+    c = cos[pos0:pos0 + T].double().cpu()
+    s = sin[pos0:pos0 + T].double().cpu()
+    x = x.double().cpu()
+    a, b = x[..., :hd // 2], x[..., hd // 2:]
+    return torch.cat([a * c - b * s, a * s + b * c], dim=-1)
+
+
+def assert_within_ulp(got, ref, what):
+    """got (bf16) within one bf16 ulp of the fp64 ref (the kernel rounds an fp32 value once)."""
+    got = got.float().cpu().double()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2 ** -120))) - 7)
+    excess = float(((got - ref).abs() - ulp).max())
+    assert excess <= 0, f"{what}: off by more than one bf16 ulp (excess {excess})"
+
+
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,H,hd,pos0", [(2, 37, 3, 64, 5), (1, 1, 6, 64, 300), (3, 130, 2, 128, 0),
+                                           (2, 17, 4, 16, 1)])
+def test_rope_qkv_matches_fp64(B, T, H, hd, pos0, table_dtype):
+    note(f"rope_qkv B={B} T={T} H={H} hd={hd} pos0={pos0} tables {table_dtype}")
+    from smlm_hip.model import RotaryEmbedding
+    rope = RotaryEmbedding(hd, 512, 10000.0)
+    cos, sin = rope.cos.to(table_dtype), rope.sin.to(table_dtype)
+    g = torch.Generator().manual_seed(T + hd)
+    qkv = torch.randn(B, T, 3 * H * hd, generator=g).to(torch.bfloat16)
+    q_ref, k_ref, v_ref = qkv.view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4)
+    qd = torch.empty(B, H, T, hd, dtype=torch.bfloat16, device=DEV)
+    cache_k = torch.zeros(B, H, pos0 + T + 8, hd, dtype=torch.bfloat16, device=DEV)
+    cache_v = torch.zeros_like(cache_k)
+    K.rope_qkv(qkv.to(DEV), cos.to(DEV), sin.to(DEV), pos0, qd, cache_k[:, :, pos0:pos0 + T],
+               cache_v[:, :, pos0:pos0 + T])
+    torch.cuda.synchronize()
+    assert_within_ulp(qd, rope_ref(q_ref, cos, sin, pos0), "q")
+    assert_within_ulp(cache_k[:, :, pos0:pos0 + T], rope_ref(k_ref, cos, sin, pos0), "k")
+    assert torch.equal(cache_v[:, :, pos0:pos0 + T].cpu(), v_ref)
+    # slots outside [pos0, pos0 + T) untouched
+    assert not cache_k[:, :, :pos0].any() and not cache_k[:, :, pos0 + T:].any()
+    assert not cache_v[:, :, :pos0].any() and not cache_v[:, :, pos0 + T:].any()
+
+
+def test_rope_qkv_errors():
+    note("rope_qkv argument checks")
+    qkv = torch.zeros(1, 8, 3 * 2 * 64, dtype=torch.bfloat16, device=DEV)
+    cos = torch.zeros(16, 32, device=DEV)
+    q = torch.empty(1, 2, 8, 64, dtype=torch.bfloat16, device=DEV)
+    k = torch.empty_like(q)
+    with pytest.raises(ValueError):
+        K.rope_qkv(qkv, cos, cos, 9, q, k)               # positions 9..16 past a 16-row table
+    with pytest.raises(ValueError):
+        K.rope_qkv(qkv.float(), cos, cos, 0, q, k)
+    with pytest.raises(ValueError):
+        K.rope_qkv(qkv, cos[:, :16], cos[:, :16], 0, q, k)
+
+
+def test_model_prefill_kernels_match_torch_path():
+    """A dense bf16 LM's prompt logits through the prompt-pass kernels (no autograd graph) against the torch ops of
+    the same model (recorded for autograd: RoPE by chunk / cat, attention by bmm + fp32 softmax), at one and two
+    prompt chunks (the second attends over a dict cache of the first)."""
+    note("model prefill: kernels vs torch ops")
+    from smlm_hip.model import ModelConfig, Transformer
+    torch.manual_seed(0)
+    cfg = ModelConfig(vocab_size=512, d_model=384, n_layers=2, n_heads=6, ffn_hidden=1024, max_seq_len=512,
+                      mem_layers=[])
+    model = Transformer(cfg).to(DEV).to(torch.bfloat16).eval()
+    idx = torch.randint(0, 512, (2, 300), device=DEV)
+    ref = model(idx)                                   # grad enabled: parameters record -> torch path
+    with torch.no_grad():
+        got = model(idx)
+        cache = [dict() for _ in range(cfg.n_layers)]
+        a = model(idx[:, :170], kv_caches=cache, pos0=0)
+        b = model(idx[:, 170:], kv_caches=cache, pos0=170)
+    torch.cuda.synchronize()
+    ref = ref.detach().float()
+    scale = float(ref.abs().max())
+    for what, t in (("one pass", got), ("two chunks", torch.cat([a, b], dim=1))):
+        err = float((t.float() - ref).abs().max())
+        assert err <= 2e-2 * scale, f"{what}: logits off by {err:.3e} (scale {scale:.3e})"
