@@ -14,7 +14,8 @@ HBM GB/s".
   config1        config 1: the same LM with the B-1M memory (1024^2 rows), 512-token prompt, greedy decode at
                  batch 1 (whole-step graph).
   prefill        config 2: the LM with the B-4M memory (2048^2 rows) forward over 8 x 2048 prompt tokens (no
-                 cache), tokens / median forward time.
+                 cache), tokens / median forward time; `attention`: the prompt-pass attention kernel alone at that
+                 shape, causal flops / time against the bf16 MFMA peak.
   pkm_lookup     config 2 (B-4M, 8 x 2048 tokens): scoring + selection + value bag kernels, tokens / time.
   gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out;
                  algorithmic bytes 3,439,329,280 per call; plus a uniform-index control.
@@ -145,6 +146,22 @@ def zipf_rows(n, rows, s, g, dev):
     del cdf, u
     perm = torch.randperm(rows, generator=g, device=dev)
     return perm[ranks]
+
+
+def prefill_attention_kernel(dev, reps):
+    """The prompt-pass attention kernel alone at the config-2 shape (8 x 2048 tokens, 6 heads of 64): causal flops
+    (q k^T and p v over the T (T + 1) / 2 visible pairs) / HIP-event time against the bf16 MFMA peak."""
+    import torch
+    from smlm_hip import kernels as K
+    B, H, T, hd = 8, 6, 2048, 64
+    g = torch.Generator(device=dev).manual_seed(4)
+    q, k, v = (torch.randn(B, H, T, hd, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    out = torch.empty(B, T, H, hd, dtype=torch.bfloat16, device=dev)
+    ms = event_time_ms(lambda: K.prefill_attention(q, k, v, out=out), reps)
+    flops = 4.0 * B * H * hd * T * (T + 1) / 2
+    del q, k, v, out
+    return {"shape": f"B={B} H={H} T={T} head_dim={hd}, causal", "ms": ms, "TFLOPs": flops / ms / 1e9,
+            "mfma_frac": flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS}
 
 
 def gather_stress(dev, reps):
@@ -575,7 +592,7 @@ def main():
         m2 = build_lm(lm_config(2048, 2048), dev)
         tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
         pf = {"tok_s": tok_s, "ms_per_forward": ms, "batch": 8, "seq_len": 2048,
-              "table": "4,194,304 x 384 bf16 (B-4M)"}
+              "table": "4,194,304 x 384 bf16 (B-4M)", "attention": prefill_attention_kernel(dev, args.reps)}
         log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
         del m2
         torch.cuda.empty_cache()

@@ -25,8 +25,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kFaBM = 128;  // queries per workgroup
 constexpr int kFaBN = 64;   // keys per tile
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+// two fp32 -> packed bf16, round to nearest even, in one v_cvt_pk_bf16_f32 (values here are finite)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return bf16_bits_rtne(lo) | (bf16_bits_rtne(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ float xor_lane_f(float v, int j) {
@@ -89,9 +93,25 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int j = 0; j < 2; ++j) oacc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // tile loads: chunk id = tid + 256 u -> row id / CPR, 16-byte chunk id % CPR (rows past S load as zeros)
+  // tile loads: chunk id = tid + 256 u -> row id / CPR, 16-byte chunk id % CPR.  Whole tiles read through row
+  // pointers set up once; the last, partial tile clamps its rows into range and loads rows past S as zeros.
   uint4 kr[LPT], vr[LPT];
+  const uint16_t *kp[LPT], *vp[LPT];
+#pragma unroll
+  for (int u = 0; u < LPT; ++u) {
+    const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
+    kp[u] = kb + row * kst + 8 * c;
+    vp[u] = vb + row * vst + 8 * c;
+  }
   auto load_tile = [&](int kv0) {
+    if (kv0 + kFaBN <= S) {  // workgroup-uniform
+#pragma unroll
+      for (int u = 0; u < LPT; ++u) {
+        kr[u] = *(const uint4 *)(kp[u] + kv0 * kst);
+        vr[u] = *(const uint4 *)(vp[u] + kv0 * vst);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
       const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
@@ -144,8 +164,12 @@ __global__ void __launch_bounds__(256)
           sacc[kt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kt], bq[j][s], sacc[kt][j], 0, 0, 0);
     }
 
-    // online softmax per query (lane), in the log2 domain
-    bf16x8 bp[2][2];
+    // online softmax per query (lane), in the log2 domain.  The reference point m of the exponentials is raised
+    // (and the output and sum rescaled) only when some query of the wavefront has a tile maximum more than 2^8
+    // above it: until then the probabilities exp2(s - m) stay below 256, exact enough in fp32 and bf16, and the
+    // rescale, which costs as much as a tile's products, is skipped.  Every query sees key 0 in tile 0, so m is
+    // finite from the first tile on.
+    float mx[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int qpos = offset + qw + 16 * j + r;
@@ -158,30 +182,38 @@ __global__ void __launch_bounds__(256)
             if (key > qpos || key >= S) sacc[kt][j][i] = -__builtin_inff();
           }
       }
-      float mx = -__builtin_inff();
+      float a = fmaxf(fmaxf(sacc[0][j][0], sacc[0][j][1]), fmaxf(sacc[0][j][2], sacc[0][j][3]));
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 1; kt < 4; ++kt)
+        a = fmaxf(a, fmaxf(fmaxf(sacc[kt][j][0], sacc[kt][j][1]), fmaxf(sacc[kt][j][2], sacc[kt][j][3])));
+      a = fmaxf(a, xor_lane_f(a, 16));
+      mx[j] = fmaxf(a, xor_lane_f(a, 32)) * scale_log2;
+    }
+    if (__builtin_amdgcn_ballot_w64(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {  // wavefront-uniform
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][j][i]);
-      mx = fmaxf(mx, xor_lane_f(mx, 16));
-      mx = fmaxf(mx, xor_lane_f(mx, 32));
-      const float mnew = fmaxf(m[j], mx * scale_log2);  // finite: every query sees key 0 in tile 0
-      const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
+      for (int j = 0; j < 2; ++j) {
+        const float mnew = fmaxf(m[j], mx[j]);
+        const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
+        l[j] *= alpha;
+        m[j] = mnew;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
+      }
+    }
+    bf16x8 bp[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
       float ls = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - mnew);
+          const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - m[j]);
           sacc[kt][j][i] = p;
           ls += p;
         }
       ls += xor_lane_f(ls, 16);
-      ls += xor_lane_f(ls, 32);
-      l[j] = l[j] * alpha + ls;
-      m[j] = mnew;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
+      l[j] += xor_lane_f(ls, 32) + ls;
       // P^T as B fragments: 32-key step ks = key tiles 2 ks and 2 ks + 1
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {

@@ -25,6 +25,9 @@ CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall",
     # no packed-fp32 (v_pk_*_f32) instructions anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: otherwise the compiler keeps them in AGPRs and copies them back and
+    # forth around every epilogue / softmax (v_accvgpr_read / write; ~23k of them across the decode linears)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
 ]
 
