@@ -169,6 +169,16 @@ int smlm_add_rmsnorm(const void *x, const void *delta, const void *weight, float
                      void *h_out, void *stream);
 
 /*
+ * Eval-mode BatchNorm of the memory query on bf16 rows in one pass: replaces `q = query_norm(q)` with the running
+ * statistics (smlm/pkm.py:188-191; BN in fp32 under autocast, then the bf16 cast of pkm.py:197):
+ *   out[m, c] = bf16(x[m, c] * scale[c] + shift[c]),  scale = weight / sqrt(var + eps), shift = bias - mean * scale
+ * fp32 arithmetic (one fused multiply-add), round to nearest even.  x, out (M, C) bf16 with row strides (elements,
+ * multiples of 8); scale, shift (C,) fp32; C a multiple of 8; pointers 16-byte aligned.
+ */
+int smlm_affine_bf16(const void *x, int64_t x_row_stride, const float *scale, const float *shift, int64_t M, int C,
+                     void *out, int64_t out_row_stride, void *stream);
+
+/*
  * RoPE of a prompt pass in one launch: replaces the chunk / multiply / add / cat ops of smlm/model.py:63-78 applied
  * to q and k of `q, k, v = wqkv(x).view(B, T, 3, H, hd).permute(2, 0, 3, 1, 4)` (smlm/model.py:92-93).  Token t of
  * the (B*T, 3*H*hd) bf16 projection (row b*T + t at qkv + (b*T + t)*qkv_row_stride) is at position pos0 + t:

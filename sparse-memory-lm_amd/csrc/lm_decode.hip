@@ -426,8 +426,119 @@ __global__ void __launch_bounds__(256) add_rmsnorm_kernel(const uint16_t *__rest
   }
 }
 
+// The same with 16 lanes per row and 16-byte accesses, the row held in registers between the statistics and the
+// output (C % 8 == 0, C <= 128 * CPQ): 16 rows per workgroup of 256 threads.  Rows past M repeat the last row's
+// loads (every lane takes part in the row sums) and store nothing.
+__device__ __forceinline__ float row16_add(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+__device__ __forceinline__ uint4 pack8_rtne(const float *f) {
+  uint32_t u[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) u[e] = bf16_bits_rtne(f[2 * e]) | (bf16_bits_rtne(f[2 * e + 1]) << 16);
+  return uint4{u[0], u[1], u[2], u[3]};
+}
+
+template <int CPQ>
+__global__ void __launch_bounds__(256) add_rmsnorm_vec_kernel(const uint16_t *__restrict__ x,
+                                                              const uint16_t *__restrict__ delta,
+                                                              const uint16_t *__restrict__ weight, float eps,
+                                                              int64_t M, int C, uint16_t *__restrict__ x_out,
+                                                              uint16_t *__restrict__ h_out) {
+  const int sub = threadIdx.x & 15;
+  const int64_t m = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
+  const bool live = m < M;
+  const int64_t row = (live ? m : M - 1) * C;
+  const int CH = C / 8;
+  uint4 xv[CPQ], dv[CPQ], gv[CPQ];
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    const int c = min(sub + 16 * j, CH - 1);
+    xv[j] = *(const uint4 *)(x + row + 8 * c);
+    if (delta) dv[j] = *(const uint4 *)(delta + row + 8 * c);
+    gv[j] = *(const uint4 *)(weight + 8 * c);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    float v[8];
+    unpack8(xv[j], v);
+    if (delta) {
+      float d[8];
+      unpack8(dv[j], d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = round_bf16(v[e] + d[e]);
+      xv[j] = pack8_rtne(v);
+    }
+    if (sub + 16 * j < CH) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+  }
+  ss = row16_add(ss);
+  const float rstd = rsqrtf(ss / (float)C + eps);
+  if (!live) return;
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    const int c = sub + 16 * j;
+    if (c >= CH) continue;
+    if (delta) *(uint4 *)(x_out + row + 8 * c) = xv[j];
+    float v[8], w[8];
+    unpack8(xv[j], v);
+    unpack8(gv[j], w);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = v[e] * rstd * w[e];
+    *(uint4 *)(h_out + row + 8 * c) = pack8_rtne(v);
+  }
+}
+
+// ---- eval BatchNorm of the memory query on bf16 rows (smlm/pkm.py:188-191 with running statistics): out[m, c] =
+// bf16(x[m, c] * scale[c] + shift[c]), fp32 arithmetic, one pass (no fp32 intermediate tensor).  8 columns per
+// thread with 16-byte accesses.
+__global__ void __launch_bounds__(256) affine_bf16_kernel(const uint16_t *__restrict__ x, int64_t x_stride,
+                                                          const float *__restrict__ scale,
+                                                          const float *__restrict__ shift, int64_t M, int C,
+                                                          uint16_t *__restrict__ out, int64_t out_stride) {
+  const int per_row = C / 8;
+  const int64_t item = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= M * per_row) return;
+  const int64_t m = item / per_row;
+  const int c = (int)(item % per_row) * 8;
+  float v[8];
+  unpack8(*(const uint4 *)(x + m * x_stride + c), v);
+  const float4 s0 = *(const float4 *)(scale + c), s1 = *(const float4 *)(scale + c + 4);
+  const float4 b0 = *(const float4 *)(shift + c), b1 = *(const float4 *)(shift + c + 4);
+  const float sc[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  const float sh[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = fmaf(v[e], sc[e], sh[e]);
+  *(uint4 *)(out + m * out_stride + c) = pack8_rtne(v);
+}
+
 }  // namespace
 }  // namespace smlm
+
+extern "C" int smlm_affine_bf16(const void *x, int64_t x_row_stride, const float *scale, const float *shift,
+                                int64_t M, int C, void *out, int64_t out_row_stride, void *stream) {
+  using namespace smlm;
+  if (!x || !scale || !shift || !out) return fail(SMLM_EINVAL, "smlm_affine_bf16: null pointer");
+  if (M < 0 || C < 8 || C % 8 || x_row_stride < C || out_row_stride < C || x_row_stride % 8 || out_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_affine_bf16: bad shape M=%lld C=%d (C a multiple of 8, row strides >= C and "
+                             "multiples of 8)", (long long)M, C);
+  if (((uintptr_t)x | (uintptr_t)scale | (uintptr_t)shift | (uintptr_t)out) % 16)
+    return fail(SMLM_EINVAL, "smlm_affine_bf16: pointers must be 16-byte aligned");
+  const int64_t items = M * (C / 8);
+  if (items == 0) return SMLM_OK;
+  if ((items + 255) / 256 > 0x7FFFFFFFLL) return fail(SMLM_EINVAL, "smlm_affine_bf16: M too large");
+  hipLaunchKernelGGL(affine_bf16_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t *)x, x_row_stride, scale, shift, M, C, (uint16_t *)out, out_row_stride);
+  return launch_status("smlm_affine_bf16");
+}
 
 extern "C" int smlm_swiglu(const void *in, int64_t in_row_stride, void *out, int64_t M, int hidden, void *stream) {
   using namespace smlm;
@@ -464,6 +575,22 @@ extern "C" int smlm_add_rmsnorm(const void *x, const void *delta, const void *we
   if (!x || !weight || !h_out || (delta && !x_out)) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: null pointer");
   if (M < 0 || C < 1 || !(eps >= 0.f)) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: bad shape or eps");
   if (M == 0) return SMLM_OK;
+  const bool vec = C % 8 == 0 && C <= 512 &&
+                   ((uintptr_t)x | (uintptr_t)delta | (uintptr_t)weight | (uintptr_t)x_out | (uintptr_t)h_out) % 16 == 0;
+  if (vec) {
+    const int64_t vblocks = (M + 15) / 16;
+    if (vblocks > 0x7FFFFFFFLL) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: M too large");
+    const dim3 g((unsigned)vblocks), b(256);
+    hipStream_t s = (hipStream_t)stream;
+    const uint16_t *xx = (const uint16_t *)x, *dd = (const uint16_t *)delta, *ww = (const uint16_t *)weight;
+    uint16_t *xo = (uint16_t *)x_out, *ho = (uint16_t *)h_out;
+    const int cpq = (C / 8 + 15) / 16;
+    if (cpq == 1) hipLaunchKernelGGL(add_rmsnorm_vec_kernel<1>, g, b, 0, s, xx, dd, ww, eps, M, C, xo, ho);
+    else if (cpq == 2) hipLaunchKernelGGL(add_rmsnorm_vec_kernel<2>, g, b, 0, s, xx, dd, ww, eps, M, C, xo, ho);
+    else if (cpq == 3) hipLaunchKernelGGL(add_rmsnorm_vec_kernel<3>, g, b, 0, s, xx, dd, ww, eps, M, C, xo, ho);
+    else hipLaunchKernelGGL(add_rmsnorm_vec_kernel<4>, g, b, 0, s, xx, dd, ww, eps, M, C, xo, ho);
+    return launch_status("smlm_add_rmsnorm");
+  }
   const int64_t blocks = (M + 3) / 4;
   if (blocks > 0x7FFFFFFFLL) return fail(SMLM_EINVAL, "smlm_add_rmsnorm: M too large");
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)blocks), dim3(4 * kWave), 0, (hipStream_t)stream,

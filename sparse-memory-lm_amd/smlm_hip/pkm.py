@@ -206,6 +206,9 @@ class ProductKeyMemory(nn.Module):
                 raise NotImplementedError("smlm_hip is inference-only: put the model in eval() mode")
             # BatchNorm with the running statistics, in fp32 whatever the parameter dtype: q * scale + shift
             scale, shift = self._bn_affine()
+            if q.is_cuda and q.dtype == torch.bfloat16 and q.shape[-1] % 8 == 0 and not (
+                    torch.is_grad_enabled() and q.requires_grad):
+                return kernels.affine_bf16(q, scale, shift)     # straight to the bf16 the scores are computed on
             q = torch.addcmul(shift, q, scale)
         return q
 

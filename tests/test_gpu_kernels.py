@@ -424,7 +424,7 @@ def test_greedy_argmax_first_index_and_history():
     assert bool((hist[:, 6:] == -1).all())
 
 
-@pytest.mark.parametrize("M,C", [(64, 384), (1, 384), (5, 100), (4096, 384)])
+@pytest.mark.parametrize("M,C", [(64, 384), (1, 384), (5, 100), (4096, 384), (37, 512), (3, 64), (17, 200)])
 def test_add_rmsnorm_matches_reference_ops(M, C):
     """x + delta rounded to bf16 (the residual stream), then RMSNorm with fp32 statistics and bf16 weight."""
     g = torch.Generator().manual_seed(M + C)
@@ -442,3 +442,29 @@ def test_add_rmsnorm_matches_reference_ops(M, C):
     x0, h0 = K.add_rmsnorm(x.to(DEV), None, norm)
     ref0 = (torch.nn.functional.rms_norm(x.double(), (C,), eps=1e-5) * norm.weight.cpu().double()).float()
     torch.testing.assert_close(h0.cpu().float(), ref0, rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("M,C", [(1, 2048), (300, 2048), (7, 40)])
+def test_affine_bf16_matches_fp64(M, C):
+    """The eval BatchNorm of the memory query (smlm/pkm.py:188-191) on bf16 rows: bf16(x * scale + shift) within one
+    bf16 ulp of the fp64 value (one fp32 fused multiply-add, then one rounding), and equal to torch's
+    BatchNorm1d(eval) of the same rows rounded to bf16 within that ulp."""
+    g = torch.Generator().manual_seed(M + C)
+    x = torch.randn(M, C, generator=g).to(torch.bfloat16)
+    bn = torch.nn.BatchNorm1d(C).eval()
+    with torch.no_grad():
+        bn.running_mean.copy_(torch.randn(C, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(C, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(C, generator=g) + 0.5)
+        bn.bias.copy_(torch.randn(C, generator=g) * 0.1)
+    scale = (bn.weight / torch.sqrt(bn.running_var + bn.eps)).detach()
+    shift = (bn.bias - bn.running_mean * scale).detach()
+    got = K.affine_bf16(x.to(DEV), scale.to(DEV), shift.to(DEV)).cpu()
+    exact = x.double() * scale.double() + shift.double()
+    ulp = torch.exp2(torch.floor(torch.log2(exact.abs().clamp_min(2 ** -120))) - 7)
+    assert float(((got.double() - exact).abs() - ulp).max()) <= 0
+    with torch.no_grad():
+        ref = bn(x.float()).to(torch.bfloat16).double()
+    assert float(((got.double() - ref).abs() - 2 * ulp).max()) <= 0
+    with pytest.raises(ValueError):
+        K.affine_bf16(x.to(DEV), scale[:-1].to(DEV), shift.to(DEV))
