@@ -112,6 +112,22 @@ __global__ void __launch_bounds__(kAttnThreads)
   const uint16_t *row = qkv + (int64_t)b * qkv_stride;
   const int64_t cache_row = ((int64_t)b * H + h) * max_len;
 
+  // 0. The first group of cache rows (keys and values of rows < P, which do not depend on this step) is loaded
+  // before anything else, so its round trip overlaps the one of the qkv row below.  Row P itself (written in 1.)
+  // is never loaded: rows are clamped to P - 1 and row P is taken from LDS.
+  constexpr int U = kAttnUnroll;
+  const int sub = lane % LPR, rw = lane / LPR;
+  const int slot = wave * RPW + rw;
+  const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
+  uint4 kv[U], vpre[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
+    const int64_t t = min((int64_t)(u * RPB + slot), last);
+    kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
+    vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
+  }
+
   // 1. RoPE on q, k; v as is; new k, v into the cache
   for (int i = tid; i < HD / 2; i += kAttnThreads) {
     const float c = table_val<ROPE_F32>(rope_cos, P * (HD / 2) + i);
@@ -134,30 +150,18 @@ __global__ void __launch_bounds__(kAttnThreads)
   __syncthreads();
 
   // 2. scores.  Every cache load of a group of U passes is issued before the first is used (the step is latency-
-  // bound: one round trip per group, not per pass), and the first group's value rows are loaded with its key rows.
-  constexpr int U = kAttnUnroll;
-  const int sub = lane % LPR, rw = lane / LPR;
-  const int slot = wave * RPW + rw;
-  const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
+  // bound: one round trip per group, not per pass); the first group's keys and values came in step 0.
   const float scale = rsqrtf((float)HD);
   float qf[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) qf[e] = s_q[sub * 8 + e];
-  uint4 vpre[U];
   for (int t0 = 0; t0 <= P; t0 += RPB * U) {
-    uint4 kv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (t0 + u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
-      const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
-      kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
-    }
-    if (t0 == 0) {
+    if (t0 > 0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (u * RPB > P) continue;
-        const int64_t t = min((int64_t)(u * RPB + slot), last);
-        vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
+        if (t0 + u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
+        const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
+        kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
       }
     }
 #pragma unroll
