@@ -429,7 +429,8 @@ __global__ void __launch_bounds__(WAVES * 64)
 // their bf16 scores to an LDS output tile; meanwhile the memory wavefronts put block kb + 1 (fetched during the
 // previous block) into the other LDS key buffer, fetch block kb + 2, and write block kb - 1's output tile to memory
 // as whole 128-byte score rows.  A wavefront that stalls on a store is then never one that has MFMAs to issue: the
-// stores (537 MB at config 2) and the products overlap.  One barrier per block.
+// stores (537 MB at config 2) and the products overlap.  One barrier per block.  The score rows are written with
+// non-temporal stores: they stream to memory instead of displacing the caches (0.217 -> 0.148 ms at config 2).
 constexpr int kWsTok = 256;             // tokens per workgroup
 constexpr int kWsOutStride = kStreamKeys + 8;  // LDS output tile row stride (bf16)
 
@@ -534,7 +535,7 @@ __global__ void __launch_bounds__(512)
           const int id = mt + 256 * u, t = id >> 3, c = id & 7;
           const u32x4 v = *(const u32x4 *)&O[t * kWsOutStride + c * 8];
           const int tok = tok_base + t;
-          if (tok < N) *(u32x4 *)(out + ((int64_t)tok * H + h) * NK + key0 + c * 8) = v;
+          if (tok < N) __builtin_nontemporal_store(v, (u32x4 *)(out + ((int64_t)tok * H + h) * NK + key0 + c * 8));
         }
       }
       if (kb < nkb) __syncthreads();
