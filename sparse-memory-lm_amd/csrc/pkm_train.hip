@@ -80,9 +80,10 @@ __global__ void __launch_bounds__(kTrainThreads)
   const int chunks = NK / EPV;
   char *r1 = (char *)ds1 + row * (int64_t)NK * (F32 ? 4 : 2);
   char *r2 = (char *)ds2 + row * (int64_t)NK * (F32 ? 4 : 2);
-  for (int c = lane; c < chunks; c += kWave) {
-    *(uint4 *)(r1 + (int64_t)c * 16) = uint4{0u, 0u, 0u, 0u};
-    *(uint4 *)(r2 + (int64_t)c * 16) = uint4{0u, 0u, 0u, 0u};
+  typedef unsigned u32x4z __attribute__((ext_vector_type(4)));
+  for (int c = lane; c < chunks; c += kWave) {  // streamed to memory (non-temporal): 2 x NK per row, written once
+    __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r1 + (int64_t)c * 16));
+    __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r2 + (int64_t)c * 16));
   }
   // every zero store acknowledged before the first value store: the value then lands after the zero
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
