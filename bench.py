@@ -9,6 +9,9 @@ HBM GB/s".
                  prompts, then K greedy steps; each step is one replay of the captured whole-step HIP graph
                  (embedding, 6 blocks, lm_head, argmax, KV write).  value = 64 * K / time of the K steps.
   decode_bs1     the same at batch 1.
+  decode_roofline  each decode step against its two floors: the HBM bytes it must move (weights, sub-keys, value
+                 rows, KV cache at the mean timed position) over 8 TB/s, and its kernel count times the measured
+                 device time of a chained kernel in a HIP graph.
   config0        config 0: the B-1M PKM layer forward alone in fp32 over 8 x 256 tokens, on the GPU and as the
                  reference's torch path on the host cores.
   config1        config 1: the same LM with the B-1M memory (1024^2 rows), 512-token prompt, greedy decode at
@@ -98,6 +101,58 @@ def time_decode(model, B, steps, warmup, dev, seed=1, prompt_len=128):
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0
     return B * steps / dt, 1000.0 * dt / steps
+
+
+def chained_launch_us(dev, numel=384, kernels=272, replays=40):
+    """Device time per kernel of a HIP graph of `kernels` back-to-back elementwise kernels, each reading the `numel`
+    fp32 values its predecessor wrote (in-place adds): 384 values are one workgroup, the floor every kernel of a
+    captured decode step pays whatever its work; 262,144 values spread one kernel over the whole chip.
+    272 = the 8 decode steps of one graph replay x 34 kernels."""
+    import torch
+    x = torch.zeros(numel, dtype=torch.float32, device=dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            x.add_(1.0)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(kernels):
+            x.add_(1.0)
+    return 1000.0 * event_time_ms(graph.replay, replays) / kernels
+
+
+def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
+    """The two floors of one fused decode step against its measured time.
+    HBM: the bytes a step must move — every weight matrix once (the tied embedding once as lm_head, plus B embedding
+    rows), every memory layer's sub-keys, the B x heads x knn value rows (bf16 table), the K and V cache rows of
+    positions 0..pos-1 read and row pos written per layer — over 8 TB/s.
+    Launch: the step's kernel count (5 per dense block, 7 per memory block, 2 for the head; one fewer per block
+    where the attention launch does wo as well) x the one-workgroup chained-kernel time of chained_launch_us."""
+    from smlm_hip.model import _FusedDecodeStep
+    cfg = model.cfg
+    C = cfg.d_model
+    w = 0
+    for name, p in model.named_parameters():
+        if name.endswith("values.weight"):
+            continue
+        w += p.numel() * p.element_size()
+    w += B * C * 2                                                      # embedding rows of the step's tokens
+    n_mem = len(cfg.mem_layers)
+    values = n_mem * B * cfg.mem_heads * cfg.mem_knn * C * 2
+    kv = cfg.n_layers * 2 * B * (mean_pos + 1) * C * 2                  # read rows < pos, write row pos
+    total = w + values + kv
+    hbm_ms = total / (HBM_PEAK_GBS * 1e9) * 1e3
+    fold = B <= _FusedDecodeStep.proj_max_batch and cfg.n_heads <= 8
+    launches = (4 if fold else 5) * (cfg.n_layers - n_mem) + (6 if fold else 7) * n_mem + 2
+    launch_ms = launches * launch_us / 1e3
+    return {"bound": "launch" if launch_ms >= hbm_ms else "hbm", "ms_per_step": ms_per_step,
+            "hbm_bytes_per_step": total, "weight_bytes": w, "value_row_bytes": values, "kv_cache_bytes": kv,
+            "mean_position": mean_pos, "hbm_floor_ms": hbm_ms, "hbm_frac": hbm_ms / ms_per_step,
+            "launches_per_step": launches, "chained_launch_us": launch_us,
+            "chained_launch_us_chip_wide": wide_launch_us, "launch_floor_ms": launch_ms,
+            "launch_frac": launch_ms / ms_per_step}
 
 
 def time_prefill(model, B, T, reps, dev, seed=3):
@@ -563,7 +618,7 @@ def main():
         calibration_copy(dev)
         log("calibration copy of 1 GiB done")
     model = None
-    tok_s64 = ms64 = tok_s1 = ms1 = None
+    tok_s64 = ms64 = tok_s1 = ms1 = dec_roof = None
     if "decode" in phases or "cpu" in phases or "offload" in phases:
         cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
         t0 = time.perf_counter()
@@ -574,6 +629,11 @@ def main():
         log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
         tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
         log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
+        launch_us, wide_us = chained_launch_us(dev), chained_launch_us(dev, numel=1 << 18)
+        mean_pos = 128 + args.warmup + (args.steps - 1) / 2.0
+        dec_roof = {"bs64": decode_roofline(model, 64, ms64, mean_pos, launch_us, wide_us),
+                    "bs1": decode_roofline(model, 1, ms1, mean_pos, launch_us, wide_us)}
+        log(f"decode floors: chained launch {launch_us:.2f} us (chip-wide {wide_us:.2f} us); {dec_roof}")
     c0 = c1 = pf = None
     if "config0" in phases:
         c0 = layer_config0(dev, args.reps)
@@ -647,7 +707,7 @@ def main():
                                "(16,777,216 x 384 bf16 values), greedy decode at batch 64, 128-token prompts, "
                                "whole-step hipGraph", "global_batch": 64, "prompt_len": 128,
                    "new_tokens": args.steps},
-        "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1,
+        "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1, "decode_roofline": dec_roof,
         "layer_config0": c0, "decode_config1_bs1": c1, "prefill_config2": pf,
         "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
         "offload_config3": off, "engram_lookup": eng,

@@ -142,6 +142,21 @@ int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, const void *r
                           int H, int head_dim, int max_len, void *out, void *stream);
 
 /*
+ * smlm_decode_attention followed by the attention's output projection (smlm/model.py:107, self.wo), per head:
+ *   parts[b, h, n] = sum_d bf16(y[b, h, d]) * wo[n, h*head_dim + d]   (fp32, n < n_out)
+ * with y the attention output smlm_decode_attention would write.  The sum over h, bf16(sum_h parts[b, h, :]), is
+ * the projection (fp32 accumulation, one rounding); the RMSNORM_PARTS prologue of smlm_decode_linear adds it to
+ * the residual stream, so the projection needs no launch of its own.
+ *   wo     (n_out, >= H*head_dim) bf16 rows at wo + n*wo_row_stride (nn.Linear.weight), 16-byte aligned
+ *   parts  (B, H, n_out) fp32, dense
+ * Other arguments and the out-of-range position (NaN parts) as smlm_decode_attention.
+ */
+int smlm_decode_attention_proj(const void *qkv, int64_t qkv_row_stride, const void *rope_cos, const void *rope_sin,
+                               int rope_dtype, int rope_len, const int64_t *pos, void *k_cache, void *v_cache,
+                               int64_t B, int H, int head_dim, int max_len, const void *wo, int64_t wo_row_stride,
+                               int n_out, float *parts, void *stream);
+
+/*
  * SwiGLU activation of the dense FFN.  Replaces `a, b = w13(x).chunk(2, -1); F.silu(a) * b` of
  * smlm/model.py:110-118 (after the w13 projection) in one launch, with the reference's bf16 roundings:
  *   out[m, c] = bf16( bf16(silu(a[m, c])) * b[m, c] ),  a = in[m, :hidden], b = in[m, hidden:2*hidden]
@@ -215,6 +230,10 @@ int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *
  *            SMLM_LIN_RMSNORM        xs = bf16(x + delta) (delta may be NULL), h = bf16(xs * rsqrt(mean(xs^2) + eps) * g)
  *                                    (the residual add, smlm/model.py:156-163, and the next sublayer's RMSNorm)
  *            SMLM_LIN_EMBED_RMSNORM  xs = emb[tok[m]] (smlm/model.py:268), then as SMLM_LIN_RMSNORM
+ *            SMLM_LIN_RMSNORM_PARTS  as SMLM_LIN_RMSNORM with delta = bf16(sum over q < delta_parts of
+ *                                    delta[m, q, :]) from fp32 (M, delta_parts, K) parts, summed in q order: the
+ *                                    per-head output projections of smlm_decode_attention_proj (1 <= delta_parts
+ *                                    <= 8; not with SMLM_LIN_ARGMAX)
  *            with an RMSNorm prologue, xs is also written to x_out (if not NULL): the residual stream
  *   epilogue SMLM_LIN_STORE          v = bf16(acc + bias); on columns < n_affine v = bf16(v * scale + shift) (eval
  *                                    BatchNorm of the memory query); columns < n_split to out, the rest to out2
@@ -231,7 +250,8 @@ int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *
 typedef enum smlm_linear_prologue {
   SMLM_LIN_PLAIN = 0,
   SMLM_LIN_RMSNORM = 1,
-  SMLM_LIN_EMBED_RMSNORM = 2
+  SMLM_LIN_EMBED_RMSNORM = 2,
+  SMLM_LIN_RMSNORM_PARTS = 3
 } smlm_linear_prologue;
 
 typedef enum smlm_linear_epilogue {
@@ -248,7 +268,7 @@ typedef struct smlm_linear_args {
   int K;                    /* input features */
   const void *x;            /* (M, K) bf16 rows at x + m*x_stride (PLAIN, RMSNORM) */
   int64_t x_stride;
-  const void *delta;        /* (M, K) bf16 or NULL (RMSNORM) */
+  const void *delta;        /* (M, K) bf16 or NULL (RMSNORM); (M, delta_parts, K) fp32 (RMSNORM_PARTS) */
   const int64_t *tok;       /* (M,) token ids (EMBED_RMSNORM) */
   const void *emb;          /* (emb_rows, K) bf16 (EMBED_RMSNORM) */
   int64_t emb_rows;
@@ -267,6 +287,7 @@ typedef struct smlm_linear_args {
   int64_t out2_stride;
   uint64_t *partial;        /* ARGMAX: (M, >= smlm_linear_argmax_blocks(N)) */
   int64_t partial_stride;
+  int delta_parts;          /* RMSNORM_PARTS: number of fp32 parts of delta */
 } smlm_linear_args;
 
 /* Number of 128-column blocks of the ARGMAX epilogue for N columns (the width partial needs). */

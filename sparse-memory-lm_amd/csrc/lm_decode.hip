@@ -9,6 +9,10 @@
 //   3. softmax over t in fp32;
 //   4. y = sum_t p_t v_t, rows split over the workgroup's lanes, partial sums added through LDS; y is written as
 //      bf16 into the (B, H*head_dim) layout the output projection reads.
+// The PROJ variant folds the output projection (model.py:107, wo) in: y, rounded to bf16 as above, is multiplied by
+// the head's column slice of wo, and the n_out fp32 dot products go to parts[b, h, :]; the sum over heads (in head
+// order) is left to the consumer (the RMSNORM_PARTS prologue of smlm_decode_linear), one launch fewer per layer.
+// The slice's first rows are loaded at the start, so they arrive with the cache rows.
 // A position outside [0, min(max_len, rope_len)) writes nothing to the cache and NaN to the output.
 #include "pkm_common.h"
 
@@ -82,16 +86,24 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   }
 }
 
-template <bool ROPE_F32, int HD, int kAttnThreads>
+// Rows of wo per workgroup pass of the projection (PROJ) that are loaded at the start: 512 for 1024 threads and
+// head_dim 64.
+template <int kAttnThreads>
+constexpr int wo_regs() { return kAttnThreads >= 1024 ? 4 : kAttnThreads >= 512 ? 6 : 12; }
+
+template <bool ROPE_F32, int HD, int kAttnThreads, bool PROJ>
 __global__ void __launch_bounds__(kAttnThreads)
     decode_attention_kernel(const uint16_t *__restrict__ qkv, int64_t qkv_stride, const void *__restrict__ rope_cos,
                             const void *__restrict__ rope_sin, int rope_len, const int64_t *__restrict__ pos_ptr,
                             uint16_t *__restrict__ k_cache, uint16_t *__restrict__ v_cache, int H, int max_len,
-                            uint16_t *__restrict__ out) {
+                            uint16_t *__restrict__ out, const uint16_t *__restrict__ wo, int64_t wo_stride,
+                            int n_out, float *__restrict__ parts) {
   constexpr int kAttnWaves = kAttnThreads / kWave;
   constexpr int LPR = HD / 8;            // lanes per cache row (8 dims, 16 bytes each)
   constexpr int RPW = kWave / LPR;       // rows per wavefront per pass
   constexpr int RPB = RPW * kAttnWaves;  // rows per workgroup per pass
+  constexpr int WR = wo_regs<kAttnThreads>();
+  constexpr int RPP = kAttnThreads / LPR;  // wo rows per projection pass (LPR lanes per row, 8 columns each)
   extern __shared__ __align__(16) float smem[];
   float *s_q = smem;                     // [HD]
   float *s_k = s_q + HD;                 // [HD] new token's k (bf16 values)
@@ -103,10 +115,27 @@ __global__ void __launch_bounds__(kAttnThreads)
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int C = H * HD;
+  // the projection's first wo rows (they depend on nothing this step computes); row wr0 + i * RPP, columns
+  // h * HD + wc * 8 .. + 7; passes that start past n_out load nothing, rows past n_out re-read row n_out - 1
+  const int wc = tid % LPR, wr0 = tid / LPR;
+  uint4 wreg[PROJ ? WR : 1];
+  if constexpr (PROJ) {
+#pragma unroll
+    for (int i = 0; i < WR; ++i) {
+      if (i * RPP >= n_out) break;  // workgroup-uniform
+      const int n = min(wr0 + i * RPP, n_out - 1);
+      wreg[i] = *(const uint4 *)(wo + (int64_t)n * wo_stride + h * HD + wc * 8);
+    }
+  }
   const int64_t P = *pos_ptr;
-  uint16_t *o = out + (int64_t)b * C + (int64_t)h * HD;
+  uint16_t *o = PROJ ? nullptr : out + (int64_t)b * C + (int64_t)h * HD;
+  float *po = PROJ ? parts + ((int64_t)b * H + h) * n_out : nullptr;
   if (P < 0 || P >= max_len || P >= rope_len) {
-    for (int i = tid; i < HD; i += kAttnThreads) o[i] = 0x7FC0;  // bf16 NaN
+    if constexpr (PROJ) {
+      for (int i = tid; i < n_out; i += kAttnThreads) po[i] = __builtin_nanf("");
+    } else {
+      for (int i = tid; i < HD; i += kAttnThreads) o[i] = 0x7FC0;  // bf16 NaN
+    }
     return;
   }
   const uint16_t *row = qkv + (int64_t)b * qkv_stride;
@@ -115,7 +144,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   // 0. The first group of cache rows (keys and values of rows < P, which do not depend on this step) is loaded
   // before anything else, so its round trip overlaps the one of the qkv row below.  Row P itself (written in 1.)
   // is never loaded: rows are clamped to P - 1 and row P is taken from LDS.
-  constexpr int U = kAttnUnroll;
+  // (the projection's wo registers leave room for 6 passes under the 128 VGPRs of a 1024-thread workgroup)
+  constexpr int U = PROJ && kAttnThreads >= 1024 ? 6 : kAttnUnroll;
   const int sub = lane % LPR, rw = lane / LPR;
   const int slot = wave * RPW + rw;
   const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
@@ -248,48 +278,121 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
   __syncthreads();
   const float inv = 1.0f / sum;
-  for (int i = tid; i < HD; i += kAttnThreads) {
-    float y = 0.f;
+  if constexpr (!PROJ) {
+    for (int i = tid; i < HD; i += kAttnThreads) {
+      float y = 0.f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
-    o[i] = (uint16_t)bf16_bits_rtne(y * inv);
+      for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
+      o[i] = (uint16_t)bf16_bits_rtne(y * inv);
+    }
+  } else {
+    // 5. parts[b, h, n] = sum_d bf16(y_d) wo[n, h * HD + d]: LPR lanes per wo row, 8 columns each, reduced with
+    // lane shuffles.  y goes through LDS (s_q is free: q has been in registers since step 2).
+    float *s_y = s_q;
+    for (int i = tid; i < HD; i += kAttnThreads) {
+      float y = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
+      s_y[i] = round_bf16(y * inv);
+    }
+    __syncthreads();
+    float yv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) yv[e] = s_y[wc * 8 + e];
+    for (int base = 0; base < n_out; base += WR * RPP) {
+      if (base > 0) {
+#pragma unroll
+        for (int i = 0; i < WR; ++i) {
+          if (base + i * RPP >= n_out) break;  // workgroup-uniform
+          const int n = min(base + wr0 + i * RPP, n_out - 1);
+          wreg[i] = *(const uint4 *)(wo + (int64_t)n * wo_stride + h * HD + wc * 8);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < WR; ++i) {
+        if (base + i * RPP >= n_out) break;  // workgroup-uniform
+        float wf[8];
+        unpack8(wreg[i], wf);
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(yv[e], wf[e], d);
+        d = group_sum<LPR>(d);
+        const int n = base + wr0 + i * RPP;
+        if (wc == 0 && n < n_out) po[n] = d;
+      }
+    }
   }
 }
 
-template <int HD, int NT>
-int launch_attention_nt(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
-                        int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
-                        void *out, hipStream_t stream) {
-  const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave) + (size_t)max_len);
+// Launch arguments of the attention kernels (PROJ: wo and parts set, out unused).
+struct AttnArgs {
+  const void *qkv;
+  int64_t qkv_stride;
+  const void *cos, *sin;
+  int rope_f32, rope_len;
+  const int64_t *pos;
+  void *k_cache, *v_cache;
+  int64_t B;
+  int H, max_len;
+  void *out;
+  const void *wo;
+  int64_t wo_stride;
+  int n_out;
+  float *parts;
+};
+
+template <int HD, int NT, bool PROJ>
+int launch_attention_nt(const AttnArgs &a, hipStream_t stream) {
+  const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave) + (size_t)a.max_len);
   if (shmem > 64 * 1024)
-    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len=%d too long for one workgroup", max_len);
-  const dim3 grid((unsigned)(B * H));
-  if (rope_f32)
-    hipLaunchKernelGGL((decode_attention_kernel<true, HD, NT>), grid, dim3(NT), shmem, stream,
-                       (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
-                       (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len=%d too long for one workgroup", a.max_len);
+  const dim3 grid((unsigned)(a.B * a.H));
+  if (a.rope_f32)
+    hipLaunchKernelGGL((decode_attention_kernel<true, HD, NT, PROJ>), grid, dim3(NT), shmem, stream,
+                       (const uint16_t *)a.qkv, a.qkv_stride, a.cos, a.sin, a.rope_len, a.pos, (uint16_t *)a.k_cache,
+                       (uint16_t *)a.v_cache, a.H, a.max_len, (uint16_t *)a.out, (const uint16_t *)a.wo, a.wo_stride,
+                       a.n_out, a.parts);
   else
-    hipLaunchKernelGGL((decode_attention_kernel<false, HD, NT>), grid, dim3(NT), shmem, stream,
-                       (const uint16_t *)qkv, qkv_stride, cos, sin, rope_len, pos, (uint16_t *)k_cache,
-                       (uint16_t *)v_cache, H, max_len, (uint16_t *)out);
+    hipLaunchKernelGGL((decode_attention_kernel<false, HD, NT, PROJ>), grid, dim3(NT), shmem, stream,
+                       (const uint16_t *)a.qkv, a.qkv_stride, a.cos, a.sin, a.rope_len, a.pos, (uint16_t *)a.k_cache,
+                       (uint16_t *)a.v_cache, a.H, a.max_len, (uint16_t *)a.out, (const uint16_t *)a.wo, a.wo_stride,
+                       a.n_out, a.parts);
   return launch_status("smlm_decode_attention");
 }
 
 // 256 threads per (sequence, head) when those workgroups fill the chip twice over; 512 from one workgroup per CU up
 // (two of them still fit a CU: batch 64 x 6 heads, 0.212 -> 0.206 ms per decode step); otherwise (small decode
 // batches) 1024, so each workgroup's rows are spread over more lanes and its chain of loads and reductions is shorter.
-template <int HD>
-int launch_attention(const void *qkv, int64_t qkv_stride, const void *cos, const void *sin, int rope_f32,
-                     int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H, int max_len,
-                     void *out, hipStream_t stream) {
-  if (B * H >= 512)
-    return launch_attention_nt<HD, 256>(qkv, qkv_stride, cos, sin, rope_f32, rope_len, pos, k_cache, v_cache, B, H,
-                                        max_len, out, stream);
-  if (B * H >= 256)
-    return launch_attention_nt<HD, 512>(qkv, qkv_stride, cos, sin, rope_f32, rope_len, pos, k_cache, v_cache, B, H,
-                                        max_len, out, stream);
-  return launch_attention_nt<HD, 1024>(qkv, qkv_stride, cos, sin, rope_f32, rope_len, pos, k_cache, v_cache, B, H,
-                                       max_len, out, stream);
+template <int HD, bool PROJ>
+int launch_attention(const AttnArgs &a, hipStream_t stream) {
+  if (a.B * a.H >= 512) return launch_attention_nt<HD, 256, PROJ>(a, stream);
+  if (a.B * a.H >= 256) return launch_attention_nt<HD, 512, PROJ>(a, stream);
+  return launch_attention_nt<HD, 1024, PROJ>(a, stream);
+}
+
+template <bool PROJ>
+int launch_attention_hd(const AttnArgs &a, int head_dim, hipStream_t stream) {
+  switch (head_dim) {
+    case 16: return launch_attention<16, PROJ>(a, stream);
+    case 32: return launch_attention<32, PROJ>(a, stream);
+    case 64: return launch_attention<64, PROJ>(a, stream);
+    case 128: return launch_attention<128, PROJ>(a, stream);
+    default: return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: head_dim %d not in {16, 32, 64, 128}", head_dim);
+  }
+}
+
+int check_attention(const void *qkv, int64_t qkv_row_stride, const void *rope_cos, const void *rope_sin,
+                    int rope_dtype, int rope_len, const int64_t *pos, void *k_cache, void *v_cache, int64_t B, int H,
+                    int max_len) {
+  if (!qkv || !rope_cos || !rope_sin || !pos || !k_cache || !v_cache)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: null pointer argument");
+  if (rope_dtype != SMLM_F32 && rope_dtype != SMLM_BF16)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: rope tables must be SMLM_F32 or SMLM_BF16");
+  if (B < 0 || H < 1 || max_len < 1 || rope_len < 1 || B * (int64_t)H > 0x7FFFFFFFLL)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: bad shape B=%lld H=%d max_len=%d", (long long)B, H, max_len);
+  if ((((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) || qkv_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv and caches must be 16-byte aligned");
+  return SMLM_OK;
 }
 
 }  // namespace
@@ -300,26 +403,38 @@ extern "C" int smlm_decode_attention(const void *qkv, int64_t qkv_row_stride, co
                                      void *k_cache, void *v_cache, int64_t B, int H, int head_dim, int max_len,
                                      void *out, void *stream) {
   using namespace smlm;
-  if (!qkv || !rope_cos || !rope_sin || !pos || !k_cache || !v_cache || !out)
-    return fail(SMLM_EINVAL, "smlm_decode_attention: null pointer argument");
-  if (rope_dtype != SMLM_F32 && rope_dtype != SMLM_BF16)
-    return fail(SMLM_EINVAL, "smlm_decode_attention: rope tables must be SMLM_F32 or SMLM_BF16");
-  if (B < 0 || H < 1 || max_len < 1 || rope_len < 1 || B * (int64_t)H > 0x7FFFFFFFLL)
-    return fail(SMLM_EINVAL, "smlm_decode_attention: bad shape B=%lld H=%d max_len=%d", (long long)B, H, max_len);
+  if (!out) return fail(SMLM_EINVAL, "smlm_decode_attention: null pointer argument");
+  int rc = check_attention(qkv, qkv_row_stride, rope_cos, rope_sin, rope_dtype, rope_len, pos, k_cache, v_cache, B,
+                           H, max_len);
+  if (rc != SMLM_OK) return rc;
   if (qkv_row_stride < 3LL * H * head_dim)
     return fail(SMLM_EINVAL, "smlm_decode_attention: qkv_row_stride %lld < 3*H*head_dim", (long long)qkv_row_stride);
-  if ((((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) || qkv_row_stride % 8)
-    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv and caches must be 16-byte aligned");
   if (B == 0) return SMLM_OK;
-  const int f32 = rope_dtype == SMLM_F32;
-  hipStream_t s = (hipStream_t)stream;
-  switch (head_dim) {
-    case 16: return launch_attention<16>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
-    case 32: return launch_attention<32>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
-    case 64: return launch_attention<64>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
-    case 128: return launch_attention<128>(qkv, qkv_row_stride, rope_cos, rope_sin, f32, rope_len, pos, k_cache, v_cache, B, H, max_len, out, s);
-    default: return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: head_dim %d not in {16, 32, 64, 128}", head_dim);
-  }
+  const AttnArgs a{qkv, qkv_row_stride, rope_cos, rope_sin, rope_dtype == SMLM_F32, rope_len, pos, k_cache, v_cache,
+                   B, H, max_len, out, nullptr, 0, 0, nullptr};
+  return launch_attention_hd<false>(a, head_dim, (hipStream_t)stream);
+}
+
+extern "C" int smlm_decode_attention_proj(const void *qkv, int64_t qkv_row_stride, const void *rope_cos,
+                                          const void *rope_sin, int rope_dtype, int rope_len, const int64_t *pos,
+                                          void *k_cache, void *v_cache, int64_t B, int H, int head_dim, int max_len,
+                                          const void *wo, int64_t wo_row_stride, int n_out, float *parts,
+                                          void *stream) {
+  using namespace smlm;
+  if (!wo || !parts) return fail(SMLM_EINVAL, "smlm_decode_attention_proj: null wo or parts");
+  int rc = check_attention(qkv, qkv_row_stride, rope_cos, rope_sin, rope_dtype, rope_len, pos, k_cache, v_cache, B,
+                           H, max_len);
+  if (rc != SMLM_OK) return rc;
+  if (qkv_row_stride < 3LL * H * head_dim)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv_row_stride %lld < 3*H*head_dim", (long long)qkv_row_stride);
+  if (n_out < 1 || wo_row_stride < (int64_t)H * head_dim || wo_row_stride % 8 || (uintptr_t)wo % 16 ||
+      (uintptr_t)parts % 4)
+    return fail(SMLM_EINVAL, "smlm_decode_attention_proj: wo must be 16-byte aligned (n_out=%d rows of stride %lld "
+                "in multiples of 8, >= H*head_dim) and parts 4-byte aligned", n_out, (long long)wo_row_stride);
+  if (B == 0) return SMLM_OK;
+  const AttnArgs a{qkv, qkv_row_stride, rope_cos, rope_sin, rope_dtype == SMLM_F32, rope_len, pos, k_cache, v_cache,
+                   B, H, max_len, nullptr, wo, wo_row_stride, n_out, parts};
+  return launch_attention_hd<true>(a, head_dim, (hipStream_t)stream);
 }
 
 // ---- SwiGLU activation (smlm/model.py:110-118): out = bf16(silu(a)) * b rounded to bf16, a | b = halves of the

@@ -6,6 +6,8 @@
 //             RMSNORM        xs = bf16(x + delta) (delta optional), h = bf16(xs * rsqrt(mean(xs^2) + eps) * g):
 //                            the residual add and the RMSNorm of the next sublayer
 //             EMBED_RMSNORM  xs = emb[tok[m]] (the token embedding), then as RMSNORM
+//             RMSNORM_PARTS  as RMSNORM with delta = bf16(sum_q parts[m, q, :]), fp32 parts summed in q order (the
+//                            per-head output projections the attention kernel wrote: wo costs no launch)
 //                            xs is written once to x_out (the residual stream), by the column block 0.
 //   epilogue  STORE          v = bf16(acc + bias); on the first n_affine columns v = bf16(v * scale + shift) (the
 //                            eval BatchNorm of the memory query); columns [0, n_split) go to out, [n_split, N) to
@@ -123,6 +125,47 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
   }
 }
 
+// RMSNORM_PARTS: delta rows from fp32 parts, a whole wavefront per row (lane = one 8-column chunk, K <= 512): the
+// token groups of this prologue are kPartsRows = 4 rows, row `wave` of the group for wavefront `wave`.  load_parts
+// issues the loads of the row (all its parts at once, before the weight fragments); sum_parts adds them in part
+// order and writes the bf16 delta row to LDS (the prologue's row buffer, where norm_activations reads it back).
+constexpr int kMaxParts = 8;
+constexpr int kPartsRows = kLinWaves;
+
+struct PartsIn {
+  uint4 pv[kMaxParts][2];
+};
+
+__device__ __forceinline__ void load_parts(const smlm_linear_args &a, int64_t m0, int nrows, PartsIn &in) {
+  const int CH = a.K / 8, lane = lane_id(), wave = threadIdx.x / kWave;
+  if (wave >= nrows) return;  // wavefront-uniform
+  const float *src = (const float *)a.delta + (m0 + wave) * (int64_t)a.delta_parts * a.K + min(lane, CH - 1) * 8;
+#pragma unroll
+  for (int q = 0; q < kMaxParts; ++q) {
+    if (q >= a.delta_parts) break;  // uniform
+    const float *pq = src + (int64_t)q * a.K;
+    in.pv[q][0] = *(const uint4 *)pq;
+    in.pv[q][1] = *(const uint4 *)(pq + 4);
+  }
+}
+
+__device__ __forceinline__ void sum_parts(const smlm_linear_args &a, int nrows, uint16_t *sH, int KP, PartsIn &in) {
+  const int CH = a.K / 8, lane = lane_id(), wave = threadIdx.x / kWave;
+  if (wave >= nrows) return;  // wavefront-uniform
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int q = 0; q < kMaxParts; ++q) {
+    if (q >= a.delta_parts) break;
+    const uint4 u0 = in.pv[q][0], u1 = in.pv[q][1];
+    const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __uint_as_float(w[e]);
+  }
+  if (lane < CH) *(uint4 *)(sH + wave * KP + lane * 8) = pack8(acc);
+}
+
 template <int PRO, int CPQ, int MTB>
 __device__ __forceinline__ void norm_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
                                                  uint16_t *sH, int KP, bool first_block, ActIn<CPQ, MTB> &in) {
@@ -140,13 +183,18 @@ __device__ __forceinline__ void norm_activations(const smlm_linear_args &a, int6
     if (p >= passes) continue;
     const int rr = p * 16 + wave * 4 + quarter;
     const bool live = rr < nrows;
+    if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) {  // the delta row sum_parts left in this row of sH
+#pragma unroll
+      for (int j = 0; j < CPQ; ++j)
+        dv[p][j] = live ? *(const uint4 *)(sH + rr * KP + min(sub + 16 * j, CH - 1) * 8) : uint4{0u, 0u, 0u, 0u};
+    }
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < CPQ; ++j) {
       float xf[8];
       unpack8(xv[p][j], xf);
-      if constexpr (PRO == SMLM_LIN_RMSNORM) {
-        if (a.delta) {
+      if constexpr (PRO == SMLM_LIN_RMSNORM || PRO == SMLM_LIN_RMSNORM_PARTS) {
+        if (PRO == SMLM_LIN_RMSNORM_PARTS || a.delta) {
           float df[8];
           unpack8(dv[p][j], df);
 #pragma unroll
@@ -198,7 +246,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int K = a.K, KP = K + 8;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
-  constexpr int TB = MTB * 16;
+  constexpr int TB = PRO == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : MTB * 16;  // token rows per group
   int cb = (int)blockIdx.x, tg = 0;
   if (ntg > 1) {  // id = ((cb / 8) * ntg + tg) * 8 + cb % 8: the token groups of a column block on one XCD
     const int q = (int)blockIdx.x / kXcds;
@@ -223,6 +271,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   // their products are unused): the prologue's arithmetic then overlaps the weights' arrival
   ActIn<CPQ, PRO == SMLM_LIN_PLAIN ? 1 : MTB> act;
   if constexpr (PRO != SMLM_LIN_PLAIN) load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, act);
+  PartsIn parts_in;
+  if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) load_parts(a, m0, nrows, parts_in);
   uint4 areg[NT][MAXS];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -251,6 +301,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       }
     }
   } else {
+    if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) {
+      sum_parts(a, nrows, sH, KP, parts_in);
+      __syncthreads();  // the delta rows in LDS (the weight fragments keep arriving meanwhile)
+    }
     norm_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0, act);
     __syncthreads();
   }
@@ -463,17 +517,20 @@ void launch_linear_mtb(const smlm_linear_args &a, const LinGrid &lg, hipStream_t
 
 template <int PRO, int EPI, int MAXS>
 void launch_linear_cpq(const smlm_linear_args &a, const LinGrid &lg, hipStream_t stream) {
-  if (lg.mtb == 1) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);
+  if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);  // mtb is 1
+  else if (lg.mtb == 1) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);
   else launch_linear_mtb<PRO, EPI, MAXS, kMaxTiles>(a, lg, stream);
 }
 
 template <int PRO>
 void launch_linear_pro(const smlm_linear_args &a, const LinGrid &grid, hipStream_t stream) {
   const int steps = a.K / 32;
-  if (a.epilogue == SMLM_LIN_ARGMAX) {
-    if (steps <= 12) launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 12>(a, grid, stream);
-    else launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 16>(a, grid, stream);
-    return;
+  if constexpr (PRO != SMLM_LIN_RMSNORM_PARTS) {
+    if (a.epilogue == SMLM_LIN_ARGMAX) {
+      if (steps <= 12) launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 12>(a, grid, stream);
+      else launch_linear_cpq<PRO, SMLM_LIN_ARGMAX, 16>(a, grid, stream);
+      return;
+    }
   }
   const int per_wave = (steps + kLinWaves - 1) / kLinWaves;
 #define SMLM_LIN_MAXS(EPI)                                                               \
@@ -501,7 +558,8 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   if (!a) return fail(SMLM_EINVAL, "smlm_decode_linear: null argument block");
   const smlm_linear_args &A = *a;
   const int pro = A.prologue, epi = A.epilogue;
-  if (pro != SMLM_LIN_PLAIN && pro != SMLM_LIN_RMSNORM && pro != SMLM_LIN_EMBED_RMSNORM)
+  if (pro != SMLM_LIN_PLAIN && pro != SMLM_LIN_RMSNORM && pro != SMLM_LIN_EMBED_RMSNORM &&
+      pro != SMLM_LIN_RMSNORM_PARTS)
     return fail(SMLM_EINVAL, "smlm_decode_linear: unknown prologue %d", pro);
   if (epi != SMLM_LIN_STORE && epi != SMLM_LIN_SWIGLU && epi != SMLM_LIN_ARGMAX)
     return fail(SMLM_EINVAL, "smlm_decode_linear: unknown epilogue %d", epi);
@@ -528,8 +586,13 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
       return fail(SMLM_EINVAL, "smlm_decode_linear: the RMSNorm needs a 16-byte aligned weight and eps >= 0");
     if (A.K > 480)
       return fail(SMLM_EUNSUPPORTED, "smlm_decode_linear: normalised rows of K=%d > 480 do not fit in LDS", A.K);
-    if ((A.delta && (pro != SMLM_LIN_RMSNORM || !aligned16(A.delta))) || (A.x_out && !aligned16(A.x_out)))
-      return fail(SMLM_EINVAL, "smlm_decode_linear: delta (RMSNORM only) and x_out must be 16-byte aligned");
+    if ((A.delta && ((pro != SMLM_LIN_RMSNORM && pro != SMLM_LIN_RMSNORM_PARTS) || !aligned16(A.delta))) ||
+        (A.x_out && !aligned16(A.x_out)))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: delta (RMSNORM prologues only) and x_out must be 16-byte aligned");
+    if (pro == SMLM_LIN_RMSNORM_PARTS &&
+        (!A.delta || A.delta_parts < 1 || A.delta_parts > kMaxParts || epi == SMLM_LIN_ARGMAX))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: RMSNORM_PARTS needs delta with 1..%d parts (delta_parts=%d) and "
+                  "no ARGMAX epilogue", kMaxParts, A.delta_parts);
   } else if (A.delta || A.x_out) {
     return fail(SMLM_EINVAL, "smlm_decode_linear: delta and x_out belong to the RMSNorm prologues");
   }
@@ -555,7 +618,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   // epilogue over more than 16 rows, whose 128-column blocks already fill the chip
   LinGrid lg;
   lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
-  const int tb = lg.mtb * 16;
+  const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : lg.mtb * 16;
   const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
   lg.ncb = (cols + cols_per_block - 1) / cols_per_block;
   lg.ntg = (int)((A.M + tb - 1) / tb);
@@ -573,6 +636,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   hipStream_t s = (hipStream_t)stream;
   if (pro == SMLM_LIN_PLAIN) launch_linear_pro<SMLM_LIN_PLAIN>(A, lg, s);
   else if (pro == SMLM_LIN_RMSNORM) launch_linear_pro<SMLM_LIN_RMSNORM>(A, lg, s);
+  else if (pro == SMLM_LIN_RMSNORM_PARTS) launch_linear_pro<SMLM_LIN_RMSNORM_PARTS>(A, lg, s);
   else launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, lg, s);
   return launch_status("smlm_decode_linear");
 }

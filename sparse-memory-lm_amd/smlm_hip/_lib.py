@@ -19,7 +19,7 @@ OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
 _p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # smlm_linear_prologue / smlm_linear_epilogue
-LIN_PLAIN, LIN_RMSNORM, LIN_EMBED_RMSNORM = range(3)
+LIN_PLAIN, LIN_RMSNORM, LIN_EMBED_RMSNORM, LIN_RMSNORM_PARTS = range(4)
 LIN_STORE, LIN_SWIGLU, LIN_ARGMAX = range(3)
 
 
@@ -30,7 +30,7 @@ class LinearArgs(ctypes.Structure):
         ("x", _p), ("x_stride", _i64), ("delta", _p), ("tok", _p), ("emb", _p), ("emb_rows", _i64),
         ("norm_w", _p), ("eps", ctypes.c_float), ("x_out", _p), ("w", _p), ("bias", _p), ("scale", _p),
         ("shift", _p), ("n_affine", _i), ("n_split", _i), ("out", _p), ("out_stride", _i64), ("out2", _p),
-        ("out2_stride", _i64), ("partial", _p), ("partial_stride", _i64),
+        ("out2_stride", _i64), ("partial", _p), ("partial_stride", _i64), ("delta_parts", _i),
     ]
 
 # name -> (restype, argtypes); every function declared in include/smlm_pkm.h
@@ -44,6 +44,8 @@ EXPORTS = {
     "smlm_pkm_select_bag": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p]),
     "smlm_pkm_quantize": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
     "smlm_decode_attention": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _p]),
+    "smlm_decode_attention_proj": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _i64, _i, _p,
+                                        _p]),
     "smlm_swiglu": (_i, [_p, _i64, _p, _i64, _i, _p]),
     "smlm_greedy_argmax": (_i, [_p, _i64, _i64, _i, _p, _p, _p, _i64, _i64, _p]),
     "smlm_add_rmsnorm": (_i, [_p, _p, _p, ctypes.c_float, _i64, _i, _p, _p, _p]),

@@ -439,8 +439,16 @@ class _FusedDecodeStep:
     (smlm/model.py:63-118, 156-163, 266-293; smlm/pkm.py:186-228) with the same bf16 roundings: 5 launches per
     dense block, 7 per memory block and 2 for the head, instead of the ~10 PyTorch launches per block.
 
+    At batches up to proj_max_batch the attention launch also does wo, per head (decode_attention_proj), and the
+    next launch's prologue sums the heads: 4 launches per dense block, 6 per memory block (MI355X, config 3:
+    0.155 -> 0.144 ms per step at batch 1, 0.177 -> 0.173 at 32).  Larger batches keep the wo launch: the summing
+    prologue works on 4-token groups, and from 48 tokens up re-reading the weights per group costs more than the
+    launch (0.196 -> 0.236 ms at 64).
+
     Derived weights (the concatenated query_proj | swilu_proj and its bias) are built at construction and rebuilt
     on an eager run after a parameter changed; a captured graph keeps what it was captured with."""
+
+    proj_max_batch = 32
 
     @staticmethod
     def supported(model, dtype):
@@ -498,6 +506,7 @@ class _FusedDecodeStep:
         if not torch.cuda.is_current_stream_capturing() and self._params_tag() != self._tag:
             self._prepare()
         B = tok.shape[0]
+        proj = B <= self.proj_max_batch and model.cfg.n_heads <= 8
         x = delta = None
         for i, blk in enumerate(model.layers):
             at = blk.attn
@@ -506,8 +515,12 @@ class _FusedDecodeStep:
                                                norm=blk.attn_norm, write_x=True)
             else:
                 x, qkv = kernels.decode_linear(at.wqkv.weight, x, delta=delta, norm=blk.attn_norm, write_x=True)
-            y = kernels.decode_attention(qkv, at.rope.cos, at.rope.sin, pos, caches[i].k, caches[i].v)
-            delta = kernels.decode_linear(at.wo.weight, y)
+            if proj:
+                delta = kernels.decode_attention_proj(qkv, at.rope.cos, at.rope.sin, pos, caches[i].k, caches[i].v,
+                                                      at.wo.weight)
+            else:
+                y = kernels.decode_attention(qkv, at.rope.cos, at.rope.sin, pos, caches[i].k, caches[i].v)
+                delta = kernels.decode_linear(at.wo.weight, y)
             if blk.is_memory:
                 m = blk.ffn
                 w, b = self.mem[i]

@@ -8,6 +8,8 @@ accumulates in fp32 in its own order and rounds once); the residual stream (x + 
 argmax token is exact wherever the best logit is separated from the runner-up, and planted exact ties resolve to
 the lowest column.
 """
+import ctypes
+
 import pytest
 import torch
 
@@ -194,6 +196,57 @@ def test_decode_linear_rejects_bad_shapes():
         K.decode_linear(w2, x2, norm=make_norm(1024, torch.Generator().manual_seed(0)))
 
 
+@pytest.mark.parametrize("M,NP,swiglu", [(1, 6, True), (1, 6, False), (3, 1, True), (4, 8, False), (16, 6, True),
+                                         (17, 6, False), (40, 3, True), (64, 6, False)])
+def test_rmsnorm_parts_prologue_equals_summed_delta(M, NP, swiglu):
+    """The RMSNORM_PARTS prologue (delta = fp32 parts summed in part order, rounded to bf16 once) gives exactly
+    what the RMSNORM prologue gives on that bf16 delta: the same residual stream and the same outputs, bit for
+    bit (one row per wavefront, several rows per wavefront, several token groups)."""
+    note(f"decode_linear parts prologue M={M} parts={NP} swiglu={swiglu}")
+    g = torch.Generator().manual_seed(M * 10 + NP)
+    K_ = 384
+    x = bf(torch.randn(M, K_, generator=g))
+    parts = torch.randn(M, NP, K_, generator=g) * 0.5
+    d = parts[:, 0].clone()
+    for q in range(1, NP):
+        d = d + parts[:, q]
+    d = bf(d)
+    norm = make_norm(K_, g)
+    if swiglu:
+        w = bf(torch.randn(2048, K_, generator=g) * 0.05).to(DEV)
+        kw = dict(norm=norm, write_x=True, swiglu=True)
+    else:
+        w = bf(torch.randn(2048 + 384, K_, generator=g) * 0.05).to(DEV)
+        b = bf(torch.randn(2048 + 384, generator=g) * 0.1).to(DEV)
+        kw = dict(norm=norm, write_x=True, bias=b, n_split=2048)
+    xs, y = K.decode_linear(w, x.to(DEV), delta=parts.to(DEV), **kw)
+    xs_ref, y_ref = K.decode_linear(w, x.to(DEV), delta=d.to(DEV), **kw)
+    assert torch.equal(xs, xs_ref)
+    assert torch.equal(xs.cpu(), bf(x.double() + d.double()))
+    if swiglu:
+        assert torch.equal(y, y_ref)
+    else:
+        assert torch.equal(y[0], y_ref[0]) and torch.equal(y[1], y_ref[1])
+
+
+def test_rmsnorm_parts_prologue_rejects():
+    x = torch.zeros(2, 384, dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros(64, 384, dtype=torch.bfloat16, device=DEV)
+    norm = make_norm(384, torch.Generator().manual_seed(0))
+    with pytest.raises(ValueError):                                   # more than 8 parts
+        K.decode_linear(w, x, delta=torch.zeros(2, 9, 384, device=DEV), norm=norm)
+    with pytest.raises(ValueError):                                   # parts with the argmax epilogue
+        K.decode_linear(w, x, delta=torch.zeros(2, 6, 384, device=DEV), norm=norm, argmax=True)
+    a = _lib.LinearArgs()                                             # the library's own check: 0 parts
+    a.prologue, a.epilogue, a.M, a.N, a.K = _lib.LIN_RMSNORM_PARTS, _lib.LIN_STORE, 2, 64, 384
+    parts = torch.zeros(2, 1, 384, device=DEV)
+    out = torch.empty(2, 64, dtype=torch.bfloat16, device=DEV)
+    a.x, a.x_stride, a.delta, a.delta_parts = x.data_ptr(), 384, parts.data_ptr(), 0
+    a.norm_w, a.eps, a.w = norm.weight.data_ptr(), 1e-5, w.data_ptr()
+    a.n_split, a.out, a.out_stride = 64, out.data_ptr(), 64
+    assert _lib.lib().smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+
+
 # ------------------------------------------------------------------------------------- fused selection + value bag
 def _tables(kind, rows, D, seed):
     """A (rows, D) value table drawn on the device (N(0, 0.02)), in the given inference format."""
@@ -265,18 +318,22 @@ def _prefilled(model, B, P, seed):
     return dec, prompt
 
 
+# proj_max_batch 0: the attention output goes through its own wo launch; 64: wo is folded into the attention
+# launch and summed over heads in the next launch's prologue
+@pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
-def test_fused_step_logits_match_generic_step():
+def test_fused_step_logits_match_generic_step(monkeypatch, proj_max):
     """The fused decode step (no memory layer) against Transformer.forward's single-token static-cache step on
     the same caches and token: logits within 2e-2 of their scale (the two paths round their GEMMs in different
     orders), and the step's token is the argmax of its own logits wherever that is separated."""
     from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
+    monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=1024, d_model=384, n_layers=3, n_heads=6, ffn_hidden=1024, max_seq_len=64)
     torch.manual_seed(0)
     m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
     assert _FusedDecodeStep.supported(m, torch.bfloat16)
-    for B in (1, 5):
-        note(f"fused step vs generic B={B}")
+    for B in (1, 5, 40):
+        note(f"fused step vs generic B={B} proj_max_batch={proj_max}")
         dec, _ = _prefilled(m, B, 12, B)
         assert dec.fused is not None
         ref = m(dec.tok, kv_caches=dec.caches, pos0=dec.pos.clone()).float()[:, -1]
@@ -292,17 +349,19 @@ def test_fused_step_logits_match_generic_step():
         assert torch.equal(dec.hist[:, pos0 + 1], dec.tok.view(-1))
 
 
+@pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
-def test_fused_generate_multi_step_graph_matches_eager():
+def test_fused_generate_multi_step_graph_matches_eager(monkeypatch, proj_max):
     """generate() on the fused step: the graph of steps_per_graph steps in a row plus single-step replays (19
     tokens = 2 runs of 8 + 3 single steps) gives the eager loop's tokens exactly, on every call."""
-    from smlm_hip.model import ModelConfig, Transformer, _StepDecoder
+    from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep, _StepDecoder
+    monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=1024, d_model=384, n_layers=3, n_heads=6, ffn_hidden=1024, max_seq_len=64)
     torch.manual_seed(1)
     m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
     assert _StepDecoder.steps_per_graph == 8
     prompt = torch.randint(0, 1024, (2, 9), generator=torch.Generator().manual_seed(5)).to(DEV)
-    note("fused generate multi-step graph B=2")
+    note(f"fused generate multi-step graph B=2 proj_max_batch={proj_max}")
     eager = m.generate(prompt, 19, use_graph=False)
     graph = m.generate(prompt, 19, use_graph=True)
     graph2 = m.generate(prompt, 19, use_graph=True)
@@ -310,8 +369,9 @@ def test_fused_generate_multi_step_graph_matches_eager():
     assert torch.equal(graph, eager) and torch.equal(graph2, eager)
 
 
+@pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
-def test_fused_step_with_memory_layer_matches_torch_path():
+def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
     """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its selection is
     bit-exact against the oracle on the step's own sub-key scores, and its logits are within 1e-2 of the fp32
     torch path (oracle/torch_path.py) given that selection (the prompt pass does not reach the step through
@@ -319,7 +379,8 @@ def test_fused_step_with_memory_layer_matches_torch_path():
     import numpy as np
     import oracle.pkm_oracle as O
     import oracle.torch_path as TP
-    from smlm_hip.model import ModelConfig, Transformer
+    from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
+    monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=512, d_model=128, n_layers=3, n_heads=2, ffn_hidden=256, max_seq_len=64,
                       mem_layers=[2], mem_n_keys=128, mem_heads=4, mem_knn=16, mem_k_dim=64)
     torch.manual_seed(3)
@@ -333,7 +394,7 @@ def test_fused_step_with_memory_layer_matches_torch_path():
     for kind in ("bf16", "int8"):
         m.set_memory_inference_table(kind)
         B, P = 3, 10
-        note(f"fused step memory layer table={kind}")
+        note(f"fused step memory layer table={kind} proj_max_batch={proj_max}")
         dec, prompt = _prefilled(m, B, P, 7)
         assert dec.fused is not None
         rec = {}

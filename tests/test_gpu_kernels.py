@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle.pkm_oracle as O
+from smlm_hip import _lib
 from smlm_hip import kernels as K
 
 pytestmark = pytest.mark.gpu
@@ -390,7 +391,67 @@ def test_decode_attention_bad_position():
     for P in (L, -1, 10 ** 6):
         out = K.decode_attention(qkv, cos, cos, torch.tensor(P, device=DEV), kc, vc)
         assert torch.isnan(out.float()).all()
+        parts = K.decode_attention_proj(qkv, cos, cos, torch.tensor(P, device=DEV), kc, vc,
+                                        torch.ones(64, H * hd, dtype=torch.bfloat16, device=DEV))
+        assert parts.shape == (B, H, 64) and torch.isnan(parts).all()
     assert not kc.any() and not vc.any()
+
+
+# B x H picks 1024 / 512 / 256 threads; the wo rows cover one or several loads of a workgroup's wo registers;
+# P past 768 makes the 1024-thread variant load its cache rows in two groups
+@pytest.mark.parametrize("B,H,hd,max_len,P,N", [(1, 6, 64, 394, 300, 384), (4, 6, 64, 1100, 767, 384),
+                                                (2, 6, 64, 1100, 1000, 1500), (64, 6, 64, 394, 200, 384),
+                                                (100, 6, 64, 64, 30, 384), (3, 4, 32, 100, 57, 200),
+                                                (2, 2, 16, 40, 1, 1100), (2, 3, 128, 300, 299, 384),
+                                                (1, 6, 64, 394, 0, 384)])
+def test_decode_attention_proj_matches_attention_then_wo(B, H, hd, max_len, P, N):
+    """The attention with wo folded in: parts[b, h] = bf16(y[b, h]) @ wo[:, h*hd:(h+1)*hd].T with y what
+    decode_attention writes (the same arithmetic up to y), within fp32 rounding of the fp64 products (2^-20 of
+    the sum of their magnitudes), and the caches written exactly as decode_attention writes them."""
+    note(f"decode attention proj B={B} H={H} hd={hd} max_len={max_len} P={P} N={N}")
+    g = torch.Generator().manual_seed(B * 1000 + P + N)
+    C = H * hd
+    qkv = torch.randn(B, 3 * C, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(B, H, max_len, hd, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, H, max_len, hd, generator=g).to(torch.bfloat16).to(DEV)
+    wo = (torch.randn(N, C, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2).float() / hd))
+    ang = torch.outer(torch.arange(max_len).float(), inv)
+    cos, sin = ang.cos().to(DEV), ang.sin().to(DEV)
+    pos = torch.tensor(P, device=DEV)
+    k1, v1 = kc.clone(), vc.clone()
+    y = K.decode_attention(qkv, cos, sin, pos, k1, v1)
+    k2, v2 = kc.clone(), vc.clone()
+    parts = K.decode_attention_proj(qkv, cos, sin, pos, k2, v2, wo)
+    assert parts.shape == (B, H, N) and parts.dtype == torch.float32
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    yh = y.double().cpu().view(B, H, 1, hd)
+    wh = wo.double().cpu().view(N, H, hd).permute(1, 2, 0)                   # (H, hd, N)
+    ref = (yh @ wh).squeeze(2)                                              # (B, H, N)
+    bound = ((yh.abs() @ wh.abs()).squeeze(2)) * 2 ** -20 + 1e-30
+    err = (parts.double().cpu() - ref).abs()
+    assert bool((err <= bound).all()), f"worst {float((err / bound).max())} x the bound"
+    # the sum over heads is the projection of the plain path (its linear kernel takes N in multiples of 16)
+    if N % 16 == 0:
+        proj = K.decode_linear(wo, y)
+        diff = (parts.cpu().sum(1).to(torch.bfloat16).double() - proj.double().cpu()).abs()
+        assert float(diff.max()) <= 2 ** -7 * float(proj.double().abs().max())
+
+
+def test_decode_attention_proj_rejects():
+    B, H, hd, L = 2, 2, 64, 16
+    qkv = torch.zeros(B, 3 * H * hd, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(B, H, L, hd, dtype=torch.bfloat16, device=DEV)
+    cos = torch.ones(L, hd // 2, device=DEV)
+    pos = torch.tensor(1, device=DEV)
+    with pytest.raises(ValueError):                                   # wo columns != H * head_dim
+        K.decode_attention_proj(qkv, cos, cos, pos, kc, kc.clone(), torch.zeros(8, 100, dtype=torch.bfloat16,
+                                                                                  device=DEV))
+    with pytest.raises(ValueError):                                   # fp32 wo
+        K.decode_attention_proj(qkv, cos, cos, pos, kc, kc.clone(), torch.zeros(8, H * hd, device=DEV))
+    assert _lib.lib().smlm_decode_attention_proj(
+        qkv.data_ptr(), qkv.stride(0), cos.data_ptr(), cos.data_ptr(), _lib.F32, L, pos.data_ptr(), kc.data_ptr(),
+        kc.data_ptr(), B, H, hd, L, None, H * hd, 8, None, None) == _lib.EINVAL
 
 
 # ------------------------------------------------------------------------------------------------ decode-step helpers
