@@ -136,3 +136,54 @@ def test_decode_linear_argument_checks():
     assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.OK
     assert lib.smlm_linear_argmax_blocks(32000) == 250 and lib.smlm_linear_argmax_blocks(129) == 2
     assert lib.smlm_argmax_finish(None, 1, 1, 1, fake, fake, None, 0, 0, 1, None) == _lib.EINVAL
+
+
+def test_parts_prologue_and_attention_proj_argument_checks():
+    """The RMSNORM_PARTS prologue and smlm_decode_attention_proj refuse bad arguments before any launch."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    a = _lib.LinearArgs()
+    a.prologue, a.epilogue, a.M, a.N, a.K = _lib.LIN_RMSNORM_PARTS, _lib.LIN_STORE, 2, 64, 384
+    a.x, a.x_stride, a.w, a.norm_w, a.n_split, a.out, a.out_stride = fake, 384, fake, fake, 64, fake, 64
+    a.delta, a.delta_parts = None, 6                      # no parts
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.delta = fake
+    for bad in (0, 9):                                    # 1..8 parts
+        a.delta_parts = bad
+        assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "parts" in _lib.last_error()
+    a.delta_parts, a.epilogue, a.partial, a.partial_stride = 6, _lib.LIN_ARGMAX, fake, 1   # not with ARGMAX
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.epilogue, a.M = _lib.LIN_STORE, 0                   # zero rows: a valid no-op
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.OK
+    # attention + wo: null wo / parts, short wo rows, misaligned wo
+    args = [fake, 1152, fake, fake, _lib.F32, 16, fake, fake, fake, 2, 6, 64, 16]
+    assert lib.smlm_decode_attention_proj(*args, None, 384, 384, fake, None) == _lib.EINVAL
+    assert lib.smlm_decode_attention_proj(*args, fake, 384, 384, None, None) == _lib.EINVAL
+    assert lib.smlm_decode_attention_proj(*args, fake, 200, 384, fake, None) == _lib.EINVAL
+    assert lib.smlm_decode_attention_proj(*args, ctypes.c_void_p(0x1008), 384, 384, fake, None) == _lib.EINVAL
+    args[9] = 0                                           # B = 0: a valid no-op
+    assert lib.smlm_decode_attention_proj(*args, fake, 384, 384, fake, None) == _lib.OK
+
+
+def test_bench_decode_roofline_accounting():
+    """bench.py's decode floors on the config-3 model (meta tensors, nothing allocated): the bytes a step moves and
+    its launch count, with and without wo folded into the attention launch."""
+    import bench
+    from smlm_hip.model import Transformer, _FusedDecodeStep
+    cfg = bench.lm_config(4096, 400)
+    with torch.device("meta"):
+        m = Transformer(cfg)
+    m = m.to(torch.bfloat16)
+    C, L = 384, 6
+    weights = 2 * (32000 * C + 5 * (3 * C * C + C * C + 2 * 1024 * C + 1024 * C)       # embedding / lm_head, dense
+                   + 4 * C * C + 2048 * C + 2 * C * C + 4 * 2 * 4096 * 256            # block 3: attention, query,
+                   + 2048 * 3 + 2 * C + (2 * L + 1) * C)                              # swilu, value, keys; biases,
+    r = bench.decode_roofline(m, 64, 0.2, 100.0, 1.5, 1.8)                            # BatchNorm, norms
+    assert r["weight_bytes"] == weights + 64 * C * 2
+    assert r["value_row_bytes"] == 64 * 4 * 32 * C * 2
+    assert r["kv_cache_bytes"] == L * 2 * 64 * 101 * C * 2
+    assert r["launches_per_step"] == 34 and r["bound"] == "launch"
+    assert abs(r["launch_floor_ms"] - 34 * 1.5e-3) < 1e-12
+    assert abs(r["hbm_floor_ms"] - r["hbm_bytes_per_step"] / 8e12 * 1e3) < 1e-12
+    assert _FusedDecodeStep.proj_max_batch >= 1
+    assert bench.decode_roofline(m, 1, 0.15, 100.0, 1.5, 1.8)["launches_per_step"] == 28
