@@ -358,8 +358,12 @@ def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
 @pytest.mark.parametrize("B,H,hd,max_len,P,rope", [(64, 6, 64, 394, 300, "bf16"), (1, 6, 64, 394, 0, "bf16"),
                                                     (1, 6, 64, 394, 393, "f32"), (3, 4, 32, 100, 57, "f32"),
                                                     (2, 2, 16, 40, 1, "bf16"), (2, 3, 128, 300, 299, "bf16"),
-                                                    (5, 6, 64, 600, 511, "f32")])
+                                                    (5, 6, 64, 600, 511, "f32"), (20, 6, 64, 300, 250, "bf16"),
+                                                    (1, 6, 64, 1100, 1000, "f32")])
 def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
+    """1024 / 512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the
+    last slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second
+    round trip)."""
     note(f"decode attention B={B} H={H} hd={hd} max_len={max_len} P={P}")
     g = torch.Generator().manual_seed(B * 1000 + P)
     C = H * hd
