@@ -359,7 +359,7 @@ def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
                                                     (1, 6, 64, 394, 393, "f32"), (3, 4, 32, 100, 57, "f32"),
                                                     (2, 2, 16, 40, 1, "bf16"), (2, 3, 128, 300, 299, "bf16"),
                                                     (5, 6, 64, 600, 511, "f32"), (20, 6, 64, 300, 250, "bf16"),
-                                                    (1, 6, 64, 1100, 1000, "f32")])
+                                                    (1, 6, 64, 1100, 1050, "f32")])
 def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
     """1024 / 512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the
     last slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second
