@@ -86,8 +86,8 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   }
 }
 
-// Rows of wo per workgroup pass of the projection (PROJ) that are loaded at the start: 512 for 1024 threads and
-// head_dim 64.
+// Passes of wo rows the projection (PROJ) holds in registers, the first of them loaded at the start (one pass =
+// threads / (head_dim / 8) rows: with 1024 threads and head_dim 64, 4 passes = 512 rows).
 template <int kAttnThreads>
 constexpr int wo_regs() { return kAttnThreads >= 1024 ? 4 : kAttnThreads >= 512 ? 6 : 12; }
 
