@@ -349,6 +349,26 @@ def test_fused_step_logits_match_generic_step(monkeypatch, proj_max):
         assert torch.equal(dec.hist[:, pos0 + 1], dec.tok.view(-1))
 
 
+@pytest.mark.parametrize("n_heads", [8, 16])
+@torch.no_grad()
+def test_fused_step_head_counts(n_heads):
+    """d_model 256 with 8 heads (head_dim 32: wo folded in as 8 parts, the most the summing prologue takes) and 16
+    heads (head_dim 16: more parts than that, so the step keeps its wo launch): logits within 2e-2 of
+    Transformer.forward's static-cache step."""
+    from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
+    cfg = ModelConfig(vocab_size=512, d_model=256, n_layers=2, n_heads=n_heads, ffn_hidden=512, max_seq_len=48)
+    torch.manual_seed(n_heads)
+    m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
+    assert _FusedDecodeStep.supported(m, torch.bfloat16)
+    note(f"fused step d_model=256 heads={n_heads}")
+    dec, _ = _prefilled(m, 3, 10, n_heads)
+    assert dec.fused is not None
+    ref = m(dec.tok, kv_caches=dec.caches, pos0=dec.pos.clone()).float()[:, -1]
+    got = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True).float()
+    err = float((got - ref).abs().max() / ref.abs().max())
+    assert err < 2e-2, err
+
+
 @pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
 def test_fused_generate_multi_step_graph_matches_eager(monkeypatch, proj_max):
