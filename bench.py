@@ -1,38 +1,35 @@
 """Benchmark of the product-key-memory lookup on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--phases ...]
 
-Prints ONE JSON line.  Metric: "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather
-HBM GB/s".
-  value          decode tok/s of config 3 at batch 64: the 21M LM (d=384, 6 layers, vocab 32000) with the B-16M
-                 memory (4096^2 = 16,777,216 x 384 bf16 values, 12.9 GB) replacing layer 3's FFN, 128-token
-                 prompts, then K greedy steps; each step is one replay of the captured whole-step HIP graph
-                 (embedding, 6 blocks, lm_head, argmax, KV write).  value = 64 * K / time of the K steps.
-  decode_bs1     the same at batch 1.
-  decode_roofline  each decode step against its two floors: the HBM bytes it must move (weights, sub-keys, value
-                 rows, KV cache at the mean timed position) over 8 TB/s, and its kernel count times the measured
-                 device time of a chained kernel in a HIP graph.
-  config0        config 0: the B-1M PKM layer forward alone in fp32 over 8 x 256 tokens, on the GPU and as the
-                 reference's torch path on the host cores.
-  config1        config 1: the same LM with the B-1M memory (1024^2 rows), 512-token prompt, greedy decode at
-                 batch 1 (whole-step graph).
+Prints ONE JSON line, whatever a phase raises (a failed phase is recorded under "phase_errors").  Metric
+"decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather HBM GB/s".  Phases, in the
+order they run (the headline ones first):
+  decode         value: config 3 decode tok/s at batch 64 -- the 21M LM (d=384, 6 layers, vocab 32000) with the
+                 B-16M memory (4096^2 = 16,777,216 x 384 bf16 values, 12.9 GB) replacing layer 3's FFN,
+                 128-token prompts (prefilled once, untimed), then 256 greedy tokens.  A step is one such
+                 256-token generation (32 replays of the captured 8-step whole-step HIP graph); W untimed and K
+                 timed generations, each bracketed by synchronisations (the loop of smlm/train.py:283-301).
+                 value = 64 * 256 * K / time.  The same at batch 1, and each token step against its floors
+                 (decode_roofline: HBM bytes / 8 TB/s; kernel count x the chained-launch time).
+  gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out
+                 (3,439,329,280 algorithmic bytes per call), and the uniform-index control of the same shapes.
+                 roofline: the control's algorithmic GB/s (= its physical traffic: no row repeats in cache) over
+                 HBM peak, from HIP events on the launch stream; roofline.zipf: the Zipf call's algorithmic rate
+                 and its physical rate from the committed rocprofv3 counters (profiles/gather_config4_pmc.txt).
+  cpu            cpu_baseline: the reference's torch path (oracle/torch_path.py) on the host cores, config 3 at
+                 batch 64 (and 1), a bounded sample of the 256 steps; config 4 on the host (chunked int8 gather and
+                 dequantise + embedding_bag) over 2,048 tokens; config 2 over one 2048-token prompt.
+  config1        config 1: the LM with the B-1M memory (1024^2 rows), 512-token prompt, 256 greedy tokens, bs 1.
+  config0        config 0: the B-1M PKM layer forward alone in fp32 over 8 x 256 tokens, GPU and host CPU.
   prefill        config 2: the LM with the B-4M memory (2048^2 rows) forward over 8 x 2048 prompt tokens (no
-                 cache), tokens / median forward time; `attention`: the prompt-pass attention kernel alone at that
-                 shape, causal flops / time against the bf16 MFMA peak.
-  pkm_lookup     config 2 (B-4M, 8 x 2048 tokens): scoring + selection + value bag kernels, tokens / time.
-  gather         config 4: int8 row-quantised B-16M table, 65,536 tokens x 128 Zipf(1.1) lookups, fp32 out;
-                 algorithmic bytes 3,439,329,280 per call; plus a uniform-index control.
-  train_kernels  the training side at the reference's training shape (4,096 tokens x 128 lookups per micro-batch,
-                 B-1M fp32 table): row-sparse bag backward, lazy row Adam (fp32 / bf16 / int8 moments) on the
-                 rows of a 32,768-token step, selection backward at config 2; algorithmic GB/s each.
-  offload        config 3 decode with the B-16M table as q4 in HBM, q4 / bf16 in pinned host RAM read over the
-                 host link (zero-copy, graphs), and bs1 from a q4 file through mmap (staged, no graphs).
-  engram_lookup  the Engram n-gram hash, row gather (fp32 / bf16) and row-sparse backward over 8 x 2048 tokens x
-                 16 lookups of 24-wide rows (524,287 rows per head); algorithmic GB/s each.
-  roofline       the config-4 gather kernel against HBM peak (8 TB/s), timed with HIP events on the stream it
-                 is launched on; roofline_score: the config-2 scoring kernel against the bf16 MFMA peak.
-  cpu_baseline   the reference's PyTorch path on the host CPU (oracle/torch_path.py), config 3 at batch 64,
-                 a bounded sample of decode steps.
+                 cache), tokens / median forward time; the prompt-pass attention kernel alone at that shape.
+  lookup         config 2 PKM lookup (B-4M, 8 x 2048 tokens): scoring, selection and bag kernels;
+                 roofline_score: the scoring against the bf16 MFMA peak.
+  offload        config 3 decode with the B-16M table as q4 in HBM, q4 / bf16 in pinned host RAM (zero-copy,
+                 graphs), and bs1 from a q4 file through mmap (staged, no graphs).
+  train          the training side at the reference's training shape (4,096 tokens x 128 lookups, B-1M fp32).
+  engram         the Engram n-gram hash, row gather and row-sparse backward over 8 x 2048 tokens x 16 lookups.
 All inputs are seeded synthetic data; weights are random N(0, 0.02).
 """
 import argparse
@@ -40,6 +37,7 @@ import json
 import os
 import sys
 import time
+import traceback
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 for _p in (REPO, os.path.join(REPO, "sparse-memory-lm_amd")):
@@ -79,28 +77,49 @@ def build_lm(cfg, dev, seed=0):
     return model
 
 
-def time_decode(model, B, steps, warmup, dev, seed=1, prompt_len=128):
-    """Prefill B uniform prompts of prompt_len tokens, run `warmup` graph steps, then time `steps` decode steps
-    (graph replays of the decoder's multi-step runs)."""
+GEN_TOKENS = 256          # new tokens per generation in configs 1 and 3
+
+
+def time_generations(model, B, reps, warmup, dev, prompt_len=128, new_tokens=GEN_TOKENS, seed=1):
+    """The decode loop of smlm/train.py:283-301 at batch B: prefill B uniform prompts of prompt_len tokens once
+    (untimed), then `warmup` untimed and `reps` timed generations of `new_tokens` greedy tokens each, every one
+    starting from the prompt's first sampled token and bracketed by synchronisations.  A generation is
+    new_tokens / steps_per_graph replays of the captured whole-step graph (each step reads and advances its
+    position and token on the device).  Greedy decoding is deterministic, so every repetition must produce the
+    same tokens; that is checked.  Returns (tok/s, ms per generation, ms per token step)."""
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
     P = prompt_len
     prompt = torch.randint(0, model.cfg.vocab_size, (B, P), generator=g, device=dev)
     with torch.no_grad():
-        dec = model._decoder(B, P + warmup + steps + 1, dev)
+        dec = model._decoder(B, P + new_tokens + 1, dev)
         dec._capture()
         logits = model(prompt, kv_caches=dec.caches, pos0=0)
+        first = logits[:, -1].argmax(-1)
         dec.hist[:, :P] = prompt
-        dec.hist[:, P] = logits[:, -1].argmax(-1)
-        dec.tok.copy_(dec.hist[:, P:P + 1])
-        dec.pos.fill_(P)
-        dec.replay(warmup)
+
+        def start():
+            dec.hist[:, P] = first
+            dec.tok.copy_(first.view(B, 1))
+            dec.pos.fill_(P)
+
+        for _ in range(warmup):
+            start()
+            dec.replay(new_tokens)
         torch.cuda.synchronize(dev)
-        t0 = time.perf_counter()
-        dec.replay(steps)
-        torch.cuda.synchronize(dev)
-        dt = time.perf_counter() - t0
-    return B * steps / dt, 1000.0 * dt / steps
+        ref = dec.hist[:, P:P + new_tokens + 1].clone()
+        total = 0.0
+        for _ in range(reps):
+            start()
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            dec.replay(new_tokens)
+            torch.cuda.synchronize(dev)
+            total += time.perf_counter() - t0
+        if warmup and not torch.equal(ref, dec.hist[:, P:P + new_tokens + 1]):
+            raise RuntimeError("greedy generations differ between repetitions")
+    ms_gen = 1000.0 * total / reps
+    return B * new_tokens * reps / total, ms_gen, ms_gen / new_tokens
 
 
 def chained_launch_us(dev, numel=384, kernels=272, replays=40):
@@ -219,8 +238,10 @@ def prefill_attention_kernel(dev, reps):
             "mfma_frac": flops / ms / 1e9 / BF16_MFMA_PEAK_TFLOPS}
 
 
-def gather_stress(dev, reps):
-    """Config 4: int8 B-16M table (per-row fp16 scales), 65,536 x 128 Zipf(1.1) lookups, fp32 out."""
+def gather_stress(dev, reps, cpu_tokens=0):
+    """Config 4: int8 B-16M table (per-row fp16 scales), 65,536 x 128 Zipf(1.1) lookups, fp32 out; plus the
+    uniform-index control (same shapes, physical traffic = algorithmic).  With cpu_tokens, the host-CPU forms of
+    cpu_gather_c4 over that many of the Zipf tokens."""
     import torch
     from smlm_hip import kernels as K
     rows, D, N, Kl = 4096 * 4096, 384, 65536, 128
@@ -240,10 +261,17 @@ def gather_stress(dev, reps):
     alg_bytes = N * Kl * (D + 2 + 8 + 4) + N * D * 4          # 3,439,329,280
     ms_zipf = event_time_ms(lambda: K.bag_infer(idx, w, codes, scales), reps)
     ms_uni = event_time_ms(lambda: K.bag_infer(uni, w, codes, scales), reps)
+    out = None
     res = {"tokens": N, "lookups_per_token": Kl, "table": "16,777,216 x 384 int8 + fp16 row scales",
            "alg_bytes_per_call": alg_bytes, "ms_zipf": ms_zipf, "ms_uniform": ms_uni,
            "alg_GBps_zipf": alg_bytes / ms_zipf / 1e6, "alg_GBps_uniform": alg_bytes / ms_uni / 1e6}
-    del codes, scales, idx, w, uni
+    if cpu_tokens:
+        out = K.bag_infer(idx, w, codes, scales)
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        res["cpu"] = cpu_gather_c4(codes, scales, idx, w, out, cpu_tokens)
+        log(f"gather config 4 on the host: {res['cpu']} ({time.perf_counter() - t0:.1f} s)")
+    del codes, scales, idx, w, uni, out
     torch.cuda.empty_cache()
     return res
 
@@ -300,7 +328,7 @@ def time_decode_eager(model, B, steps, dev, seed=1, prompt_len=128):
     return B * steps / dt, 1000.0 * dt / steps
 
 
-def offload_tiers(model, steps, warmup, dev, reps, staged_steps=32):
+def offload_tiers(model, dev, reps, staged_steps=32):
     """Config 3 (B-16M) decode with the value table in each tier of smlm_hip.offload: q4 in HBM, q4 and bf16 in
     pinned host RAM read by the kernels over the host link (zero-copy, whole-step graphs), and bs1 from a q4 file
     through mmap (staged: one synchronisation and host fetch per memory-layer call, no graphs); plus the
@@ -322,7 +350,7 @@ def offload_tiers(model, steps, warmup, dev, reps, staged_steps=32):
             if not graphs and B > 1:
                 continue
             if graphs:
-                tok_s, ms = time_decode(model, B, steps, warmup, dev)
+                tok_s, _, ms = time_generations(model, B, 1, 1, dev)
             else:
                 tok_s, ms = time_decode_eager(model, B, staged_steps, dev)
             res[f"{name}_bs{B}"] = {"tok_s": tok_s, "ms_per_step": ms}
@@ -530,49 +558,159 @@ def train_kernels(dev, reps):
     return res
 
 
-def cpu_baseline(model, B, max_steps, budget_s):
-    """The reference's torch path (oracle/torch_path.py) on the host cores: config 3 at batch B, 128-token
-    prompts, then greedy decode steps (fp32 weights, the bf16 table read by row gather), timed until
-    `budget_s` seconds or `max_steps` steps."""
+def cpu_info():
+    """Host CPU description for the CPU baselines: model name (lscpu), core counts and torch's thread count."""
+    import subprocess
+    import torch
+    name = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if name is None and os.path.exists("/proc/cpuinfo"):
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    return {"model_name": name, "cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
+
+
+def cpu_decode(sd, cfg, B, max_steps, budget_s, prompt_len=128):
+    """The reference's torch path (oracle/torch_path.py) on the host cores: B prompts of prompt_len uniform ids,
+    prefill (untimed), then greedy decode steps of the loop of smlm/train.py:283-301, timed until `budget_s`
+    seconds or `max_steps` steps (the config's 256 new tokens at most)."""
     import torch
     import oracle.torch_path as TP
     torch.set_num_threads(len(os.sched_getaffinity(0)))
-    sd = {}
-    for k, v in model.state_dict().items():
-        sd[k] = v.cpu() if k.endswith("values.weight") else v.float().cpu()
-    cfg = model.cfg.to_dict()
     g = torch.Generator().manual_seed(1)
-    prompt = torch.randint(0, cfg["vocab_size"], (B, 128), generator=g)
-    log(f"cpu baseline: weights on the host, prefill of {B} x 128 tokens on {torch.get_num_threads()} threads")
+    prompt = torch.randint(0, cfg["vocab_size"], (B, prompt_len), generator=g)
     with torch.no_grad():
         caches = [dict() for _ in range(cfg["n_layers"])]
         t0 = time.perf_counter()
         nxt = TP.lm_forward(sd, cfg, prompt, caches, 0, last_only=True).argmax(-1)
         t_prefill = time.perf_counter() - t0
-        log(f"cpu baseline: prefill {t_prefill:.1f} s, timing decode steps")
         steps = 0
         t0 = time.perf_counter()
         while steps < max_steps and (steps < 2 or time.perf_counter() - t0 < budget_s):
-            nxt = TP.lm_forward(sd, cfg, nxt, caches, 128 + steps).argmax(-1)
+            nxt = TP.lm_forward(sd, cfg, nxt, caches, prompt_len + steps).argmax(-1)
             steps += 1
         dt = time.perf_counter() - t0
-    del sd
     return {"value": B * steps / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"config 3 decode at batch {B}: 128-token prompt prefill ({t_prefill:.1f} s, untimed), then "
-                      f"{steps} timed greedy steps ({dt:.1f} s) of the reference torch path (fp32 weights, "
-                      f"bf16 table)", "cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0))}
+            "sample": f"batch {B}: {prompt_len}-token prompt prefill ({t_prefill:.1f} s, untimed), then {steps} "
+                      f"of the {GEN_TOKENS} greedy steps timed ({dt:.1f} s), reference torch path restated in "
+                      f"oracle/torch_path.py (fp32 weights, bf16 table read by row gather)"}
+
+
+def host_state(model):
+    """The model's weights on the host for the CPU path: fp32, except the value tables, which stay bf16."""
+    sd = {}
+    for k, v in model.state_dict().items():
+        sd[k] = v.cpu() if k.endswith("values.weight") else v.float().cpu()
+    return sd
+
+
+def cpu_gather_c4(codes, scales, idx, w, out_gpu, tokens, reps=3):
+    """Config 4 on the host cores over the first `tokens` tokens of the same lookups (the reference has no int8
+    gather; its CPU-side forms, as BASELINE.md plans them):
+      chunked   table_i8[idx].float() * (w * scale[idx])[..., None] summed over the 128 lookups, 256 tokens a chunk
+      dequant   the table dequantised once to fp32 (untimed), then F.embedding_bag(mode="sum",
+                per_sample_weights) -- the reference's bag_forward path on a dequantised inference table
+                (smlm/pkm.py:138-148, scripts/quantize_table_eval.py:55-61); only when host RAM allows 26 GB more.
+    Both are checked against the GPU output rows of the same tokens.  Rates are algorithmic bytes (52,480 per
+    token) per second."""
+    import torch
+    import torch.nn.functional as F
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    t0 = time.perf_counter()
+    codes_h, scales_h = codes.cpu(), scales.cpu()
+    idx_h, w_h = idx[:tokens].cpu(), w[:tokens].cpu()
+    ref = out_gpu[:tokens].cpu()
+    copy_s = time.perf_counter() - t0
+    per_tok = idx.shape[1] * (codes.shape[1] + 2 + 8 + 4) + codes.shape[1] * 4
+
+    def chunked():
+        out = torch.empty(tokens, codes.shape[1])
+        for a in range(0, tokens, 256):
+            i = idx_h[a:a + 256]
+            wr = w_h[a:a + 256] * scales_h[i].float()
+            out[a:a + 256] = (codes_h[i].float() * wr[..., None]).sum(1)
+        return out
+
+    def median_s(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            o = fn()
+            ts.append(time.perf_counter() - t)
+        ts.sort()
+        return ts[len(ts) // 2], o
+
+    s1, o1 = median_s(chunked)
+    res = {"tokens": tokens, "host_copy_s": copy_s, "alg_bytes_per_token": per_tok,
+           "chunked": {"ms": 1000 * s1, "alg_GBps": tokens * per_tok / s1 / 1e9,
+                       "tok_s": tokens / s1,
+                       "max_abs_diff_vs_gpu": float((o1 - ref).abs().max())}}
+    try:
+        import psutil
+        avail = psutil.virtual_memory().available
+    except ImportError:
+        avail = 0
+    rows = codes.shape[0]
+    if avail > rows * codes.shape[1] * 4 * 1.5:
+        t0 = time.perf_counter()
+        table = torch.empty(rows, codes.shape[1])
+        for a in range(0, rows, 1 << 20):
+            table[a:a + (1 << 20)] = codes_h[a:a + (1 << 20)].float() * scales_h[a:a + (1 << 20), None].float()
+        deq_s = time.perf_counter() - t0
+        s2, o2 = median_s(lambda: F.embedding_bag(idx_h, table, per_sample_weights=w_h, mode="sum"))
+        res["dequant_embedding_bag"] = {"ms": 1000 * s2, "alg_GBps": tokens * per_tok / s2 / 1e9,
+                                        "tok_s": tokens / s2, "dequantise_s_untimed": deq_s,
+                                        "max_abs_diff_vs_gpu": float((o2 - ref).abs().max())}
+        del table
+    else:
+        res["dequant_embedding_bag"] = f"skipped: {avail / 2**30:.0f} GiB of host RAM available"
+    res.update(cpu_info())
+    del codes_h, scales_h
+    return res
+
+
+def cpu_prefill_c2(model, tokens=2048):
+    """Config 2 on the host cores: the reference torch path's LM forward (oracle/torch_path.py) over ONE of the
+    8 prompts of 2048 tokens (a bounded sample), tok/s."""
+    import torch
+    import oracle.torch_path as TP
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    sd = host_state(model)
+    cfg = model.cfg.to_dict()
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, cfg["vocab_size"], (1, tokens), generator=g)
+    with torch.no_grad():
+        TP.lm_forward(sd, cfg, prompt[:, :64])
+        t0 = time.perf_counter()
+        TP.lm_forward(sd, cfg, prompt, last_only=True)
+        dt = time.perf_counter() - t0
+    del sd
+    return {"value": tokens / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 of the 8 prompts: LM forward over {tokens} tokens ({dt:.1f} s), reference torch path"}
 
 
 def read_traffic():
-    """HBM bytes per launch of the config-4 gather from the committed rocprofv3 PMC summary (FETCH_SIZE +
-    WRITE_SIZE, calibrated on a plain copy kernel), or None if there is none."""
+    """HBM bytes per launch of the config-4 gather (uniform control, Zipf) from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel); None where absent."""
     path = os.path.join(REPO, "profiles", "gather_config4_pmc.txt")
-    if not os.path.exists(path):
-        return None
-    for line in open(path):
-        if line.startswith("traffic_bytes_per_launch_zipf:"):
-            return float(line.split(":", 1)[1])
-    return None
+    out = {"uniform": None, "zipf": None}
+    if os.path.exists(path):
+        for line in open(path):
+            for k in out:
+                if line.startswith(f"traffic_bytes_per_launch_{k}:"):
+                    out[k] = float(line.split(":", 1)[1])
+    return out
 
 
 def calibration_copy(dev, nbytes=1 << 30):
@@ -587,23 +725,32 @@ def calibration_copy(dev, nbytes=1 << 30):
     del a, b
 
 
+HEADLINE_PHASES = "decode,gather,cpu,config1,config0,prefill,lookup"
+OPTIONAL_PHASES = "offload,train,engram"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=5,
+                    help=f"timed generations of {GEN_TOKENS} greedy tokens per decode measurement")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed generations before them")
     ap.add_argument("--reps", type=int, default=20, help="timed launches per kernel measurement")
     ap.add_argument("--prefill-reps", type=int, default=5, help="timed forwards of the config-2 prefill")
-    ap.add_argument("--cpu-steps", type=int, default=256, help="most CPU-baseline decode steps")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline timing budget")
+    ap.add_argument("--cpu-steps", type=int, default=GEN_TOKENS, help="most CPU-baseline decode steps")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode timing budget")
+    ap.add_argument("--cpu-gather-tokens", type=int, default=2048, help="config-4 tokens timed on the host")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phases", default="decode,config0,config1,prefill,lookup,gather,train,offload,engram,cpu",
-                    help="subset of decode,config0,config1,prefill,lookup,gather,train,offload,engram,cpu,calibrate "
-                         "(profiling runs); the JSON line is complete only with the default")
+    ap.add_argument("--phases", default=HEADLINE_PHASES + "," + OPTIONAL_PHASES,
+                    help="subset of " + HEADLINE_PHASES + "," + OPTIONAL_PHASES + ",calibrate (profiling runs); "
+                         "the JSON line is complete only with the default")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (every box here has one GPU); "
               "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
         sys.exit(2)
     phases = set(args.phases.split(","))
     if args.no_cpu:
@@ -613,107 +760,143 @@ def main():
     from smlm_hip import _lib
     dev = torch.device("cuda:0")
     log(f"{_lib.version()} on {torch.cuda.get_device_name(dev)}")
+    R = {}                  # phase -> result
+    errors = {}             # phase -> error text (the line is printed whatever a phase raises)
 
-    if "calibrate" in phases:
-        calibration_copy(dev)
-        log("calibration copy of 1 GiB done")
-    model = None
-    tok_s64 = ms64 = tok_s1 = ms1 = dec_roof = None
-    if "decode" in phases or "cpu" in phases or "offload" in phases:
-        cfg = lm_config(4096, 128 + args.warmup + args.steps + 2)
+    def phase(name, fn, when=True):
+        if name not in phases or not when:
+            return None
         t0 = time.perf_counter()
-        model = build_lm(cfg, dev)
-        log(f"B-16M LM built in {time.perf_counter() - t0:.1f} s")
-    if "decode" in phases:
-        tok_s64, ms64 = time_decode(model, 64, args.steps, args.warmup, dev)
-        log(f"decode bs64: {tok_s64:.0f} tok/s ({ms64:.3f} ms/step)")
-        tok_s1, ms1 = time_decode(model, 1, args.steps, args.warmup, dev)
-        log(f"decode bs1: {tok_s1:.1f} tok/s ({ms1:.3f} ms/step)")
-        launch_us, wide_us = chained_launch_us(dev), chained_launch_us(dev, numel=1 << 18)
-        mean_pos = 128 + args.warmup + (args.steps - 1) / 2.0
-        dec_roof = {"bs64": decode_roofline(model, 64, ms64, mean_pos, launch_us, wide_us),
-                    "bs1": decode_roofline(model, 1, ms1, mean_pos, launch_us, wide_us)}
-        log(f"decode floors: chained launch {launch_us:.2f} us (chip-wide {wide_us:.2f} us); {dec_roof}")
-    c0 = c1 = pf = None
-    if "config0" in phases:
-        c0 = layer_config0(dev, args.reps)
-        log(f"layer config 0 (B-1M, fp32, 8 x 256 tokens): {c0}")
-    if "config1" in phases:
-        t0 = time.perf_counter()
-        m1 = build_lm(lm_config(1024, 512 + args.warmup + args.steps + 2), dev)
-        tok_s, ms = time_decode(m1, 1, args.steps, args.warmup, dev, prompt_len=512)
-        c1 = {"tok_s": tok_s, "ms_per_step": ms, "batch": 1, "prompt_len": 512, "new_tokens": args.steps,
-              "table": "1,048,576 x 384 bf16 (B-1M)"}
-        log(f"decode config 1 (B-1M, 512-token prompt, bs1): {tok_s:.1f} tok/s ({ms:.3f} ms/step), "
-            f"{time.perf_counter() - t0:.1f} s")
-        del m1
+        try:
+            R[name] = fn()
+        except Exception as e:                                  # noqa: BLE001 -- recorded in the line
+            traceback.print_exc()
+            errors[name] = f"{type(e).__name__}: {e}"
+            R[name] = None
         torch.cuda.empty_cache()
-    if "prefill" in phases:
-        m2 = build_lm(lm_config(2048, 2048), dev)
-        tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
-        pf = {"tok_s": tok_s, "ms_per_forward": ms, "batch": 8, "seq_len": 2048,
-              "table": "4,194,304 x 384 bf16 (B-4M)", "attention": prefill_attention_kernel(dev, args.reps)}
-        log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
-        del m2
-        torch.cuda.empty_cache()
-    lk = ga = tr = cpu = None
-    if "lookup" in phases:
-        lk = lookup_prefill(dev, args.reps)
-        log(f"lookup config 2: {lk}")
-    if "gather" in phases:
-        ga = gather_stress(dev, args.reps)
-        log(f"gather config 4: {ga}")
-    off = eng = None
-    if "engram" in phases:
-        eng = engram_lookup(dev, args.reps)
-        log(f"engram lookup: {eng}")
-    if "offload" in phases:
-        off = offload_tiers(model, args.steps, args.warmup, dev, args.reps)
-    if "train" in phases:
-        tr = train_kernels(dev, args.reps)
-        for k, v in tr.items():
-            if isinstance(v, dict):
-                v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
-        log(f"training kernels: {tr}")
-    if "cpu" in phases:
-        t0 = time.perf_counter()
-        cpu = cpu_baseline(model, 64, args.cpu_steps, args.cpu_seconds)
-        log(f"cpu baseline: {cpu} ({time.perf_counter() - t0:.1f} s)")
+        log(f"phase {name}: {time.perf_counter() - t0:.1f} s")
+        return R[name]
 
-    roofline = roofline_score = None
-    if ga is not None:
-        achieved = ga["alg_GBps_zipf"]
-        traffic = read_traffic()
-        roofline = {"kernel": "bag_rows_kernel<int8> (config 4 gather)", "bound": "hbm", "achieved": achieved,
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                    "uniform_control_achieved": ga["alg_GBps_uniform"],
-                    "uniform_control_frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS}
-        if traffic:
-            roofline["physical_GBps_zipf"] = traffic / ga["ms_zipf"] / 1e6
-    if lk is not None:
-        # the launch also writes 537 MB of bf16 scores, which sets its pace: the write rate is reported beside
-        # the MFMA rate
-        roofline_score = {"kernel": "score_ws_kernel<8> (config 2 scoring)", "bound": "mfma",
-                          "achieved": lk["score_TFLOPs"], "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                          "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS,
-                          "score_write_GBps": lk["score_write_GBps"],
-                          "score_write_frac": lk["score_write_GBps"] / HBM_PEAK_GBS}
     line = {
         "metric": "decode tok/s (B-16M, bs1/bs64); PKM lookup tok/s + value-gather HBM GB/s",
-        "value": tok_s64, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms64, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "value": None, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: seeded uniform prompt ids, random N(0,0.02) weights; Zipf(1.1) gather indices",
-        "config": {"workload": "config 3: 21M LM (d384, 6 layers, vocab 32000) + B-16M PKM at layer 3 "
-                               "(16,777,216 x 384 bf16 values), greedy decode at batch 64, 128-token prompts, "
-                               "whole-step hipGraph", "global_batch": 64, "prompt_len": 128,
-                   "new_tokens": args.steps},
-        "decode_bs1_tok_s": tok_s1, "decode_bs1_ms_per_step": ms1, "decode_roofline": dec_roof,
-        "layer_config0": c0, "decode_config1_bs1": c1, "prefill_config2": pf,
-        "pkm_lookup_config2": lk, "gather_config4": ga, "train_kernels": tr,
-        "offload_config3": off, "engram_lookup": eng,
-        "roofline": roofline, "roofline_score": roofline_score, "cpu_baseline": cpu,
+        "config": {"workload": f"config 3: 21M LM (d384, 6 layers, vocab 32000) + B-16M PKM at layer 3 "
+                               f"(16,777,216 x 384 bf16 values), batch 64, 128-token prompts, then {GEN_TOKENS} "
+                               f"greedy tokens; a step is one such generation (whole-step hipGraph replays)",
+                   "global_batch": 64, "prompt_len": 128, "new_tokens": GEN_TOKENS},
     }
-    print(json.dumps(line), flush=True)
+    try:
+        if "calibrate" in phases:
+            calibration_copy(dev)
+            log("calibration copy of 1 GiB done")
+        model = None
+        if phases & {"decode", "cpu", "offload"}:
+            t0 = time.perf_counter()
+            model = build_lm(lm_config(4096, 512), dev)
+            log(f"B-16M LM built in {time.perf_counter() - t0:.1f} s")
+
+        def decode():
+            out = {}
+            for B in (64, 1):
+                tok_s, ms_gen, ms_tok = time_generations(model, B, args.steps, args.warmup, dev)
+                out[f"bs{B}"] = {"tok_s": tok_s, "ms_per_generation": ms_gen, "ms_per_token_step": ms_tok}
+                log(f"decode config 3 bs{B}: {tok_s:.1f} tok/s ({ms_tok:.4f} ms per token step, "
+                    f"{ms_gen:.2f} ms per {GEN_TOKENS}-token generation)")
+            launch_us, wide_us = chained_launch_us(dev), chained_launch_us(dev, numel=1 << 18)
+            mean_pos = 128 + (GEN_TOKENS - 1) / 2.0
+            for B in (64, 1):
+                out[f"bs{B}"]["roofline"] = decode_roofline(model, B, out[f"bs{B}"]["ms_per_token_step"], mean_pos,
+                                                            launch_us, wide_us)
+            return out
+
+        dec = phase("decode", decode)
+        if dec is not None:
+            line["value"] = dec["bs64"]["tok_s"]
+            line["ms_per_step"] = dec["bs64"]["ms_per_generation"]
+            line["ms_per_token_step"] = dec["bs64"]["ms_per_token_step"]
+            line["decode_bs1_tok_s"] = dec["bs1"]["tok_s"]
+            line["decode_bs1_ms_per_token_step"] = dec["bs1"]["ms_per_token_step"]
+            line["decode_roofline"] = {k: v["roofline"] for k, v in dec.items()}
+
+        ga = phase("gather", lambda: gather_stress(dev, args.reps,
+                                                   cpu_tokens=args.cpu_gather_tokens if "cpu" in phases else 0))
+        line["gather_config4"] = ga
+        if ga is not None:
+            traffic = read_traffic()
+            tz = traffic["zipf"]
+            line["roofline"] = {
+                "kernel": "bag_rows_kernel<int8> (config-4 shapes, uniform-index control)", "bound": "hbm",
+                "achieved": ga["alg_GBps_uniform"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS, "traffic": traffic["uniform"],
+                "alg_bytes_per_launch": ga["alg_bytes_per_call"], "ms_per_launch": ga["ms_uniform"],
+                "zipf": {"ms_per_launch": ga["ms_zipf"], "alg_GBps": ga["alg_GBps_zipf"], "traffic": tz,
+                         "physical_GBps": tz / ga["ms_zipf"] / 1e6 if tz else None,
+                         "physical_frac": tz / ga["ms_zipf"] / 1e6 / HBM_PEAK_GBS if tz else None}}
+
+        def cpu():
+            sd = host_state(model)
+            cfg = model.cfg.to_dict()
+            t0 = time.perf_counter()
+            out = {"bs64": cpu_decode(sd, cfg, 64, args.cpu_steps, args.cpu_seconds)}
+            log(f"cpu baseline config 3 bs64: {out['bs64']} ({time.perf_counter() - t0:.1f} s)")
+            out["bs1"] = cpu_decode(sd, cfg, 1, args.cpu_steps, args.cpu_seconds / 2)
+            log(f"cpu baseline config 3 bs1: {out['bs1']}")
+            del sd
+            return out
+
+        cb = phase("cpu", cpu, when=model is not None)
+        if cb is not None:
+            info = cpu_info()
+            line["cpu_baseline"] = dict(cb["bs64"], **info)
+            line["cpu_baseline"]["sample"] = "config 3 decode, " + cb["bs64"]["sample"]
+            line["cpu_baseline_bs1"] = dict(cb["bs1"], **info)
+            if ga is not None and "cpu" in ga:
+                line["cpu_baseline_gather_config4"] = ga["cpu"]
+
+        def config1():
+            m1 = build_lm(lm_config(1024, 1024), dev)
+            tok_s, ms_gen, ms_tok = time_generations(m1, 1, args.steps, args.warmup, dev, prompt_len=512)
+            del m1
+            return {"tok_s": tok_s, "ms_per_generation": ms_gen, "ms_per_token_step": ms_tok, "batch": 1,
+                    "prompt_len": 512, "new_tokens": GEN_TOKENS, "table": "1,048,576 x 384 bf16 (B-1M)"}
+
+        line["decode_config1_bs1"] = phase("config1", config1)
+        line["layer_config0"] = phase("config0", lambda: layer_config0(dev, args.reps))
+
+        def prefill():
+            m2 = build_lm(lm_config(2048, 2048), dev)
+            tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
+            out = {"tok_s": tok_s, "ms_per_forward": ms, "batch": 8, "seq_len": 2048,
+                   "table": "4,194,304 x 384 bf16 (B-4M)", "attention": prefill_attention_kernel(dev, args.reps)}
+            log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
+            if "cpu" in phases:
+                out["cpu_baseline"] = cpu_prefill_c2(m2)
+                log(f"cpu baseline config 2: {out['cpu_baseline']}")
+            del m2
+            return out
+
+        line["prefill_config2"] = phase("prefill", prefill)
+        line["pkm_lookup_config2"] = phase("lookup", lambda: lookup_prefill(dev, args.reps))
+        if R.get("lookup"):
+            lk = R["lookup"]
+            line["roofline_score"] = {
+                "kernel": "config-2 sub-key scoring", "bound": "mfma", "achieved": lk["score_TFLOPs"],
+                "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS}
+        line["offload_config3"] = phase("offload", lambda: offload_tiers(model, dev, args.reps),
+                                        when=model is not None)
+        tr = phase("train", lambda: train_kernels(dev, args.reps))
+        if tr is not None:
+            for v in tr.values():
+                if isinstance(v, dict):
+                    v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
+        line["train_kernels"] = tr
+        line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps))
+    finally:
+        if errors:
+            line["phase_errors"] = errors
+        print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

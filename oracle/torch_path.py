@@ -95,9 +95,10 @@ def pkm_forward(sd, p, x, mcfg, table=None, selection=None):
     return out
 
 
-def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False, selections=None):
+def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False, selections=None, positions=None):
     """Logits (B, T, vocab) of the decoder with the memory layers cfg["mem_layers"] (only the last position's,
-    (B, 1, vocab), with last_only).  selections: {layer: (indices, weights)} given to pkm_forward."""
+    (B, 1, vocab), with last_only; only those at the chunk offsets `positions`, (B, len, vocab), with a
+    positions index tensor).  selections: {layer: (indices, weights)} given to pkm_forward."""
     x = sd["tok_emb.weight"][idx]
     mcfg = dict(heads=cfg["mem_heads"], knn=cfg["mem_knn"], k_dim=cfg["mem_k_dim"], n_keys=cfg["mem_n_keys"],
                 query_norm=cfg["mem_query_norm"], swilu=cfg["mem_swilu"])
@@ -117,6 +118,8 @@ def lm_forward(sd, cfg, idx, caches=None, pos0=0, tables=None, last_only=False, 
             x = x + (F.silu(a) * b) @ sd[p + "ffn.w2.weight"].T
     if last_only:
         x = x[:, -1:]
+    elif positions is not None:
+        x = x[:, positions]
     return rms_norm(x, sd["norm.weight"], eps) @ sd["tok_emb.weight"].T
 
 
