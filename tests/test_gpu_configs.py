@@ -1,0 +1,267 @@
+"""Parity at the BASELINE configurations themselves (the shapes bench.py measures), not scaled-down models.
+
+  c1  the 21M LM (d 384, 6 layers, 6 heads, vocab 32000) with the B-1M memory at layer 3, 512-token prompt, bs 1
+  c3  the same LM with the B-16M memory (4096^2 x 384 bf16, 12.9 GB), 128-token prompts, bs 1 and 64
+  c2  the B-4M sub-key scoring kernel at its bench shape (16,384 tokens x 4 heads x 2048 sub-keys of 256), and
+      one 8 x 2048 prefill forward of the LM with the B-4M memory
+  c4  the full 16,777,216 x 384 int8 table (byte offsets past 2^32) read by the gather
+
+Decode (c1, c3): the prompt pass runs with the memory layer recording its selection, then several fused decode
+steps record theirs (sub-key scores, selected scores, rows, weights).  Each step's selection must be bit-exact
+against the oracle on the step's own scores (oracle/pkm_oracle.py, smlm/kernels.py:128-177), and its logits within
+1e-2 of their scale of the reference torch path (oracle/torch_path.py: smlm/model.py:63-118, 156-163, 266-293 in
+fp32 on the CPU) run on the same tokens with the same selections -- the KV-cache decode equality of
+tests/test_pkm.py:91-119, with the einsum scores taken from the kernel (their bits are not reproducible across
+backends).  The whole-step graph then replays the same steps from the same state and must produce the same tokens.
+Only the table rows the selections use are pulled to the host (as tests/test_kernels.py:323-360 does for its
+large table).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.pkm_oracle as O
+import oracle.torch_path as TP
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MEM_LAYER = 3
+
+
+def note(msg):
+    print(msg, flush=True)
+
+
+def bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def build_lm(n_keys, max_seq_len, seed=0):
+    """The LM of configs 1-3 with every matrix, the sub-keys and the value table drawn from N(0, 0.02), in bf16
+    (bench.py builds the same model)."""
+    from smlm_hip.model import ModelConfig, Transformer
+    cfg = ModelConfig(vocab_size=32000, d_model=384, n_layers=6, n_heads=6, ffn_hidden=1024,
+                      max_seq_len=max_seq_len, mem_layers=[MEM_LAYER], mem_n_keys=n_keys, mem_heads=4, mem_knn=32,
+                      mem_k_dim=512)
+    torch.manual_seed(seed)
+    with torch.device(DEV):
+        model = Transformer(cfg)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if p.dim() >= 2 or name.endswith("keys"):
+                p.normal_(0.0, 0.02)
+    model = model.to(torch.bfloat16).eval()
+    torch.cuda.empty_cache()
+    model.set_memory_inference_table("bf16")
+    return model
+
+
+def compact_rows(table, idx_list):
+    """Rows of `table` (device) used by the index tensors of idx_list, as an fp32 host table, and the indices
+    remapped into it."""
+    allidx = torch.cat([i.reshape(-1) for i in idx_list])
+    used, inv = torch.unique(allidx, return_inverse=True)
+    sub = table.index_select(0, used).float().cpu()
+    out, a = [], 0
+    for i in idx_list:
+        out.append(inv[a:a + i.numel()].view(i.shape).cpu())
+        a += i.numel()
+    return sub, out
+
+
+def host_weights(model):
+    return {k: v.float().cpu() for k, v in model.state_dict().items() if not k.endswith("values.weight")}
+
+
+def check_selection(s1, s2, sc, idx, w, knn):
+    rs, ri, rw = O.pk_select(bits(s1), bits(s2), knn)
+    assert np.array_equal(idx.cpu().numpy(), ri), "selected rows differ from the oracle"
+    assert np.array_equal(bits(sc), rs), "selected scores differ from the oracle"
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)
+
+
+@torch.no_grad()
+def decode_parity(model, B, P, steps, seed):
+    from smlm_hip.model import _StepDecoder
+    cfg = model.cfg
+    mem = model.layers[MEM_LAYER].ffn
+    dec = model._decoder(B, P + steps + 1, DEV)
+    assert dec.fused is not None, "the fused decode step must cover the config"
+    dec._capture()                               # before the prompt pass: its warm-up steps write cache slots 0, 1
+    prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(seed)).to(DEV)
+    mem.record = True
+    logits = model(prompt, kv_caches=dec.caches, pos0=0)
+    mem.record = False
+    sel_prompt = (mem.last_indices.clone(), mem.last_weights.clone())
+    first = logits[:, -1].argmax(-1)
+    dec.hist[:, :P] = prompt
+    dec.hist[:, P] = first
+    dec.tok.copy_(first.view(B, 1))
+    dec.pos.fill_(P)
+    got_logits, toks, sels = [], [], []
+    for t in range(steps):
+        rec = {}
+        toks.append(dec.tok.clone().cpu())
+        lg = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec)
+        s1, s2, sc, idx, w = rec[MEM_LAYER]
+        check_selection(s1, s2, sc, idx, w, cfg.mem_knn)
+        got_logits.append(lg.float().cpu())
+        sels.append((idx.clone(), w.clone()))
+        dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist)
+        assert int(dec.pos) == P + t + 1
+    eager = dec.hist[:, P:P + steps + 1].clone()
+    note(f"  B={B} P={P}: {steps} fused steps, selections bit-exact; checking logits on the host")
+
+    # the reference torch path on the same tokens with the same selections
+    sub, remapped = compact_rows(mem.values.weight, [sel_prompt[0]] + [s[0] for s in sels])
+    sd = host_weights(model)
+    cd = cfg.to_dict()
+    caches = [dict() for _ in range(cfg.n_layers)]
+    TP.lm_forward(sd, cd, prompt.cpu(), caches, 0, tables={MEM_LAYER: sub}, last_only=True,
+                  selections={MEM_LAYER: (remapped[0], sel_prompt[1].cpu())})
+    worst = 0.0
+    for t in range(steps):
+        ref = TP.lm_forward(sd, cd, toks[t], caches, P + t, tables={MEM_LAYER: sub},
+                            selections={MEM_LAYER: (remapped[t + 1], sels[t][1].cpu())})[:, -1]
+        err = float((got_logits[t] - ref).abs().max() / ref.abs().max())
+        assert err < 1e-2, f"step {t}: logits off by {err:.3e} of their scale"
+        worst = max(worst, err)
+    note(f"  logits within {worst:.2e} of their scale ({sub.shape[0]} distinct rows pulled)")
+
+    # the whole-step graph from the same state gives the same tokens (runs of 8 steps, then single steps)
+    dec.hist[:, P + 1:] = -1
+    dec.tok.copy_(first.view(B, 1))
+    dec.pos.fill_(P)
+    dec.replay(steps)
+    torch.cuda.synchronize()
+    assert _StepDecoder.steps_per_graph == 8
+    assert torch.equal(dec.hist[:, P:P + steps + 1], eager), "graph replays differ from the eager steps"
+
+
+@pytest.mark.parametrize("B", [1, 64])
+def test_config3_decode_b16m(B):
+    """Config 3: B-16M (16,777,216 x 384 bf16), 128-token prompts, 9 decode steps (a graph run of 8 + 1)."""
+    note(f"config 3 decode B={B}: building the LM with the B-16M table")
+    model = build_lm(4096, 160)
+    decode_parity(model, B, 128, 9, seed=B)
+    del model
+    torch.cuda.empty_cache()
+
+
+def test_config1_decode_b1m():
+    """Config 1: B-1M (1,048,576 x 384 bf16), a 512-token prompt, batch 1, 9 decode steps."""
+    note("config 1 decode: building the LM with the B-1M table")
+    model = build_lm(1024, 544)
+    decode_parity(model, 1, 512, 9, seed=11)
+    del model
+    torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------------------------- config 2
+@torch.no_grad()
+def test_config2_scoring_and_selection_at_bench_shape():
+    """pk_scores at (16,384 tokens, 4 heads, 2048 sub-keys, half 256) -- the launch bench.py times for config 2
+    -- within one bf16 ulp of fp64 on 96 sampled tokens (every head, both halves, all 2048 sub-keys), and the
+    selection of the full launch bit-exact against the oracle on those tokens' rows."""
+    from smlm_hip import kernels as K
+    N, H, NK, half = 16384, 4, 2048, 256
+    note(f"config 2 scoring N={N} H={H} NK={NK} half={half}")
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(N, H, 2 * half, generator=g).to(torch.bfloat16)
+    keys = (torch.randn(H, 2, NK, half, generator=g) / 16).to(torch.bfloat16)
+    s1, s2 = K.pk_scores(q.to(DEV), keys.to(DEV))
+    sc, idx, w = K.pk_select(s1, s2, 32)
+    rows = torch.cat([torch.arange(0, 32), torch.arange(N // 2 - 16, N // 2 + 16), torch.arange(N - 32, N)])
+    rows = torch.cat([rows, torch.randint(0, N, (32,), generator=g)])
+    qs = q[rows].float().numpy()
+    kf = keys.float().numpy()
+    r1, r2 = O.subkey_scores(qs, kf)
+    mag1 = np.einsum("nhd,hkd->nhk", np.abs(qs[..., :half]).astype(np.float64), np.abs(kf[:, 0]).astype(np.float64))
+    mag2 = np.einsum("nhd,hkd->nhk", np.abs(qs[..., half:]).astype(np.float64), np.abs(kf[:, 1]).astype(np.float64))
+    rd = rows.to(DEV)
+    for got, ref, mag in ((s1, r1, mag1), (s2, r2, mag2)):
+        gv = got.index_select(0, rd).float().cpu().numpy().astype(np.float64)
+        assert np.all(np.abs(gv - ref) <= 2 ** -7 * np.abs(ref) + 1e-5 * mag)
+    check_selection(s1.index_select(0, rd), s2.index_select(0, rd), sc.index_select(0, rd),
+                    idx.index_select(0, rd), w.index_select(0, rd), 32)
+
+
+@torch.no_grad()
+def test_config2_prefill_forward_b4m():
+    """Config 2: one forward of the LM with the B-4M memory over 8 x 2048 uniform prompt tokens (no cache).  The
+    memory layer's selection for every token is recorded; the reference torch path given that selection must
+    give the same logits within 1e-2 of their scale at 64 positions of every sequence."""
+    cfg_keys, B, T = 2048, 8, 2048
+    note("config 2 prefill: building the LM with the B-4M table")
+    model = build_lm(cfg_keys, T)
+    mem = model.layers[MEM_LAYER].ffn
+    prompt = torch.randint(0, 32000, (B, T), generator=torch.Generator().manual_seed(31)).to(DEV)
+    mem.record = True
+    logits = model(prompt)
+    mem.record = False
+    idx, w = mem.last_indices.clone(), mem.last_weights.clone()
+    assert idx.shape == (B * T, 4, 32)
+    pos = torch.cat([torch.arange(0, 16), torch.arange(T - 48, T)])
+    got = logits[:, pos.to(DEV)].float().cpu()
+    del logits
+    sub, (ridx,) = compact_rows(mem.values.weight, [idx])
+    note(f"  host check over {sub.shape[0]} distinct rows")
+    sd = host_weights(model)
+    ref = TP.lm_forward(sd, model.cfg.to_dict(), prompt.cpu(), tables={MEM_LAYER: sub},
+                        selections={MEM_LAYER: (ridx, w.cpu())}, positions=pos)
+    err = float((got - ref).abs().max() / ref.abs().max())
+    note(f"  prefill logits within {err:.2e} of their scale")
+    assert err < 1e-2, f"prefill logits off by {err:.3e} of their scale"
+    del model
+    torch.cuda.empty_cache()
+
+
+# --------------------------------------------------------------------------------------------- config 4
+@torch.no_grad()
+def test_config4_full_int8_table_gather():
+    """Config 4's table at full size: 16,777,216 x 384 int8 codes (6.44 GB) + fp16 row scales, quantised on the
+    GPU from N(0, 0.02).  2,048 tokens x 128 lookups: Zipf(1.1) ranks through a seeded row permutation, plus
+    forced rows above 11,184,810 (row x 384 past 2^32 bytes) and the last row.  The fp32 output must match the
+    oracle's fp64 bag of the same rows within 1e-5 of the output scale, and the quantisation of the pulled rows
+    must be bit-exact against the oracle on their bf16-free fp32 sources (regenerated from the same seed)."""
+    from smlm_hip import kernels as K
+    rows, D, N, Kl = 4096 * 4096, 384, 2048, 128
+    note("config 4: quantising the full 16.8M-row int8 table")
+    g = torch.Generator(device=DEV).manual_seed(0)
+    codes = torch.empty(rows, D, dtype=torch.int8, device=DEV)
+    scales = torch.empty(rows, dtype=torch.float16, device=DEV)
+    chunk = 1 << 21
+    for a in range(0, rows, chunk):
+        src = torch.empty(chunk, D, device=DEV).normal_(0.0, 0.02, generator=g)
+        c, s = K.quantize_int8(src)
+        codes[a:a + chunk] = c
+        scales[a:a + chunk] = s
+        if a == rows - chunk:                          # the last chunk: keep its fp32 source for the check below
+            last_src = src[-4096:].cpu().numpy()
+        del src, c, s
+    rng = np.random.default_rng(41)
+    p = 1.0 / np.arange(1, rows + 1, dtype=np.float64) ** 1.1
+    cdf = np.cumsum(p)
+    cdf /= cdf[-1]
+    ranks = np.minimum(np.searchsorted(cdf, rng.random((N, Kl))), rows - 1)
+    idx = rng.permutation(rows)[ranks]
+    idx[:, 0] = rows - 1
+    idx[:, 1] = rng.integers(11_184_811, rows, N)
+    idx[:, 2] = rng.integers(rows - 4096, rows, N)
+    assert (idx.astype(np.int64) * D >= 2 ** 32).mean() > 0.3
+    w = np.concatenate([O.softmax_f32(rng.standard_normal((N, 32)).astype(np.float32)) for _ in range(4)], 1)
+    ti = torch.from_numpy(idx).to(DEV)
+    out = K.bag_infer(ti, torch.from_numpy(w).to(DEV), codes, scales).cpu().numpy()
+    used = np.unique(idx)
+    ud = torch.from_numpy(used).to(DEV)
+    sub_codes = codes.index_select(0, ud).cpu().numpy()
+    sub_scales = scales.index_select(0, ud).cpu().numpy()
+    ref = O.bag(np.searchsorted(used, idx), w, sub_codes, "i8", sub_scales)
+    err = np.abs(out - ref).max() / np.abs(ref).max()
+    note(f"  {used.size} distinct rows, max row {used.max()}, error {err:.2e} of the output scale")
+    assert err <= 1e-5, f"int8 gather off by {err:.3e} of the output scale"
+    rc, rs = O.quantize_rows(last_src, "i8")
+    assert np.array_equal(codes[-4096:].cpu().numpy(), rc)
+    assert np.array_equal(scales[-4096:].cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    del codes, scales
+    torch.cuda.empty_cache()
