@@ -95,6 +95,26 @@ int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, int64_t N, in
                         const uint16_t *pre, void *out, int out_dtype, void *scores, int64_t *idx, float *w,
                         void *stream);
 
+/* Bytes of the static device array that smlm_pkm_lookup_noalloc keeps its sub-key scores in (one per GPU). */
+#define SMLM_LOOKUP_SCRATCH_BYTES (8u << 20)
+
+/*
+ * No counterpart in the reference.  For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the decode lookup smlm_pkm_score followed by
+ * smlm_pkm_select_bag on the same arguments, with identical results, but with the sub-key score rows s1, s2
+ * that those two calls exchange kept in a static device array of SMLM_LOOKUP_SCRATCH_BYTES instead of
+ * caller-provided buffers.  The caller passes the inputs (q, keys as smlm_pkm_score; table, scales, pre as
+ * smlm_pkm_select_bag) and the output out (N, D) of out_dtype.  Nothing is allocated or freed.
+ *   Limit: 2 * N * H * NK * sizeof(dtype) (+ 256 bytes of alignment) <= SMLM_LOOKUP_SCRATCH_BYTES, e.g. N <= 128
+ *   for bf16 scores at H = 4, NK = 4096; larger requests fail with SMLM_EUNSUPPORTED before any launch.
+ *   The stream must belong to the current device.  The first call on a device looks up the array's address on
+ *   that device (hipGetSymbolAddress): make it outside stream capture.  All calls on one GPU share its array:
+ *   calls that overlap on one GPU (different streams, or host threads) race on it.
+ */
+int smlm_pkm_lookup_noalloc(const void *q, int64_t q_row_stride, const void *keys, int dtype, int64_t N, int H,
+                            int NK, int half, int knn, const void *table, int table_dtype, int64_t rows, int D,
+                            const uint16_t *scales, const uint16_t *pre, void *out, int out_dtype, void *stream);
+
 /*
  * Weighted value bag.  Replaces bag_forward (smlm/kernels.py:229-237) and bag_infer (smlm/kernels.py:364-378):
  *   out[n, :] = sum_{j<K} w[n, j] * row(idx[n, j])        (fp32 accumulation)

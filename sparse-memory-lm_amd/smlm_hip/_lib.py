@@ -42,6 +42,8 @@ EXPORTS = {
     "smlm_pkm_select": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _p, _p, _p]),
     "smlm_pkm_bag": (_i, [_p, _i, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p]),
     "smlm_pkm_select_bag": (_i, [_p, _p, _i, _i64, _i, _i, _i, _p, _i, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p]),
+    "smlm_pkm_lookup_noalloc": (_i, [_p, _i64, _p, _i, _i64, _i, _i, _i, _i, _p, _i, _i64, _i, _p, _p, _p, _i,
+                                     _p]),
     "smlm_pkm_quantize": (_i, [_p, _i, _i64, _i, _i, _p, _p, _p]),
     "smlm_decode_attention": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _p]),
     "smlm_decode_attention_proj": (_i, [_p, _i64, _p, _p, _i, _i, _p, _p, _p, _i64, _i, _i, _i, _p, _i64, _i, _p,
