@@ -245,6 +245,21 @@ def test_bag_matches_embedding_bag(kind):
     np.testing.assert_allclose(out / scale, ref / scale, rtol=1e-5, atol=1e-5)
 
 
+def test_silu_bf16_bit_exact_against_torch_everywhere():
+    """bf16(silu(p)) of smlm/kernels.py:304-307 on every finite bf16 pattern equals torch's F.silu on bf16 (fp32
+    arithmetic, one rounding to bf16), and the values are bf16 numbers (an oracle that skipped the rounding, or
+    rounded by truncation, fails)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite(O.bf16_to_f32(bits))
+    with np.errstate(over="ignore", invalid="ignore"):
+        vals = O.silu_bf16(bits)
+    t = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+    ref = F.silu(t).view(torch.int16).numpy().view(np.uint16)
+    got = O.bf16_bits_rtne(vals)
+    assert np.array_equal(got[finite], ref[finite])
+    assert np.array_equal(O.bf16_to_f32(got[finite]).view(np.uint32), vals[finite].view(np.uint32))
+
+
 def test_bag_swilu_epilogue_matches_torch():
     rng = np.random.default_rng(8)
     rows, D, N, K = 300, 32, 20, 16

@@ -68,3 +68,46 @@ def test_greedy_decode_shapes():
     sd, cfg = tiny_sd(seed=4)
     out = TP.greedy_decode(sd, cfg, torch.randint(0, 128, (3, 5)), 7)
     assert out.shape == (3, 8) and out.dtype == torch.int64
+
+
+def _complex_rope(x, pos0, theta):
+    """RoPE written as complex rotation: dimension j < hd/2 and its partner j + hd/2 form z_j = x_j + i x_{j+hd/2},
+    turned by the angle (pos0 + t) * theta^(-2j/hd) -- a formulation independent of the cos/sin cat form."""
+    hd, T = x.shape[-1], x.shape[-2]
+    j = torch.arange(hd // 2, dtype=torch.float64)
+    ang = (pos0 + torch.arange(T, dtype=torch.float64))[:, None] * theta ** (-2.0 * j / hd)
+    z = torch.complex(x[..., :hd // 2], x[..., hd // 2:]) * torch.polar(torch.ones_like(ang), ang)
+    return torch.cat([z.real, z.imag], -1)
+
+
+def test_rope_pairs_halves_and_turns_counterclockwise():
+    """Known answers of smlm/model.py:63-78: the unit vector e_j (j < hd/2) at position p becomes
+    cos(p w_j) e_j + sin(p w_j) e_{j+hd/2}, and e_{j+hd/2} becomes -sin(p w_j) e_j + cos(p w_j) e_{j+hd/2},
+    w_j = theta^(-2j/hd).  An interleaved pairing (2j, 2j+1) or the opposite turn fails these."""
+    import importlib.util
+    import math
+    import os
+    from smlm_hip.model import RotaryEmbedding
+    hd, theta, p = 8, 10000.0, 5
+    eye = torch.eye(hd, dtype=torch.float64).view(1, 1, hd, hd).transpose(2, 3)     # row t of T=hd is e_t
+    spec = importlib.util.spec_from_file_location(
+        "gpu_attention_refs", os.path.join(os.path.dirname(__file__), "test_gpu_attention.py"))
+    attn_tests = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(attn_tests)
+    rope_mod = RotaryEmbedding(hd, 64, theta)
+    for fn in (lambda x: TP.rope(x, p, theta),
+               lambda x: attn_tests.rope_ref(x, rope_mod.cos, rope_mod.sin, p),
+               lambda x: rope_mod(x.float(), p).double()):
+        # every row of the batch at the same position p: feed the unit vectors as a batch of one-token sequences
+        out = fn(eye.reshape(hd, 1, 1, hd)).reshape(hd, hd)
+        for j in range(hd // 2):
+            w = theta ** (-2.0 * j / hd)
+            c, s = math.cos(p * w), math.sin(p * w)
+            exp_lo = torch.zeros(hd, dtype=torch.float64)
+            exp_lo[j], exp_lo[j + hd // 2] = c, s
+            exp_hi = torch.zeros(hd, dtype=torch.float64)
+            exp_hi[j], exp_hi[j + hd // 2] = -s, c
+            assert torch.allclose(out[j], exp_lo, atol=1e-6), (j, out[j])
+            assert torch.allclose(out[j + hd // 2], exp_hi, atol=1e-6), (j, out[j + hd // 2])
+    x = torch.randn(2, 3, 7, 16, dtype=torch.float64, generator=torch.Generator().manual_seed(3))
+    assert torch.allclose(TP.rope(x, 11, theta), _complex_rope(x, 11, theta), atol=1e-6)
