@@ -4,11 +4,15 @@
 //   1. RoPE (model.py:63-78: rotate the two halves of the head) on the new token's q and k, in fp32, rounded to
 //      bf16 as the bf16 model holds them; k and v are written into the cache at the device-side position `pos`;
 //   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos (the new token's own k from LDS), each cache row read
-//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles; the loads of 8 passes of rows are
-//      in flight together (a decode step is latency-bound);
-//   3. softmax over t in fp32;
-//   4. y = sum_t p_t v_t, rows split over the workgroup's lanes, partial sums added through LDS; y is written as
-//      bf16 into the (B, H*head_dim) layout the output projection reads.
+//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles; the keys and values of a group of
+//      passes of rows are in flight together (a decode step is latency-bound);
+//   3. softmax in fp32, by each wavefront over its own rows and in registers: its maximum m_w, the exponentials
+//      p_t = exp(s_t - m_w) and their sum l_w (online over the groups of passes: a group that raises the maximum
+//      rescales what came before);
+//   4. the wavefront's y_w = sum_t p_t v_t in registers; then one merge through LDS: m = max m_w,
+//      y = sum_w y_w exp(m_w - m) / sum_w l_w exp(m_w - m), written as bf16 into the (B, H*head_dim) layout the
+//      output projection reads.
+//   (A workgroup-wide softmax would need the scores in LDS and two more barriers and reductions.)
 // The PROJ variant folds the output projection (model.py:107, wo) in: y, rounded to bf16 as above, is multiplied by
 // the head's column slice of wo, and the n_out fp32 dot products go to parts[b, h, :]; the sum over heads (in head
 // order) is left to the consumer (the RMSNORM_PARTS prologue of smlm_decode_linear), one launch fewer per layer.
@@ -44,6 +48,32 @@ __device__ __forceinline__ float xor_add(float v) {
     return __builtin_bit_cast(float, (uint32_t)pr[0]) + __builtin_bit_cast(float, (uint32_t)pr[1]);
   } else {
     return v + __shfl_xor(v, MASK, kWave);
+  }
+}
+
+// max(v, v[lane ^ MASK]) on every lane, with the same lane exchanges as xor_add
+template <int MASK>
+__device__ __forceinline__ float xor_max(float v) {
+  if constexpr (MASK == 8) {
+    return fmaxf(v, dpp<0x128>(v));  // row_ror:8
+  } else if constexpr (MASK == 16 || MASK == 32) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const auto pr = MASK == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)pr[0]), __builtin_bit_cast(float, (uint32_t)pr[1]));
+  } else {
+    return fmaxf(v, __shfl_xor(v, MASK, kWave));
+  }
+}
+
+// Maximum over the lanes lane % STRIDE == this lane's (strides 2..32 in doubling steps up to 64).
+template <int STRIDE>
+__device__ __forceinline__ float strided_max(float v) {
+  if constexpr (STRIDE < kWave) {
+    v = xor_max<STRIDE>(v);
+    return strided_max<STRIDE * 2>(v);
+  } else {
+    return v;
   }
 }
 
@@ -108,9 +138,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   float *s_q = smem;                     // [HD]
   float *s_k = s_q + HD;                 // [HD] new token's k (bf16 values)
   float *s_v = s_k + HD;                 // [HD]
-  float *s_red = s_v + HD;               // [kAttnWaves][HD] partial sums of p * v
-  float *s_w = s_red + kAttnWaves * HD;  // [kAttnWaves] wavefront partials
-  float *s_p = s_w + 2 * kAttnWaves;     // [max_len] scores, then probabilities
+  float *s_red = s_v + HD;               // [kAttnWaves][HD] the wavefronts' sums of p * v
+  float *s_w = s_red + kAttnWaves * HD;  // [2][kAttnWaves] the wavefronts' maxima, then their sums of p
 
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
@@ -145,7 +174,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   // before anything else, so its round trip overlaps the one of the qkv row below.  Row P itself (written in 1.)
   // is never loaded: rows are clamped to P - 1 and row P is taken from LDS.
   // (the projection's wo registers leave room for 6 passes under the 128 VGPRs of a 1024-thread workgroup)
-  constexpr int U = PROJ && kAttnThreads >= 1024 ? 6 : kAttnUnroll;
+  // (the online softmax rescales per group, so the plain and PROJ variants group alike to reach the same y)
+  constexpr int U = kAttnThreads >= 1024 ? 6 : kAttnUnroll;
   const int sub = lane % LPR, rw = lane / LPR;
   const int slot = wave * RPW + rw;
   const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
@@ -179,12 +209,15 @@ __global__ void __launch_bounds__(kAttnThreads)
   }
   __syncthreads();
 
-  // 2. scores.  Every cache load of a group of U passes is issued before the first is used (the step is latency-
-  // bound: one round trip per group, not per pass); the first group's keys and values came in step 0.
+  // 2-4. Per wavefront, in registers: scores of its rows, their maximum, exponentials and the sum of p * v.  The
+  // first group's keys and values came in step 0; later groups load both before the first is used.
   const float scale = rsqrtf((float)HD);
   float qf[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) qf[e] = s_q[sub * 8 + e];
+  float m_run = -INFINITY, l_run = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
   for (int t0 = 0; t0 <= P; t0 += RPB * U) {
     if (t0 > 0) {
 #pragma unroll
@@ -192,10 +225,14 @@ __global__ void __launch_bounds__(kAttnThreads)
         if (t0 + u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
         const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
         kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
+        vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
       }
     }
+    float d[U];
+    float gm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      d[u] = -INFINITY;
       if (t0 + u * RPB > P) continue;
       const int t = t0 + u * RPB + slot;
       float kf[8];
@@ -205,84 +242,69 @@ __global__ void __launch_bounds__(kAttnThreads)
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] = t == P ? s_k[sub * 8 + e] : 0.f;
       }
-      float d = 0.f;
+      float dd = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qf[e], kf[e], d);
-      d = group_sum<LPR>(d);
-      if (sub == 0 && t <= P) s_p[t] = d * scale;
+      for (int e = 0; e < 8; ++e) dd = fmaf(qf[e], kf[e], dd);
+      dd = group_sum<LPR>(dd);
+      if (t <= P) d[u] = dd * scale;
+      gm = fmaxf(gm, d[u]);
     }
-  }
-  __syncthreads();
-
-  // 3. softmax over t = 0..P
-  float mx = -INFINITY;
-  for (int t = tid; t <= P; t += kAttnThreads) mx = fmaxf(mx, s_p[t]);
-  for (int m = kWave / 2; m > 0; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, kWave));
-  if (lane == 0) s_w[wave] = mx;
-  __syncthreads();
-  mx = s_w[0];
+    gm = strided_max<LPR>(gm);               // over the wavefront's row groups
+    const float m_new = fmaxf(m_run, gm);
+    if (m_new == -INFINITY) continue;        // wavefront-uniform: none of its rows so far
+    const float corr = expf(m_run - m_new);  // 0 for the first group with rows
+    l_run *= corr;
 #pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) mx = fmaxf(mx, s_w[w]);
-  float sum = 0.f;
-  for (int t = tid; t <= P; t += kAttnThreads) {
-    const float e = expf(s_p[t] - mx);
-    s_p[t] = e;
-    sum += e;
-  }
-  sum = wave_sum(sum);
-  if (lane == 0) s_w[kAttnWaves + wave] = sum;
-  __syncthreads();
-  sum = 0.f;
-#pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) sum += s_w[kAttnWaves + w];
-
-  // 4. y = sum_t p_t v_t / sum (each lane's rows in increasing t, as one pass at a time would add them)
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int t0 = 0; t0 <= P; t0 += RPB * U) {
-    uint4 vv[U];
-    if (t0 == 0) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) vv[u] = vpre[u];
-    } else {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (t0 + u * RPB > P) continue;
-        const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
-        vv[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
-      }
-    }
+    for (int e = 0; e < 8; ++e) acc[e] *= corr;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if (t0 + u * RPB > P) continue;
       const int t = t0 + u * RPB + slot;
       if (t > P) continue;
-      const float pt = s_p[t];
+      const float pt = expf(d[u] - m_new);
       float vf[8];
       if (t < P) {
-        unpack8(vv[u], vf);
+        unpack8(vpre[u], vf);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) vf[e] = s_v[sub * 8 + e];
       }
+      l_run += pt;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
     }
+    m_run = m_new;
   }
-  // the wavefront's rows summed across its lanes (lane % LPR keeps the dims), then the wavefronts through LDS
+  // the wavefront's row groups summed (lane % LPR keeps the dims; the LPR lanes of a row group hold the same p)
+  l_run = strided_sum<LPR>(l_run);
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = strided_sum<LPR>(acc[e]);
   if (rw == 0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) s_red[wave * HD + sub * 8 + e] = acc[e];
   }
+  if (lane == 0) {
+    s_w[wave] = m_run;
+    s_w[kAttnWaves + wave] = l_run;
+  }
   __syncthreads();
+  // merge: the wavefronts' statistics relative to the largest maximum (row P always counts, so it is finite)
+  float mx = s_w[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) mx = fmaxf(mx, s_w[w]);
+  float fw[kAttnWaves];
+  float sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) {
+    fw[w] = expf(s_w[w] - mx);               // 0 for a wavefront without rows (maximum -inf)
+    sum += s_w[kAttnWaves + w] * fw[w];
+  }
   const float inv = 1.0f / sum;
   if constexpr (!PROJ) {
     for (int i = tid; i < HD; i += kAttnThreads) {
       float y = 0.f;
 #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
+      for (int w = 0; w < kAttnWaves; ++w) y = fmaf(s_red[w * HD + i], fw[w], y);
       o[i] = (uint16_t)bf16_bits_rtne(y * inv);
     }
   } else {
@@ -292,7 +314,7 @@ __global__ void __launch_bounds__(kAttnThreads)
     for (int i = tid; i < HD; i += kAttnThreads) {
       float y = 0.f;
 #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) y += s_red[w * HD + i];
+      for (int w = 0; w < kAttnWaves; ++w) y = fmaf(s_red[w * HD + i], fw[w], y);
       s_y[i] = round_bf16(y * inv);
     }
     __syncthreads();
@@ -343,9 +365,7 @@ struct AttnArgs {
 
 template <int HD, int NT, bool PROJ>
 int launch_attention_nt(const AttnArgs &a, hipStream_t stream) {
-  const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave) + (size_t)a.max_len);
-  if (shmem > 64 * 1024)
-    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len=%d too long for one workgroup", a.max_len);
+  const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave));
   const dim3 grid((unsigned)(a.B * a.H));
   if (a.rope_f32)
     hipLaunchKernelGGL((decode_attention_kernel<true, HD, NT, PROJ>), grid, dim3(NT), shmem, stream,
