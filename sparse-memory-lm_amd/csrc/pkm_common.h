@@ -59,21 +59,24 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// v of lane ^ J (J < 64) on every lane: quad permutes (1, 2), row shifts by 4 either way (4), a row rotation (8),
-// and the gfx950 permlane swaps (16, 32), which given a register twice return v[lane] and v[lane ^ J] in some order.
+// v of lane ^ J (J < 64) on every lane: quad permutes (1, 2), two row rotations that each write half of the lanes
+// (4), a row rotation (8), and the gfx950 permlane swaps (16, 32), which given a register twice return v[lane] and
+// v[lane ^ J] in some order.  The DPP moves have every lane either read a valid source lane or be rewritten by the
+// second move, so they need no initial value in the destination (one instruction each, no zero fill).
 template <int J>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
   const int lane = lane_id();
   if constexpr (J == 1) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
   } else if constexpr (J == 2) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
-  } else if constexpr (J == 4) {  // row_shl:4 (lane i reads i + 4) or row_shr:4 (i - 4), both inside the row
-    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);
-    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
-    return (lane & 4) ? dn : up;
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4) {
+    // row_ror:n has lane i of a row read lane (i - n) mod 16: n = 12 is i + 4 for banks 0 and 2 (lanes 0-3,
+    // 8-11 of the row), n = 4 is i - 4 for banks 1 and 3; the bank mask keeps each move to its lanes
+    const int t = __builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xF, 0x5, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)v, 0x124, 0xF, 0xA, false);
   } else if constexpr (J == 8) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
   } else if constexpr (J == 16) {
     const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
     return (lane & 16) ? (uint32_t)p[0] : (uint32_t)p[1];
