@@ -16,8 +16,9 @@
 //      elements (the top knn lanes each hold one), found by a bitwise search over ballot() counts;
 //   3. the 16-byte chunks holding an element >= code0 are staged in LDS, and their elements >= code0 (typically a
 //      few dozen) are compacted into the candidate list via a lane prefix sum;
-//   4. the exact knn-th largest key t1 among them is found by the same bitwise search with the candidates held
-//      in registers; the knn keys >= t1 are compacted and put in descending order by counting ranks.
+//   4. up to 64 candidates (the usual case: one per lane) are sorted by a register bitonic network and the first
+//      knn lanes are the answer; more candidates take the same bitwise search for the exact knn-th largest key t1,
+//      with the knn keys >= t1 compacted and put in descending order by counting ranks.
 // Rows outside the register shapes, or with more than kCap elements at or above code0 (adversarial ties),
 // take the streaming path, which searches the row in global memory directly.
 #include "pkm_bag_dev.h"
@@ -155,6 +156,56 @@ __device__ __forceinline__ int wave_exclusive_sum(int v, int *total) {
   return incl - v;
 }
 
+// v of lane ^ J for a 32- or 64-bit key
+template <int J, typename Key>
+__device__ __forceinline__ Key xor_lane_key(Key v) {
+  if constexpr (sizeof(Key) == 8) return xor_lane64<J>(v);
+  else return xor_lane<J>(v);
+}
+
+// One compare-exchange stage (block size K, distance J < 64) of a descending bitonic sort of the wavefront's
+// SLOTS * 64 keys, element e = s * 64 + lane.
+template <typename Key, int SLOTS, int K, int J>
+__device__ __forceinline__ void bitonic_stage(Key (&x)[SLOTS]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int e = s * kWave + lane;
+    const Key y = xor_lane_key<J>(x[s]);
+    const bool take_max = ((e & J) == 0) == ((e & K) == 0);  // the lower element of a descending block: max
+    const bool gt = x[s] > y;
+    x[s] = (gt == take_max) ? x[s] : y;
+  }
+}
+
+template <typename Key, int SLOTS, int K, int J>
+__device__ __forceinline__ void bitonic_merge(Key (&x)[SLOTS]) {
+  if constexpr (J >= kWave) {  // partner in the same lane: slots s and s ^ (J / 64)
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const int s2 = s ^ (J / kWave);
+      if (s2 > s) {
+        const bool desc = ((s * kWave) & K) == 0;
+        const Key a = x[s], b = x[s2];
+        const Key mx = a > b ? a : b, mn = a > b ? b : a;
+        x[s] = desc ? mx : mn;
+        x[s2] = desc ? mn : mx;
+      }
+    }
+  } else {
+    bitonic_stage<Key, SLOTS, K, J>(x);
+  }
+  if constexpr (J > 1) bitonic_merge<Key, SLOTS, K, J / 2>(x);
+}
+
+// Descending bitonic sort of SLOTS * 64 unique keys held one per lane per slot; afterwards lane j of slot 0 holds
+// the j-th largest.
+template <typename Key, int SLOTS, int K = 2>
+__device__ __forceinline__ void bitonic_sort_desc(Key (&x)[SLOTS]) {
+  bitonic_merge<Key, SLOTS, K, K / 2>(x);
+  if constexpr (K < SLOTS * kWave) bitonic_sort_desc<Key, SLOTS, K * 2>(x);
+}
+
 // The knn keys >= t (exactly knn exist) from `src` (n entries, LDS) into out[] in descending order.
 template <typename Key, typename Fetch>
 __device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetch, Key *sel, Key *out) {
@@ -178,7 +229,6 @@ __device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetc
   wave_lds_sync();
 }
 
-// Exact top-knn among C candidate keys in LDS, into out[] descending.
 // Exact top-knn among C candidate keys in LDS (keys of sub-key indices < 2^IB), into out[] descending.
 template <bool F32>
 __device__ __forceinline__ void topk_of_candidates(int C, int knn, int IB, typename SelKey<F32>::T *cand,
@@ -187,9 +237,12 @@ __device__ __forceinline__ void topk_of_candidates(int C, int knn, int IB, typen
   constexpr int kTop = F32 ? 64 : 32, kS = F32 ? 32 : 16;
   const int lane = lane_id();
   Key t;
-  if (C <= kWave) {  // one key per lane (the common case)
-    const Key r0 = lane < C ? cand[lane] : (Key)0;
-    t = key_search<Key>(knn, kTop, kS, IB, [&](Key c) { return count_ge_lanes(r0, c); });
+  if (C <= kWave) {  // one key per lane (the common case): sort them, the first knn lanes are the answer
+    Key x[1] = {lane < C ? cand[lane] : (Key)0};
+    bitonic_sort_desc<Key, 1>(x);
+    if (lane < knn) out[lane] = x[0];
+    wave_lds_sync();
+    return;
   } else if (C <= kRegCand * kWave) {
     Key reg[kRegCand];
 #pragma unroll
@@ -384,49 +437,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-// One compare-exchange stage (block size K, distance J < 64) of a descending bitonic sort of the wavefront's
-// SLOTS * 64 keys, element e = s * 64 + lane.
-template <int SLOTS, int K, int J>
-__device__ __forceinline__ void bitonic_stage(uint64_t (&x)[SLOTS]) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const int e = s * kWave + lane;
-    const uint64_t y = xor_lane64<J>(x[s]);
-    const bool take_max = ((e & J) == 0) == ((e & K) == 0);  // the lower element of a descending block: max
-    const bool gt = x[s] > y;
-    x[s] = (gt == take_max) ? x[s] : y;
-  }
-}
-
-template <int SLOTS, int K, int J>
-__device__ __forceinline__ void bitonic_merge(uint64_t (&x)[SLOTS]) {
-  if constexpr (J >= kWave) {  // partner in the same lane: slots s and s ^ (J / 64)
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const int s2 = s ^ (J / kWave);
-      if (s2 > s) {
-        const bool desc = ((s * kWave) & K) == 0;
-        const uint64_t a = x[s], b = x[s2];
-        const uint64_t mx = a > b ? a : b, mn = a > b ? b : a;
-        x[s] = desc ? mx : mn;
-        x[s2] = desc ? mn : mx;
-      }
-    }
-  } else {
-    bitonic_stage<SLOTS, K, J>(x);
-  }
-  if constexpr (J > 1) bitonic_merge<SLOTS, K, J / 2>(x);
-}
-
-// Descending bitonic sort of SLOTS * 64 unique 64-bit keys held one per lane per slot; afterwards lane j of slot 0
-// holds the j-th largest.
-template <int SLOTS, int K = 2>
-__device__ __forceinline__ void bitonic_sort_desc(uint64_t (&x)[SLOTS]) {
-  bitonic_merge<SLOTS, K, K / 2>(x);
-  if constexpr (K < SLOTS * kWave) bitonic_sort_desc<SLOTS, K * 2>(x);
-}
-
 // The Cartesian pairs' keys (code << 32 | ~full index; 0 for a slot without a pair)
 template <bool F32, int SLOTS>
 __device__ __forceinline__ void cartesian_keys(const typename SelKey<F32>::T *top1, const typename SelKey<F32>::T *top2,
@@ -511,12 +521,12 @@ __device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *to
   } else if (knn >= 32) {
     uint64_t ck[2];
     cartesian_keys<F32, 2>(top1, top2, NK, pc, ck);
-    bitonic_sort_desc<2>(ck);
+    bitonic_sort_desc<uint64_t, 2>(ck);
     u = ck[0];
   } else {
     uint64_t ck[1];
     cartesian_keys<F32, 1>(top1, top2, NK, pc, ck);
-    bitonic_sort_desc<1>(ck);
+    bitonic_sort_desc<uint64_t, 1>(ck);
     u = ck[0];
   }
 
