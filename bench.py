@@ -142,6 +142,61 @@ def chained_launch_us(dev, numel=384, kernels=272, replays=40):
     return 1000.0 * event_time_ms(graph.replay, replays) / kernels
 
 
+def device_handoff(dev, stages=64, replays=20):
+    """Device time per dependent stage (every workgroup reads the whole 2 KB vector its predecessors wrote and
+    writes its slice of the next) when the stages are kernels back to back in a HIP graph, against one persistent
+    kernel whose workgroups hand off to each other on the device (csrc/bench/handoff.hip): one atomic counter,
+    per-XCD-group counters under a top counter, a flag per workgroup (release / acquire fences), and flags with
+    device-coherent data accesses and no fences.  Waits are bounded; a run whose waits gave up raises."""
+    import ctypes
+    import torch
+    from smlm_hip import build as hip_build
+    lib = ctypes.CDLL(hip_build.BENCH_LIB_PATH)
+    vp = ctypes.c_void_p
+    n = lib.smlm_bench_handoff_vec()
+    v0, v1 = torch.zeros(n, device=dev), torch.zeros(n, device=dev)
+    ctr = torch.zeros(576, dtype=torch.int32, device=dev)
+    abort = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {"stages": stages, "vector_bytes": 4 * n}
+
+    def stream():
+        return vp(torch.cuda.current_stream(dev).cuda_stream)
+
+    def chain(nwg):
+        rc = lib.smlm_bench_handoff_chain(vp(v0.data_ptr()), vp(v1.data_ptr()), stages, nwg, stream())
+        if rc != 0:
+            raise RuntimeError(f"smlm_bench_handoff_chain: {rc}")
+
+    for nwg in (64, 256):
+        flags = torch.zeros(nwg, dtype=torch.int32, device=dev)
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            chain(nwg)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            chain(nwg)
+        res = {"kernel_chain_us": 1000.0 * event_time_ms(graph.replay, replays) / stages}
+        for kind, name in ((0, "one_counter_us"), (1, "group_counters_us"), (2, "flags_fenced_us"),
+                           (3, "flags_coherent_us")):
+            def run(k=stages, kind=kind):
+                ctr.zero_()
+                flags.zero_()
+                rc = lib.smlm_bench_handoff_persistent(vp(v0.data_ptr()), vp(v1.data_ptr()), k, nwg, kind,
+                                                       vp(ctr.data_ptr()), vp(flags.data_ptr()),
+                                                       vp(abort.data_ptr()), stream())
+                if rc != 0:
+                    raise RuntimeError(f"smlm_bench_handoff_persistent: {rc}")
+            full, one = event_time_ms(run, replays), event_time_ms(lambda: run(1), replays)
+            if int(abort.item()):
+                raise RuntimeError(f"handoff kind {kind} at {nwg} workgroups: a wait gave up")
+            res[name] = 1000.0 * (full - one) / (stages - 1)
+        out[f"wg{nwg}"] = res
+        log(f"dependent stage at {nwg} workgroups: " + ", ".join(f"{k} {v:.2f}" for k, v in res.items()))
+    return out
+
+
 def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
     """The two floors of one fused decode step against its measured time.
     HBM: the bytes a step must move — every weight matrix once (the tied embedding once as lm_head, plus B embedding
@@ -726,7 +781,7 @@ def calibration_copy(dev, nbytes=1 << 30):
 
 
 HEADLINE_PHASES = "decode,gather,cpu,config1,config0,prefill,lookup"
-OPTIONAL_PHASES = "offload,train,engram"
+OPTIONAL_PHASES = "offload,train,engram,handoff"
 
 
 def main():
@@ -893,6 +948,7 @@ def main():
                     v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
         line["train_kernels"] = tr
         line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps))
+        line["device_handoff"] = phase("handoff", lambda: device_handoff(dev))
     finally:
         if errors:
             line["phase_errors"] = errors

@@ -30,7 +30,6 @@ namespace {
 constexpr int kTrainThreads = 256;
 constexpr int kTrainWaves = kTrainThreads / kWave;
 constexpr int kMaxD = 512;                  // columns per row: lane l owns l, l + 64, ... (at most 8 each)
-constexpr int kColsPerLane = kMaxD / kWave;
 constexpr int kBagInFlight = 4;             // lookups per wavefront whose row loads are issued together
 
 __device__ __forceinline__ float wave_sum_f32(float v) {

@@ -3,7 +3,8 @@
     python -m smlm_hip.build            (from sparse-memory-lm_amd/)
 
 Every .hip file is compiled to an object in sparse-memory-lm_amd/_build/ (in parallel), then linked into
-smlm_hip/libsmlm_pkm.so next to this file, where smlm_hip._lib loads it.
+smlm_hip/libsmlm_pkm.so next to this file, where smlm_hip._lib loads it.  The measurement kernels of bench.py
+(csrc/bench/*.hip) go into a separate smlm_hip/libsmlm_bench.so, so the lookup library holds only the product.
 """
 import os
 import subprocess
@@ -18,6 +19,7 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD_DIR = os.path.join(ROOT, "_build")
 LIB_NAME = "libsmlm_pkm.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+BENCH_LIB_PATH = os.path.join(PKG_DIR, "libsmlm_bench.so")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -32,12 +34,13 @@ CFLAGS = [
 ]
 
 
-def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+def sources(folder=CSRC):
+    return sorted(os.path.join(folder, f) for f in os.listdir(folder) if f.endswith(".hip"))
 
 
 def _compile(src):
-    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
+    sub = os.path.relpath(os.path.dirname(src), CSRC).replace(os.sep, "_").strip("._")
+    obj = os.path.join(BUILD_DIR, (sub + "_" if sub else "") + os.path.basename(src)[:-4] + ".o")
     cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so; that warning is harmless
@@ -49,20 +52,26 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
-    """Compile every csrc/*.hip for gfx950 and link libsmlm_pkm.so. Always rebuilds."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    srcs = sources()
-    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB_PATH + ".tmp"
+def _link(objs, path):
+    tmp = path + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build(verbose=True):
+    """Compile every csrc/*.hip for gfx950 and link libsmlm_pkm.so, and csrc/bench/*.hip into libsmlm_bench.so.
+    Always rebuilds."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    srcs, bench_srcs = sources(), sources(os.path.join(CSRC, "bench"))
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs) + len(bench_srcs))) as ex:
+        objs = list(ex.map(_compile, srcs + bench_srcs))
+    _link(objs[:len(srcs)], LIB_PATH)
+    _link(objs[len(srcs):], BENCH_LIB_PATH)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources", flush=True)
+        print(f"built {LIB_PATH} from {len(srcs)} sources and {BENCH_LIB_PATH} from {len(bench_srcs)}", flush=True)
     return LIB_PATH
 
 
