@@ -9,7 +9,8 @@
 //   - all keys are distinct, so "the knn largest keys" is one exact set.
 //
 // One workgroup = two wavefronts per (token, head) row: wavefront 0 selects in s1, wavefront 1 in s2, then
-// wavefront 0 does the Cartesian step.  Half top-k of a wavefront (row of NK <= 4096 bf16 / 2048 fp32 scores):
+// wavefront 0 does the Cartesian step (at knn = 32 each sorts half of the pairs and wavefront 0 merges the two).
+// Half top-k of a wavefront (row of NK <= 4096 bf16 / 2048 fp32 scores):
 //   1. the row is loaded into registers with 16-byte loads, all in flight at once (lane l holds chunks
 //      l, l+64, ...), and turned into order codes (packed 16-bit ops for bf16);
 //   2. each lane's maximum code; the knn-th largest of the 64 lane maxima, code0, is reached by at least knn
@@ -494,40 +495,54 @@ __device__ __forceinline__ uint64_t cartesian_threshold(const typename SelKey<F3
   return t;
 }
 
-// Cartesian step of one head, by one wavefront: candidates (i, j) with (i+1)(j+1) <= knn of the two halves'
-// descending top lists, scored dtype(v1[i] + v2[j]), top-knn by (score, lowest table index), softmax in fp32.
-// Lane j < knn ends with the j-th best pair: its score `sc` (code = order code of its bits), table index `full`
-// and weight `wt`.  pc: the lane's pairs from load_pairs; s_fsel, s_fin: kMaxKnn entries of LDS scratch.
+// Cartesian step of one head: candidates (i, j) with (i+1)(j+1) <= knn of the two halves' descending top lists,
+// scored dtype(v1[i] + v2[j]), top-knn by (score, lowest table index), softmax in fp32.  Called by both wavefronts
+// of the head, p = 0 and p = 1 (and by every wavefront of the workgroup, since knn = 32 has a workgroup barrier);
+// returns true on wavefront 0, whose lane j < knn then holds the j-th best pair: its score `sc` (code = order code of
+// its bits), table index `full` and weight `wt`.  pc: the lane's pairs from load_pairs; s_x, s_fsel, s_fin: kMaxKnn
+// entries of LDS scratch each (s_x may be s_fin).
+// Pairs per knn: <= 50 (one slot of 64 lanes), 119 (two), 280 (five).  One slot: a bitonic sort in registers (keys
+// are unique: distinct pairs have distinct table indices; pair-less slots sort last).  Two slots: each wavefront
+// sorts one, wavefront 1 leaves its sorted keys in s_x, and wavefront 0 takes, lane by lane, the larger of its j-th
+// and the other's (63 - j)-th key: the 64 largest of both, a bitonic sequence, which one merge puts in order.
+// Five: the threshold search, compaction and rank through LDS.
 template <bool F32>
-__device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *top1,
+__device__ __forceinline__ bool cartesian_topk(const typename SelKey<F32>::T *top1,
                                                const typename SelKey<F32>::T *top2, int NK, int knn,
-                                               const uint32_t (&pc)[kMaxPairSlots], uint64_t *s_fsel,
-                                               uint64_t *s_fin, float &sc, uint32_t &full, uint32_t &code,
-                                               float &wt) {
+                                               const uint32_t (&pc)[kMaxPairSlots], int p, uint64_t *s_x,
+                                               uint64_t *s_fsel, uint64_t *s_fin, float &sc, uint32_t &full,
+                                               uint32_t &code, float &wt) {
   const int lane = lane_id();
-  // pairs per knn: <= 50 (one slot of 64 lanes), 119 (two), 280 (five).  Up to two slots: a bitonic sort in
-  // registers (keys are unique: distinct pairs have distinct table indices; pair-less slots sort last); five: the
-  // threshold search, compaction and rank through LDS.
   uint64_t u = 0;
-  if (knn >= 64) {
-    cartesian_threshold<F32, 5>(top1, top2, NK, knn, pc, s_fsel);
-    wave_lds_sync();
-    if (lane < knn) {
-      const uint64_t mine = s_fsel[lane];
-      s_fin[rank_in(s_fsel, knn, mine)] = mine;
-    }
-    wave_lds_sync();
-    if (lane < knn) u = s_fin[lane];
-  } else if (knn >= 32) {
-    uint64_t ck[2];
-    cartesian_keys<F32, 2>(top1, top2, NK, pc, ck);
-    bitonic_sort_desc<uint64_t, 2>(ck);
-    u = ck[0];
+  if (knn == 32) {
+    const uint32_t mine[kMaxPairSlots] = {pc[p], kNoPair, kNoPair, kNoPair, kNoPair};
+    uint64_t x[1];
+    cartesian_keys<F32, 1>(top1, top2, NK, mine, x);
+    bitonic_sort_desc<uint64_t, 1>(x);
+    if (p == 1) s_x[lane] = x[0];
+    __syncthreads();
+    if (p != 0) return false;
+    const uint64_t y = s_x[kWave - 1 - lane];
+    uint64_t m[1] = {x[0] > y ? x[0] : y};
+    bitonic_merge<uint64_t, 1, kWave, kWave / 2>(m);
+    u = m[0];
   } else {
-    uint64_t ck[1];
-    cartesian_keys<F32, 1>(top1, top2, NK, pc, ck);
-    bitonic_sort_desc<uint64_t, 1>(ck);
-    u = ck[0];
+    if (p != 0) return false;
+    if (knn >= 64) {
+      cartesian_threshold<F32, 5>(top1, top2, NK, knn, pc, s_fsel);
+      wave_lds_sync();
+      if (lane < knn) {
+        const uint64_t mine = s_fsel[lane];
+        s_fin[rank_in(s_fsel, knn, mine)] = mine;
+      }
+      wave_lds_sync();
+      if (lane < knn) u = s_fin[lane];
+    } else {
+      uint64_t ck[1];
+      cartesian_keys<F32, 1>(top1, top2, NK, pc, ck);
+      bitonic_sort_desc<uint64_t, 1>(ck);
+      u = ck[0];
+    }
   }
 
   sc = 0.f;
@@ -542,6 +557,7 @@ __device__ __forceinline__ void cartesian_topk(const typename SelKey<F32>::T *to
   const float mxs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), 0));
   const float e = lane < knn ? expf(sc - mxs) : 0.f;
   wt = e / wave_sum_dpp(e);
+  return true;
 }
 
 template <bool F32, int CPL>
@@ -565,11 +581,10 @@ __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1
   if constexpr (CPL > 0) half_topk_reg<F32, CPL, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
   else half_topk_stream<F32, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
   __syncthreads();
-  if (wave != 0) return;
 
   float sc, wt;
   uint32_t full, code;
-  cartesian_topk<F32>(s_top[0], s_top[1], NK, knn, pc, s_fsel, s_fin, sc, full, code, wt);
+  if (!cartesian_topk<F32>(s_top[0], s_top[1], NK, knn, pc, wave, s_fin, s_fsel, s_fin, sc, full, code, wt)) return;
   if (lane < knn) {
     const int64_t o = row * knn + lane;
     if constexpr (F32) ((float *)scores)[o] = sc;
@@ -642,11 +657,10 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   else half_topk_stream<F32, CAP>(src, NK, knn, s_cand + wave * CAP, sel, top);
   __syncthreads();
 
-  if (p == 0) {
-    float sc, wt;
-    uint32_t full, code;
-    cartesian_topk<F32>(s_top + 2 * h * kMaxKnn, s_top + (2 * h + 1) * kMaxKnn, NK, knn, pc,
-                        s_fsel + h * kMaxKnn, s_fin + h * kMaxKnn, sc, full, code, wt);
+  float sc, wt;
+  uint32_t full, code;
+  if (cartesian_topk<F32>(s_top + 2 * h * kMaxKnn, s_top + (2 * h + 1) * kMaxKnn, NK, knn, pc, p,
+                          s_fin + h * kMaxKnn, s_fsel + h * kMaxKnn, s_fin + h * kMaxKnn, sc, full, code, wt)) {
     if (lane < knn) {
       const int64_t o = row * knn + lane;
       if (scores) {
