@@ -2,10 +2,12 @@
 // per sequence (T = 1), fused into one kernel so the captured decode step does not pay ~35 small launches per
 // layer.  Per (sequence b, head h), one workgroup:
 //   1. RoPE (model.py:63-78: rotate the two halves of the head) on the new token's q and k, in fp32, rounded to
-//      bf16 as the bf16 model holds them; k and v are written into the cache at the device-side position `pos`;
-//   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos (the new token's own k from LDS), each cache row read
-//      with 16-byte loads by head_dim/8 lanes and reduced with lane shuffles; the keys and values of a group of
-//      passes of rows are in flight together (a decode step is latency-bound);
+//      bf16 as the bf16 model holds them, by every wavefront for itself through its own LDS row (no workgroup
+//      barrier); k and v are written into the cache at the device-side position `pos`;
+//   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos, each cache row read with 16-byte loads by
+//      head_dim/8 lanes and reduced with lane shuffles; the keys and values of a group of passes of rows are in
+//      flight together (a decode step is latency-bound), issued after the new token's q, k, v and only for passes
+//      that hold rows (raw buffer loads bounded at row pos), so each pass is used as soon as its rows arrive;
 //   3. softmax in fp32, by each wavefront over its own rows and in registers: its maximum m_w, the exponentials
 //      p_t = exp(s_t - m_w) and their sum l_w (online over the groups of passes: a group that raises the maximum
 //      rescales what came before);
@@ -16,7 +18,7 @@
 // The PROJ variant folds the output projection (model.py:107, wo) in: y, rounded to bf16 as above, is multiplied by
 // the head's column slice of wo, and the n_out fp32 dot products go to parts[b, h, :]; the sum over heads (in head
 // order) is left to the consumer (the RMSNORM_PARTS prologue of smlm_decode_linear), one launch fewer per layer.
-// The slice's first rows are loaded at the start, so they arrive with the cache rows.
+// The slice's first rows are loaded first of all (they depend on nothing this step computes).
 // A position outside [0, min(max_len, rope_len)) writes nothing to the cache and NaN to the output.
 #include "pkm_common.h"
 
@@ -116,10 +118,42 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   }
 }
 
-// Passes of wo rows the projection (PROJ) holds in registers, the first of them loaded at the start (one pass =
-// threads / (head_dim / 8) rows: with 1024 threads and head_dim 64, 4 passes = 512 rows).
+// Passes of wo rows the projection (PROJ) holds in registers, loaded before the cache rows are used (one pass =
+// threads / (head_dim / 8) rows: with 1024 threads and head_dim 64, 3 passes = 384 rows, a d_model 384 model's
+// whole slice; more would spill registers of the 1024-thread workgroup).
 template <int kAttnThreads>
-constexpr int wo_regs() { return kAttnThreads >= 1024 ? 4 : kAttnThreads >= 512 ? 6 : 12; }
+constexpr int wo_regs() { return kAttnThreads >= 1024 ? 3 : kAttnThreads >= 512 ? 6 : 12; }
+
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+
+// f(IntC<n>{}) for a runtime n in [0, MAX] (a chain of compares): code that needs its count at compile time.
+template <int MAX, int N = 0, class F>
+__device__ __forceinline__ void with_count(int n, F &&f) {
+  if constexpr (N == MAX) {
+    f(IntC<N>{});
+  } else {
+    if (n == N) {
+      f(IntC<N>{});
+      return;
+    }
+    with_count<MAX, N + 1>(n, f);
+  }
+}
+
+// 16-byte loads from a range of n bf16 values through a raw buffer resource (gfx9 layout: base, stride 0,
+// num_records in bytes, dword 3 = 0x00020000): a load at or past the end returns zeros and makes no memory access,
+// so a wavefront can issue a fixed number of loads whatever the range's length.  Offsets are 32-bit bytes.
+struct BufferRows {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ BufferRows(const uint16_t *base, int64_t n)
+      : r(__builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(n * 2), 0x00020000)) {}
+  __device__ __forceinline__ uint4 load(int elem) const {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, elem * 2, 0, 0));
+  }
+};
 
 template <bool ROPE_F32, int HD, int kAttnThreads, bool PROJ>
 __global__ void __launch_bounds__(kAttnThreads)
@@ -132,148 +166,173 @@ __global__ void __launch_bounds__(kAttnThreads)
   constexpr int LPR = HD / 8;            // lanes per cache row (8 dims, 16 bytes each)
   constexpr int RPW = kWave / LPR;       // rows per wavefront per pass
   constexpr int RPB = RPW * kAttnWaves;  // rows per workgroup per pass
+  constexpr int HALF = HD / 2;           // RoPE rotates dim i with dim i + HALF
   constexpr int WR = wo_regs<kAttnThreads>();
   constexpr int RPP = kAttnThreads / LPR;  // wo rows per projection pass (LPR lanes per row, 8 columns each)
+  // (the projection's wo registers leave room for 6 passes under the 128 VGPRs of a 1024-thread workgroup)
+  // (the online softmax rescales per group, so the plain and PROJ variants group alike to reach the same y)
+  constexpr int U = kAttnThreads >= 1024 ? 6 : kAttnUnroll;
   extern __shared__ __align__(16) float smem[];
-  float *s_q = smem;                     // [HD]
-  float *s_k = s_q + HD;                 // [HD] new token's k (bf16 values)
-  float *s_v = s_k + HD;                 // [HD]
-  float *s_red = s_v + HD;               // [kAttnWaves][HD] the wavefronts' sums of p * v
+  float *s_y = smem;                     // [HD] the bf16-rounded output (PROJ)
+  float *s_red = s_y + HD;               // [kAttnWaves][HD] the wavefronts' rotated q, later their sums of p * v
   float *s_w = s_red + kAttnWaves * HD;  // [2][kAttnWaves] the wavefronts' maxima, then their sums of p
+  float *s_kv = s_w + 2 * kAttnWaves;    // [2][HD] the new token's rotated k and its v (wavefront 0)
 
-  const int b = blockIdx.x / H, h = blockIdx.x % H;
+  const int b = blockIdx.y, h = blockIdx.x;  // (the grid's linear order is b * H + h)
   const int tid = threadIdx.x, wave = tid / kWave, lane = lane_id();
   const int C = H * HD;
-  // the projection's first wo rows (they depend on nothing this step computes); row wr0 + i * RPP, columns
-  // h * HD + wc * 8 .. + 7; passes that start past n_out load nothing, rows past n_out re-read row n_out - 1
+  const uint16_t *row = qkv + (int64_t)b * qkv_stride + h * HD;
+  const int64_t cache_row = ((int64_t)b * H + h) * max_len;
+  const int sub = lane % LPR, rw = lane / LPR;
+  const int slot = wave * RPW + rw;
+  const int d0 = sub * 8;  // this lane's 8 dims of the head
+
+  // 0. Loads, in the order they are used (a wavefront's load counter retires in issue order, so anything loaded
+  // after the cache rows could only be used once they had all arrived), every one issued on every path so that
+  // the counts the compiler waits on are known.  What does not depend on the position is issued before it is read:
+  //   the projection's first wo rows (PROJ: row wr0 + i * RPP, columns h * HD + wc * 8 .. + 7, rows past n_out
+  //     re-read row n_out - 1);
+  //   the new token's q, k and v for the RoPE (lane i: rotation pair i % HALF, 2-byte loads);
+  // then, after the position: the pair's rotation factors and, per pass of the first group that holds rows < P, the
+  // cache rows (all the keys, then the values; rows at or past P read as zeros without a memory access).  Row P
+  // itself is never loaded from the cache.
   const int wc = tid % LPR, wr0 = tid / LPR;
   uint4 wreg[PROJ ? WR : 1];
   if constexpr (PROJ) {
 #pragma unroll
     for (int i = 0; i < WR; ++i) {
-      if (i * RPP >= n_out) break;  // workgroup-uniform
       const int n = min(wr0 + i * RPP, n_out - 1);
       wreg[i] = *(const uint4 *)(wo + (int64_t)n * wo_stride + h * HD + wc * 8);
     }
   }
-  const int64_t P = *pos_ptr;
+  const int pi = lane % HALF;  // this lane's rotation pair
+  const uint32_t q1b = row[pi], q2b = row[pi + HALF], k1b = row[C + pi], k2b = row[C + pi + HALF];
+  constexpr int HD_HI = HD > kWave ? HD - kWave : 1;  // v dims past the first 64 (head_dim 128)
+  const uint32_t vb0 = row[2 * C + lane % HD], vb1 = HD > kWave ? row[2 * C + kWave + lane % HD_HI] : 0;
+  // A position outside [0, min(max_len, rope_len)) computes as position 0 (so every address stays in range and no
+  // branch holds back the loads above), writes nothing to the cache and NaN to the output.
+  const int64_t P_in = *pos_ptr;
+  const bool valid = P_in >= 0 && P_in < max_len && P_in < rope_len;
+  const int64_t P = valid ? P_in : 0;
   uint16_t *o = PROJ ? nullptr : out + (int64_t)b * C + (int64_t)h * HD;
   float *po = PROJ ? parts + ((int64_t)b * H + h) * n_out : nullptr;
-  if (P < 0 || P >= max_len || P >= rope_len) {
-    if constexpr (PROJ) {
-      for (int i = tid; i < n_out; i += kAttnThreads) po[i] = __builtin_nanf("");
-    } else {
-      for (int i = tid; i < HD; i += kAttnThreads) o[i] = 0x7FC0;  // bf16 NaN
-    }
-    return;
-  }
-  const uint16_t *row = qkv + (int64_t)b * qkv_stride;
-  const int64_t cache_row = ((int64_t)b * H + h) * max_len;
+  const float c_rot = table_val<ROPE_F32>(rope_cos, P * HALF + pi);
+  const float s_rot = table_val<ROPE_F32>(rope_sin, P * HALF + pi);
+  // the cache rows 0..P-1 of (b, h) as raw buffers: a row at or past P reads as zero without a memory access
+  const BufferRows krows(k_cache + cache_row * HD, P * HD), vrows(v_cache + cache_row * HD, P * HD);
 
-  // 0. The first group of cache rows (keys and values of rows < P, which do not depend on this step) is loaded
-  // before anything else, so its round trip overlaps the one of the qkv row below.  Row P itself (written in 1.)
-  // is never loaded: rows are clamped to P - 1 and row P is taken from LDS.
-  // (the projection's wo registers leave room for 6 passes under the 128 VGPRs of a 1024-thread workgroup)
-  // (the online softmax rescales per group, so the plain and PROJ variants group alike to reach the same y)
-  constexpr int U = kAttnThreads >= 1024 ? 6 : kAttnUnroll;
-  const int sub = lane % LPR, rw = lane / LPR;
-  const int slot = wave * RPW + rw;
-  const int64_t last = P > 0 ? P - 1 : 0;  // rows 0..P-1 come from the cache (the new row P from LDS)
-  uint4 kv[U], vpre[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
-    const int64_t t = min((int64_t)(u * RPB + slot), last);
-    kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
-    vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
-  }
-
-  // 1. RoPE on q, k; v as is; new k, v into the cache
-  for (int i = tid; i < HD / 2; i += kAttnThreads) {
-    const float c = table_val<ROPE_F32>(rope_cos, P * (HD / 2) + i);
-    const float s = table_val<ROPE_F32>(rope_sin, P * (HD / 2) + i);
-    const float q1 = bf16_bits_to_f32(row[h * HD + i]), q2 = bf16_bits_to_f32(row[h * HD + HD / 2 + i]);
-    const float k1 = bf16_bits_to_f32(row[C + h * HD + i]), k2 = bf16_bits_to_f32(row[C + h * HD + HD / 2 + i]);
-    s_q[i] = round_bf16(q1 * c - q2 * s);
-    s_q[i + HD / 2] = round_bf16(q1 * s + q2 * c);
-    const uint32_t ka = bf16_bits_rtne(k1 * c - k2 * s), kb = bf16_bits_rtne(k1 * s + k2 * c);
-    s_k[i] = bf16_bits_to_f32(ka);
-    s_k[i + HD / 2] = bf16_bits_to_f32(kb);
-    k_cache[(cache_row + P) * HD + i] = (uint16_t)ka;
-    k_cache[(cache_row + P) * HD + HD / 2 + i] = (uint16_t)kb;
-  }
-  for (int i = tid; i < HD; i += kAttnThreads) {
-    const uint16_t vb = row[2 * C + h * HD + i];
-    s_v[i] = bf16_bits_to_f32(vb);
-    v_cache[(cache_row + P) * HD + i] = vb;
-  }
-  __syncthreads();
-
-  // 2-4. Per wavefront, in registers: scores of its rows, their maximum, exponentials and the sum of p * v.  The
-  // first group's keys and values came in step 0; later groups load both before the first is used.
   const float scale = rsqrtf((float)HD);
-  float qf[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) qf[e] = s_q[sub * 8 + e];
-  float m_run = -INFINITY, l_run = 0.f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  for (int t0 = 0; t0 <= P; t0 += RPB * U) {
-    if (t0 > 0) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (t0 + u * RPB > P) continue;  // workgroup-uniform: passes past the last row load nothing
-        const int64_t t = min((int64_t)(t0 + u * RPB + slot), last);
-        kv[u] = *(const uint4 *)(k_cache + (cache_row + t) * HD + sub * 8);
-        vpre[u] = *(const uint4 *)(v_cache + (cache_row + t) * HD + sub * 8);
+  float qf[8];                                   // this lane's 8 dims of the rotated q
+  float m_run = -INFINITY, l_run = 0.f, acc[8] = {};  // the wavefront's running softmax
+
+  // 1. RoPE (dim i < HALF: x_i c_i - x_{i+HALF} s_i, dim i + HALF: x_i s_i + x_{i+HALF} c_i, in fp32 with one bf16
+  // rounding), by every wavefront for itself through its own LDS row (no workgroup barrier); wavefront 0 also
+  // writes the new k and v into the cache slot P.  Then row P opens wavefront 0's running softmax (its score, in
+  // every lane: the LPR lanes of each row group sum the same dims; its weight and v in row group 0), so the passes
+  // cover the cache rows 0..P-1 only.
+  auto rope = [&]() {
+    const float q1 = bf16_bits_to_f32(q1b), q2 = bf16_bits_to_f32(q2b);
+    const float k1 = bf16_bits_to_f32(k1b), k2 = bf16_bits_to_f32(k2b);
+    float *s_q = s_red + wave * HD;
+    if (lane < HALF) {
+      s_q[pi] = round_bf16(q1 * c_rot - q2 * s_rot);
+      s_q[pi + HALF] = round_bf16(q1 * s_rot + q2 * c_rot);
+    }
+    if (wave == 0) {
+      const uint32_t ka = bf16_bits_rtne(k1 * c_rot - k2 * s_rot), kb = bf16_bits_rtne(k1 * s_rot + k2 * c_rot);
+      if (lane < HALF) {
+        s_kv[pi] = bf16_bits_to_f32(ka);
+        s_kv[pi + HALF] = bf16_bits_to_f32(kb);
+        if (valid) {
+          k_cache[(cache_row + P) * HD + pi] = (uint16_t)ka;
+          k_cache[(cache_row + P) * HD + pi + HALF] = (uint16_t)kb;
+        }
+      }
+      if (lane < HD) {
+        s_kv[HD + lane] = bf16_bits_to_f32(vb0);
+        if (valid) v_cache[(cache_row + P) * HD + lane] = (uint16_t)vb0;
+      }
+      if (HD > kWave && lane < HD - kWave) {
+        s_kv[HD + kWave + lane] = bf16_bits_to_f32(vb1);
+        if (valid) v_cache[(cache_row + P) * HD + kWave + lane] = (uint16_t)vb1;
       }
     }
-    float d[U];
+    wave_lds_sync();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[e] = s_q[d0 + e];
+    if (wave == 0) {
+      float dd = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dd = fmaf(qf[e], s_kv[d0 + e], dd);
+      dd = group_sum<LPR>(dd);
+      m_run = dd * scale;
+      l_run = rw == 0 ? 1.f : 0.f;  // exp(s_P - m_run)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = rw == 0 ? s_kv[HD + d0 + e] : 0.f;
+    }
+  };
+
+  // 2-4. Per wavefront, in registers: scores of its rows, their maximum, exponentials and the sum of p * v, over
+  // NP passes starting at row t0 with their keys and values in kv, vv (a larger maximum rescales what came before).
+  auto passes = [&](const int t0, auto np, const uint4 *kv, const uint4 *vv) {
+    constexpr int NP = decltype(np)::value;
+    float d[NP > 0 ? NP : 1];
     float gm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      d[u] = -INFINITY;
-      if (t0 + u * RPB > P) continue;
+    for (int u = 0; u < NP; ++u) {
       const int t = t0 + u * RPB + slot;
       float kf[8];
-      if (t < P) {
-        unpack8(kv[u], kf);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] = t == P ? s_k[sub * 8 + e] : 0.f;
-      }
+      unpack8(kv[u], kf);
       float dd = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dd = fmaf(qf[e], kf[e], dd);
       dd = group_sum<LPR>(dd);
-      if (t <= P) d[u] = dd * scale;
+      d[u] = t < P ? dd * scale : -INFINITY;
       gm = fmaxf(gm, d[u]);
     }
     gm = strided_max<LPR>(gm);               // over the wavefront's row groups
     const float m_new = fmaxf(m_run, gm);
-    if (m_new == -INFINITY) continue;        // wavefront-uniform: none of its rows so far
-    const float corr = expf(m_run - m_new);  // 0 for the first group with rows
+    if (m_new == -INFINITY) return;          // wavefront-uniform: none of its rows so far
+    const float corr = expf(m_run - m_new);  // 0 while the wavefront had no row
     l_run *= corr;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= corr;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (t0 + u * RPB > P) continue;
-      const int t = t0 + u * RPB + slot;
-      if (t > P) continue;
-      const float pt = expf(d[u] - m_new);
+    for (int u = 0; u < NP; ++u) {
+      const float pt = expf(d[u] - m_new);  // 0 for rows at or past P
       float vf[8];
-      if (t < P) {
-        unpack8(vpre[u], vf);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = s_v[sub * 8 + e];
-      }
+      unpack8(vv[u], vf);
       l_run += pt;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(pt, vf[e], acc[e]);
     }
     m_run = m_new;
+  };
+
+  // The first group in straight-line code for the number of passes that hold rows < P (each pass then waits only
+  // for its own rows, and passes without rows load nothing); later groups (caches longer than RPB * U rows) load
+  // their rows after it, in a second round trip.
+  const int np0 = (int)min((P + RPB - 1) / RPB, (int64_t)U);
+  with_count<U>(np0, [&](auto np) {
+    constexpr int NP = decltype(np)::value;
+    uint4 kv[NP > 0 ? NP : 1], vv[NP > 0 ? NP : 1];
+#pragma unroll
+    for (int u = 0; u < NP; ++u) kv[u] = krows.load((u * RPB + slot) * HD + d0);  // keys first: the scores and
+#pragma unroll                                                                   // the maximum need every one
+    for (int u = 0; u < NP; ++u) vv[u] = vrows.load((u * RPB + slot) * HD + d0);
+    // (every load is issued before the arithmetic: otherwise the scheduler may place the RoPE between them, and
+    // its waits for q, k, v would hold back the remaining cache rows)
+    __builtin_amdgcn_sched_barrier(0);
+    rope();
+    passes(0, np, kv, vv);
+  });
+  for (int t0 = RPB * U; t0 < P; t0 += RPB * U) {
+    uint4 kv[U], vv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) kv[u] = krows.load((t0 + u * RPB + slot) * HD + d0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vv[u] = vrows.load((t0 + u * RPB + slot) * HD + d0);
+    passes(t0, IntC<U>{}, kv, vv);
   }
   // the wavefront's row groups summed (lane % LPR keeps the dims; the LPR lanes of a row group hold the same p)
   l_run = strided_sum<LPR>(l_run);
@@ -305,12 +364,11 @@ __global__ void __launch_bounds__(kAttnThreads)
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kAttnWaves; ++w) y = fmaf(s_red[w * HD + i], fw[w], y);
-      o[i] = (uint16_t)bf16_bits_rtne(y * inv);
+      o[i] = valid ? (uint16_t)bf16_bits_rtne(y * inv) : (uint16_t)0x7FC0;  // (bf16 NaN)
     }
   } else {
     // 5. parts[b, h, n] = sum_d bf16(y_d) wo[n, h * HD + d]: LPR lanes per wo row, 8 columns each, reduced with
-    // lane shuffles.  y goes through LDS (s_q is free: q has been in registers since step 2).
-    float *s_y = s_q;
+    // lane shuffles.  y goes through LDS.
     for (int i = tid; i < HD; i += kAttnThreads) {
       float y = 0.f;
 #pragma unroll
@@ -340,7 +398,7 @@ __global__ void __launch_bounds__(kAttnThreads)
         for (int e = 0; e < 8; ++e) d = fmaf(yv[e], wf[e], d);
         d = group_sum<LPR>(d);
         const int n = base + wr0 + i * RPP;
-        if (wc == 0 && n < n_out) po[n] = d;
+        if (wc == 0 && n < n_out) po[n] = valid ? d : __builtin_nanf("");
       }
     }
   }
@@ -366,7 +424,7 @@ struct AttnArgs {
 template <int HD, int NT, bool PROJ>
 int launch_attention_nt(const AttnArgs &a, hipStream_t stream) {
   const size_t shmem = sizeof(float) * (3 * HD + (NT / kWave) * HD + 2 * (NT / kWave));
-  const dim3 grid((unsigned)(a.B * a.H));
+  const dim3 grid((unsigned)a.H, (unsigned)a.B);
   if (a.rope_f32)
     hipLaunchKernelGGL((decode_attention_kernel<true, HD, NT, PROJ>), grid, dim3(NT), shmem, stream,
                        (const uint16_t *)a.qkv, a.qkv_stride, a.cos, a.sin, a.rope_len, a.pos, (uint16_t *)a.k_cache,
@@ -410,8 +468,14 @@ int check_attention(const void *qkv, int64_t qkv_row_stride, const void *rope_co
     return fail(SMLM_EINVAL, "smlm_decode_attention: rope tables must be SMLM_F32 or SMLM_BF16");
   if (B < 0 || H < 1 || max_len < 1 || rope_len < 1 || B * (int64_t)H > 0x7FFFFFFFLL)
     return fail(SMLM_EINVAL, "smlm_decode_attention: bad shape B=%lld H=%d max_len=%d", (long long)B, H, max_len);
-  if ((((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache) % 16) || qkv_row_stride % 8)
-    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv and caches must be 16-byte aligned");
+  if (((int64_t)max_len + 1024) * 128 * 2 > 0x7FFFFFFFLL)  // a (sequence, head)'s rows: 32-bit byte offsets
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: max_len %d too long", max_len);
+  if (B > 65535 || H > 65535)  // the grid is (H, B)
+    return fail(SMLM_EUNSUPPORTED, "smlm_decode_attention: B=%lld sequences or H=%d heads above 65535",
+                (long long)B, H);
+  if ((((uintptr_t)qkv | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)rope_cos | (uintptr_t)rope_sin) % 16) ||
+      qkv_row_stride % 8)
+    return fail(SMLM_EINVAL, "smlm_decode_attention: qkv, caches and rope tables must be 16-byte aligned");
   return SMLM_OK;
 }
 
