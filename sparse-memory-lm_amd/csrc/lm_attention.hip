@@ -25,13 +25,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kFaBM = 128;  // queries per workgroup
 constexpr int kFaBN = 64;   // keys per tile
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float floatx2 __attribute__((ext_vector_type(2)));
 
-// two fp32 -> packed bf16, round to nearest even, in one v_cvt_pk_bf16_f32 (values here are finite)
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
-}
 
 __device__ __forceinline__ float xor_lane_f(float v, int j) {
   const uint32_t u = __float_as_uint(v);

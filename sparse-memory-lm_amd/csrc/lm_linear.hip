@@ -47,7 +47,7 @@ constexpr int kArgTiles = 2;      // 16-column tiles per wavefront with the ARGM
 constexpr int kArgCols = kLinWaves * kArgTiles * 16;   // 128 columns per workgroup
 constexpr uint16_t kBf16NaN = 0x7FC0;
 
-__device__ __forceinline__ float silu_bf16(float a) { return round_bf16(a / (1.0f + expf(-a))); }
+__device__ __forceinline__ float silu_bf16(float a) { return round_bf16_hw(a / (1.0f + expf(-a))); }
 
 __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
@@ -61,7 +61,7 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
 __device__ __forceinline__ uint4 pack8(const float *f) {
   uint32_t u[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) u[e] = bf16_bits_rtne(f[2 * e]) | (bf16_bits_rtne(f[2 * e + 1]) << 16);
+  for (int e = 0; e < 4; ++e) u[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
   return uint4{u[0], u[1], u[2], u[3]};
 }
 
@@ -392,14 +392,13 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
     for (int mt = 0; mt < MTB; ++mt) {
       const int tok = mt * 16 + r;
       if (mt >= MT || tok >= nrows) continue;
-      uint32_t o[4];
+      float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float v = round_bf16(acc[0][mt][e] + bias[e]);
-        if (affine) v = round_bf16(fmaf(v, sc[e], sh[e]));
-        o[e] = bf16_bits_rtne(v);
+        v[e] = acc[0][mt][e] + bias[e];
+        if (affine) v[e] = fmaf(round_bf16_hw(v[e]), sc[e], sh[e]);
       }
-      *(uint2 *)(dst + (m0 + tok) * stride) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+      *(uint2 *)(dst + (m0 + tok) * stride) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }
   } else if constexpr (EPI == SMLM_LIN_SWIGLU) {
     if (c >= cols) return;
@@ -407,11 +406,11 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
     for (int mt = 0; mt < MTB; ++mt) {
       const int tok = mt * 16 + r;
       if (mt >= MT || tok >= nrows) continue;
-      uint32_t o[4];
+      float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = bf16_bits_rtne(silu_bf16(round_bf16(acc[0][mt][e])) * round_bf16(acc[1][mt][e]));
-      *(uint2 *)((uint16_t *)a.out + (m0 + tok) * a.out_stride + c) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+      for (int e = 0; e < 4; ++e) o[e] = silu_bf16(round_bf16_hw(acc[0][mt][e])) * round_bf16_hw(acc[1][mt][e]);
+      *(uint2 *)((uint16_t *)a.out + (m0 + tok) * a.out_stride + c) = uint2{pack_bf16x2(o[0], o[1]),
+                                                                            pack_bf16x2(o[2], o[3])};
     }
   } else {  // ARGMAX
     // 32-bit keys inside the workgroup (order16(bf16 logit) << 16 | 0xFFFF - column in the block), maxima over the
@@ -428,7 +427,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
         for (int e = 0; e < 4; ++e) {
           const int local = wave * kArgTiles * 16 + 4 * g + t * 16 + e;   // column - cb * kArgCols
           if (c + t * 16 + e >= cols) continue;
-          const uint32_t key = (order16(bf16_bits_rtne(acc[t][mt][e])) << 16) | (0xFFFFu - (uint32_t)local);
+          const uint32_t key = (order16(pack_bf16x2(0.f, acc[t][mt][e]) >> 16) << 16) | (0xFFFFu - (uint32_t)local);
           best = key > best ? key : best;
         }
       auto p16 = __builtin_amdgcn_permlane16_swap(best, best, false, false);

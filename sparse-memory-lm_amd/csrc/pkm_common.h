@@ -29,6 +29,16 @@ __device__ __forceinline__ uint32_t bf16_bits_rtne(float x) {
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_bits_to_f32(bf16_bits_rtne(x)); }
 
+// Two fp32 values as packed bf16 bits (a in bits 0-15), round to nearest even, in one v_cvt_pk_bf16_f32: the same
+// bits as bf16_bits_rtne for every finite value and infinity (a NaN becomes a quiet NaN).  For arithmetic whose
+// values are finite (the LM's activations); the selection keeps the integer definition above.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+__device__ __forceinline__ float round_bf16_hw(float x) { return __uint_as_float(pack_bf16x2(0.f, x) & 0xFFFF0000u); }
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 // fp32 -> fp16 bit pattern, round to nearest even (v_cvt_f16_f32)
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }

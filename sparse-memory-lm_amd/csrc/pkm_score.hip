@@ -306,13 +306,6 @@ __global__ void __launch_bounds__(256)
 constexpr int kStreamKeys = 64;     // sub-keys per streamed block
 constexpr int kStreamWaveTok = 64;  // tokens per wavefront
 
-// Two fp32 values as packed bf16, rounded to nearest even (one v_cvt_pk_bf16_f32 on gfx950; for finite values the
-// same bits as bf16_bits_rtne).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 template <int KSTEPS, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64)
