@@ -17,7 +17,7 @@
 //             ARGMAX         per token, the largest key (bf16 logit, then lowest column) over the block's 128
 //                            columns, to partial[m, block] (lm_head + greedy argmax; no logits are written)
 //
-// Workgroup = 4 wavefronts, a token group of 16 or 64 rows x one column block.  STORE / SWIGLU: one 16-column tile
+// Workgroup = 4 wavefronts, a token group of 16 or 32 rows x one column block.  STORE / SWIGLU: one 16-column tile
 // per workgroup (SWIGLU: the 16 a columns and their 16 b columns), the 4 wavefronts split the contraction and their
 // partial sums are added in a fixed order through LDS.  ARGMAX: each wavefront owns 2 tiles (32 columns) over the
 // whole contraction.  Every result is deterministic.  With several token groups the grid is 1-D and the groups of
@@ -41,7 +41,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLinThreads = 256;
 constexpr int kLinWaves = kLinThreads / kWave;
-constexpr int kMaxTiles = 4;      // token tiles of 16 per workgroup, at most
+constexpr int kMaxTiles = 2;      // token tiles of 16 per workgroup, at most (ARGMAX over more than 16 rows)
 constexpr int kXcds = 8;          // workgroup id % 8 selects the XCD
 constexpr int kArgTiles = 2;      // 16-column tiles per wavefront with the ARGMAX epilogue
 constexpr int kArgCols = kLinWaves * kArgTiles * 16;   // 128 columns per workgroup
@@ -517,7 +517,7 @@ void launch_linear_mtb(const smlm_linear_args &a, const LinGrid &lg, hipStream_t
 template <int PRO, int EPI, int MAXS>
 void launch_linear_cpq(const smlm_linear_args &a, const LinGrid &lg, hipStream_t stream) {
   if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);  // mtb is 1
-  else if (lg.mtb == 1) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);
+  else if (EPI != SMLM_LIN_ARGMAX || lg.mtb == 1) launch_linear_mtb<PRO, EPI, MAXS, 1>(a, lg, stream);
   else launch_linear_mtb<PRO, EPI, MAXS, kMaxTiles>(a, lg, stream);
 }
 
@@ -614,7 +614,8 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   }
   if (A.M == 0) return SMLM_OK;
   // 16-token groups (more workgroups, shorter per-workgroup chains: decode is latency-bound), except the ARGMAX
-  // epilogue over more than 16 rows, whose 128-column blocks already fill the chip
+  // epilogue over more than 16 rows: 32-row groups (each workgroup normalises its rows in the prologue, so 64-row
+  // groups measured 1% slower per batch-64 decode step; 16-row groups re-read the 24.6 MB of lm_head weights 4x)
   LinGrid lg;
   lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
   const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : lg.mtb * 16;
