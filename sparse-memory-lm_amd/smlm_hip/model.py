@@ -22,7 +22,8 @@ from .pkm import ProductKeyMemory, inference_tables
 
 @dataclass
 class ModelConfig:
-    """Fields and defaults of smlm/model.py:13-60 (mem_impl defaults to "hip")."""
+    """Fields and defaults of smlm/model.py:13-60 (mem_impl defaults to "hip"; a reference config's "torch" or
+    "triton" runs the same kernels)."""
     vocab_size: int = 50304
     d_model: int = 384
     n_layers: int = 12

@@ -5,8 +5,8 @@ graph switch), whose lookup runs on the gfx950 kernels of smlm_hip.kernels:
     query_proj -> BatchNorm (fp32, eval statistics) -> pk_scores (MFMA) -> pk_select -> softmax
     -> bag_infer (value gather, swilu epilogue, bf16 out) -> value_proj
 
-impl="hip" is the only implementation here; the reference's "torch" and "triton" implementations stay in the
-reference package.
+impl: "hip", or the reference's names "torch" and "triton" (smlm/pkm.py:48), which a reference config carries;
+every name runs the same kernels (there is one implementation here) and is kept in self.impl for the config.
 
 A forward that autograd records (training) takes the reference's differentiable path with the HIP kernels where the
 reference uses its Triton ones (smlm/pkm.py:186-228): torch query projection and BatchNorm, sub-key scores by
@@ -21,7 +21,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from . import kernels
-from .sparse_values import row_sparse_embedding_bag
+from .sparse_values import check_impl, row_sparse_embedding_bag
 
 
 def _pow2(n):
@@ -45,7 +45,7 @@ def inference_tables(values):
 
 
 class ProductKeyMemory(nn.Module):
-    """Same constructor as smlm/pkm.py:33-92 (impl defaults to "hip")."""
+    """Same constructor as smlm/pkm.py:33-92 (impl defaults to "hip"; "torch" and "triton" are accepted)."""
 
     def __init__(self, d_in, d_out, n_keys=512, heads=4, knn=32, k_dim=256, v_dim=-1,
                  query_norm="batchnorm", swilu=True, value_impl="embedding_bag",
@@ -54,13 +54,11 @@ class ProductKeyMemory(nn.Module):
         super().__init__()
         if k_dim % 2 or knn > n_keys:
             raise ValueError(f"k_dim must be even and knn <= n_keys, got k_dim={k_dim}, knn={knn}, n_keys={n_keys}")
-        if impl != "hip":
-            raise ValueError(f"smlm_hip runs mem_impl='hip' only, got {impl!r}; the 'torch' and 'triton' "
-                             "implementations are the reference package's")
+        check_impl(impl, "ProductKeyMemory")
         if not (_pow2(n_keys) and n_keys <= 65536 and _pow2(knn) and knn <= 64):
             # the selection kernel packs sub-key indices into 16 bits and keeps one selected entry per lane
-            raise ValueError(f"mem_impl='hip' needs n_keys and knn to be powers of two, n_keys <= 65536 and "
-                             f"knn <= 64, got n_keys={n_keys}, knn={knn}.")
+            raise ValueError(f"the HIP kernels need n_keys and knn to be powers of two, n_keys <= 65536 and "
+                             f"knn <= 64, got n_keys={n_keys}, knn={knn} (mem_impl={impl!r}).")
         if value_grad not in ("dense", "row_sparse"):
             raise ValueError(value_grad)
         self.d_in, self.d_out = d_in, d_out

@@ -73,14 +73,28 @@ def test_status_becomes_python_exception():
 
 def test_rejects_unsupported_shapes():
     """As the reference's Triton path: non-power-of-two n_keys or knn fail at construction with a clear
-    message (and, here, knn > 64 and the other implementations)."""
+    message (and, here, knn > 64, whatever impl name is given)."""
     for n_keys, knn in ((24, 4), (16, 5), (256, 128)):
-        with pytest.raises(ValueError, match="powers of two"):
-            ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16)
-    with pytest.raises(ValueError, match="mem_impl='hip' only"):
-        ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16, impl="torch")
+        for impl in ("hip", "torch", "triton"):
+            with pytest.raises(ValueError, match="powers of two"):
+                ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16, impl=impl)
     m = ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16)
     assert m.keys.shape == (4, 2, 16, 8) and m.values.weight.shape == (256, 32)
+
+
+def test_impl_names_of_reference_configs():
+    """A reference config's mem_impl ("torch", its default, or "triton") constructs the same module, kept in
+    self.impl; any other name fails at construction."""
+    a = ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16)
+    for impl in ("torch", "triton"):
+        m = ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16, impl=impl)
+        assert m.impl == impl and set(m.state_dict()) == set(a.state_dict())
+    with pytest.raises(ValueError, match="impl must be one of"):
+        ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16, impl="cuda")
+    from smlm_hip.model import ModelConfig, Transformer
+    cfg = ModelConfig(vocab_size=64, d_model=32, n_layers=2, n_heads=2, ffn_hidden=64, max_seq_len=16,
+                      mem_layers=[1], mem_n_keys=16, mem_heads=2, mem_knn=4, mem_k_dim=16, mem_impl="torch")
+    assert Transformer(cfg).layers[1].ffn.impl == "torch"
 
 
 def test_state_dict_keys_are_the_reference_names():

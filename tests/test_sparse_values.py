@@ -40,9 +40,12 @@ def test_states_require_contiguous_tables(mode):
         LazyRowAdam([table], lr=0.01, state_dtype=mode)
 
 
-def test_only_the_hip_implementation():
-    with pytest.raises(ValueError, match="hip"):
-        LazyRowAdam([torch.nn.Parameter(torch.zeros(4, 7))], lr=0.01, impl="torch")
+def test_impl_names():
+    """The reference's impl names construct the same optimizer; other names fail."""
+    for impl in ("hip", "triton", "torch"):
+        assert LazyRowAdam([torch.nn.Parameter(torch.zeros(4, 7))], lr=0.01, impl=impl).impl == impl
+    with pytest.raises(ValueError, match="impl must be one of"):
+        LazyRowAdam([torch.nn.Parameter(torch.zeros(4, 7))], lr=0.01, impl="cuda")
 
 
 def test_row_store_follows_its_table_and_state_dict_checks():
