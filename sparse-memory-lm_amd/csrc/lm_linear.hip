@@ -125,21 +125,28 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
   }
 }
 
-// RMSNORM_PARTS: delta rows from fp32 parts, a whole wavefront per row (lane = one 8-column chunk, K <= 512): the
-// token groups of this prologue are kPartsRows = 4 rows, row `wave` of the group for wavefront `wave`.  load_parts
-// issues the loads of the row (all its parts at once, before the weight fragments); sum_parts adds them in part
-// order and writes the bf16 delta row to LDS (the prologue's row buffer, where norm_activations reads it back).
+// RMSNORM_PARTS: delta rows from fp32 parts, one row per wavefront (token groups of kPartsRows = 4 rows, row `wave`
+// of the group for wavefront `wave`).  load_parts issues the row's loads before the weight fragments: its parts with
+// a lane per 8-column chunk (K <= 512), then its x row and the norm weights in the RMSNORM layout (lane `sub` of each
+// 16-lane quarter: chunks sub, sub + 16, ...).  parts_norm adds the parts in part order, rounds once to bf16, moves
+// the chunks to the RMSNORM layout with lane swaps (chunk sub + 16 j is lane sub ^ 16 j) and finishes the row with
+// the arithmetic of norm_activations in the same lanes and order, so the result is the RMSNORM prologue's on that
+// bf16 delta bit for bit; every quarter computes the row, the first stores it.  No LDS round trip and no barrier
+// between the sum and the norm, and the group's rows are normalised by four wavefronts at once.
 constexpr int kMaxParts = 8;
 constexpr int kPartsRows = kLinWaves;
 
+template <int CPQ>
 struct PartsIn {
-  uint4 pv[kMaxParts][2];
+  uint4 pv[kMaxParts][2], xv[CPQ], gv[CPQ];
 };
 
-__device__ __forceinline__ void load_parts(const smlm_linear_args &a, int64_t m0, int nrows, PartsIn &in) {
-  const int CH = a.K / 8, lane = lane_id(), wave = threadIdx.x / kWave;
+template <int CPQ>
+__device__ __forceinline__ void load_parts(const smlm_linear_args &a, int64_t m0, int nrows, PartsIn<CPQ> &in) {
+  const int CH = a.K / 8, lane = lane_id(), wave = threadIdx.x / kWave, sub = lane & 15;
   if (wave >= nrows) return;  // wavefront-uniform
-  const float *src = (const float *)a.delta + (m0 + wave) * (int64_t)a.delta_parts * a.K + min(lane, CH - 1) * 8;
+  const int64_t m = m0 + wave;
+  const float *src = (const float *)a.delta + m * (int64_t)a.delta_parts * a.K + min(lane, CH - 1) * 8;
 #pragma unroll
   for (int q = 0; q < kMaxParts; ++q) {
     if (q >= a.delta_parts) break;  // uniform
@@ -147,11 +154,39 @@ __device__ __forceinline__ void load_parts(const smlm_linear_args &a, int64_t m0
     in.pv[q][0] = *(const uint4 *)pq;
     in.pv[q][1] = *(const uint4 *)(pq + 4);
   }
+  const uint16_t *xs = (const uint16_t *)a.x + m * a.x_stride, *nw = (const uint16_t *)a.norm_w;
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    const int c = min(sub + 16 * j, CH - 1);
+    in.xv[j] = *(const uint4 *)(xs + c * 8);
+    in.gv[j] = *(const uint4 *)(nw + c * 8);
+  }
 }
 
-__device__ __forceinline__ void sum_parts(const smlm_linear_args &a, int nrows, uint16_t *sH, int KP, PartsIn &in) {
-  const int CH = a.K / 8, lane = lane_id(), wave = threadIdx.x / kWave;
-  if (wave >= nrows) return;  // wavefront-uniform
+template <int J>
+__device__ __forceinline__ uint4 xor_lane4(uint4 v) {
+  return uint4{xor_lane<J>(v.x), xor_lane<J>(v.y), xor_lane<J>(v.z), xor_lane<J>(v.w)};
+}
+
+template <int CPQ>
+__device__ __forceinline__ void parts_norm(const smlm_linear_args &a, int64_t m0, int nrows, uint16_t *sH, int KP,
+                                           bool first_block, PartsIn<CPQ> &in) {
+  static_assert(CPQ <= 4, "parts prologue: K <= 512");
+  const int K = a.K, CH = K / 8, lane = lane_id(), wave = threadIdx.x / kWave;
+  const int quarter = lane >> 4, sub = lane & 15;
+  if (quarter > 0) {  // rows kPartsRows..15 of the 16-row tile are zero: three per wavefront
+    uint16_t *z = sH + (kPartsRows + wave * 3 + quarter - 1) * KP;
+#pragma unroll
+    for (int j = 0; j < CPQ; ++j)
+      if (sub + 16 * j < CH) *(uint4 *)(z + (sub + 16 * j) * 8) = uint4{0u, 0u, 0u, 0u};
+  }
+  uint16_t *dst = sH + wave * KP;
+  if (wave >= nrows) {  // wavefront-uniform: a row past the end is zero
+#pragma unroll
+    for (int j = 0; j < CPQ; ++j)
+      if (quarter == 0 && sub + 16 * j < CH) *(uint4 *)(dst + (sub + 16 * j) * 8) = uint4{0u, 0u, 0u, 0u};
+    return;
+  }
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -163,7 +198,42 @@ __device__ __forceinline__ void sum_parts(const smlm_linear_args &a, int nrows, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += __uint_as_float(w[e]);
   }
-  if (lane < CH) *(uint4 *)(sH + wave * KP + lane * 8) = pack8(acc);
+  const uint4 dl = pack8(acc);  // this lane's chunk of the bf16 delta row
+  uint4 dv[CPQ];
+  dv[0] = dl;
+  if constexpr (CPQ > 1) dv[1] = xor_lane4<16>(dl);
+  if constexpr (CPQ > 2) dv[2] = xor_lane4<32>(dl);
+  if constexpr (CPQ > 3) dv[3] = xor_lane4<16>(xor_lane4<32>(dl));
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    float xf[8], df[8];
+    unpack8(in.xv[j], xf);
+    unpack8(dv[j], df);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xf[e] += df[e];
+    in.xv[j] = pack8(xf);                           // the residual stream is bf16: round the sum
+    unpack8(in.xv[j], xf);
+    if (sub + 16 * j < CH) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xf[e], xf[e], ss);
+    }
+  }
+  ss = row16_sum(ss);
+  const float rstd = rsqrtf(ss / (float)K + a.eps);
+  const bool write_x = a.x_out != nullptr && first_block;
+#pragma unroll
+  for (int j = 0; j < CPQ; ++j) {
+    const int c = sub + 16 * j;
+    if (quarter != 0 || c >= CH) continue;
+    if (write_x) *(uint4 *)((uint16_t *)a.x_out + (m0 + wave) * (int64_t)K + c * 8) = in.xv[j];
+    float xf[8], gf[8];
+    unpack8(in.xv[j], xf);
+    unpack8(in.gv[j], gf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xf[e] = xf[e] * rstd * gf[e];
+    *(uint4 *)(dst + c * 8) = pack8(xf);
+  }
 }
 
 template <int PRO, int CPQ, int MTB>
@@ -183,18 +253,13 @@ __device__ __forceinline__ void norm_activations(const smlm_linear_args &a, int6
     if (p >= passes) continue;
     const int rr = p * 16 + wave * 4 + quarter;
     const bool live = rr < nrows;
-    if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) {  // the delta row sum_parts left in this row of sH
-#pragma unroll
-      for (int j = 0; j < CPQ; ++j)
-        dv[p][j] = live ? *(const uint4 *)(sH + rr * KP + min(sub + 16 * j, CH - 1) * 8) : uint4{0u, 0u, 0u, 0u};
-    }
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < CPQ; ++j) {
       float xf[8];
       unpack8(xv[p][j], xf);
-      if constexpr (PRO == SMLM_LIN_RMSNORM || PRO == SMLM_LIN_RMSNORM_PARTS) {
-        if (PRO == SMLM_LIN_RMSNORM_PARTS || a.delta) {
+      if constexpr (PRO == SMLM_LIN_RMSNORM) {
+        if (a.delta) {
           float df[8];
           unpack8(dv[p][j], df);
 #pragma unroll
@@ -270,9 +335,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   // 1. the prologue's loads, then the weight fragments (rows past N and steps past the slice re-read valid memory;
   // their products are unused): the prologue's arithmetic then overlaps the weights' arrival
   ActIn<CPQ, PRO == SMLM_LIN_PLAIN ? 1 : MTB> act;
-  if constexpr (PRO != SMLM_LIN_PLAIN) load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, act);
-  PartsIn parts_in;
-  if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) load_parts(a, m0, nrows, parts_in);
+  if constexpr (PRO != SMLM_LIN_PLAIN && PRO != SMLM_LIN_RMSNORM_PARTS)
+    load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, act);
+  PartsIn<CPQ> parts_in;
+  if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) load_parts<CPQ>(a, m0, nrows, parts_in);
   uint4 areg[NT][MAXS];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -301,11 +367,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       }
     }
   } else {
-    if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) {
-      sum_parts(a, nrows, sH, KP, parts_in);
-      __syncthreads();  // the delta rows in LDS (the weight fragments keep arriving meanwhile)
-    }
-    norm_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0, act);
+    if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) parts_norm<CPQ>(a, m0, nrows, sH, KP, cb == 0, parts_in);
+    else norm_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, sH, KP, cb == 0, act);
     __syncthreads();
   }
 
