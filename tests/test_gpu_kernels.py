@@ -359,11 +359,15 @@ def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
                                                     (1, 6, 64, 394, 393, "f32"), (3, 4, 32, 100, 57, "f32"),
                                                     (2, 2, 16, 40, 1, "bf16"), (2, 3, 128, 300, 299, "bf16"),
                                                     (5, 6, 64, 600, 511, "f32"), (20, 6, 64, 300, 250, "bf16"),
-                                                    (1, 6, 64, 1100, 1050, "f32")])
+                                                    (1, 6, 64, 1100, 1050, "f32"), (64, 6, 64, 600, 64, "bf16"),
+                                                    (64, 6, 64, 600, 512, "bf16"), (64, 6, 64, 600, 513, "f32"),
+                                                    (2, 6, 64, 800, 768, "bf16"), (2, 6, 64, 800, 769, "f32"),
+                                                    (100, 6, 64, 300, 256, "bf16"), (100, 6, 64, 300, 257, "bf16")])
 def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
     """1024 / 512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the
     last slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second
-    round trip)."""
+    round trip); positions on and just past a pass or a group boundary of each thread count (512 threads: 64 rows a
+    pass, 512 a group; 1024: 128 and 768; 256: 32 and 256)."""
     note(f"decode attention B={B} H={H} hd={hd} max_len={max_len} P={P}")
     g = torch.Generator().manual_seed(B * 1000 + P)
     C = H * hd
