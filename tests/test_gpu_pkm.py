@@ -75,6 +75,42 @@ def test_config0_layer_forward_fp32():
     assert len(rows) >= 0.9 * N
 
 
+@torch.no_grad()
+def test_learned_score_scale_forward_fp32():
+    """score_scale="learned" (smlm/pkm.py:60-62, 195-208): a positive per-head scale multiplies the selected scores
+    before the softmax.  The selection is the kernels' (bit-exact against the oracle on their own scores), the
+    weights are softmax(scale_h * scores) and the output is the value bag on them."""
+    note("learned score scale forward")
+    g = torch.Generator().manual_seed(3)
+    N, d, H, kd, NK, knn = 256, 64, 3, 64, 128, 16
+    mem = ProductKeyMemory(d, d, n_keys=NK, heads=H, knn=knn, k_dim=kd, query_norm="none", swilu=False,
+                           score_scale="learned", score_scale_init=2.0)
+    assert torch.allclose(mem.log_score_scale, torch.full((H,), float(np.log(2.0))))
+    mem.query_proj.weight.copy_(torch.randn(H * kd, d, generator=g) * 0.1)
+    mem.keys.copy_(torch.randn(H, 2, NK, kd // 2, generator=g) / 4)
+    mem.values.weight.copy_(torch.randn(NK * NK, d, generator=g) * 0.02)
+    scale = np.array([0.25, 1.0, 6.0])
+    mem.log_score_scale.copy_(torch.from_numpy(np.log(scale)))
+    mem = mem.to(DEV)
+    mem.record = True
+    x = torch.randn(N, d, generator=g).to(DEV)
+    out = mem(x)
+    q = mem.query_proj(x).view(N, H, kd)
+    s1, s2 = K.pk_scores(q, mem.keys.detach())
+    sc, idx, _ = O.pk_select(s1.cpu().numpy(), s2.cpu().numpy(), knn)
+    assert np.array_equal(mem.last_indices.cpu().numpy(), idx)
+    z = sc.astype(np.float64) * scale.reshape(1, H, 1)
+    w = np.exp(z - z.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    np.testing.assert_allclose(mem.last_weights.cpu().numpy(), w, rtol=0, atol=1e-6)
+    # the sharpest head's weights differ from the unscaled softmax: the scale is applied, not dropped
+    w1 = np.exp(sc - sc.max(-1, keepdims=True))
+    w1 /= w1.sum(-1, keepdims=True)
+    assert np.abs(w[:, 2] - w1[:, 2]).max() > 1e-2
+    ref = O.bag(idx.reshape(N, -1), w.reshape(N, -1).astype(np.float32), mem.values.weight.cpu().numpy(), "f32")
+    close(out.cpu().numpy(), ref)
+
+
 def _bf16_layer(N, seed, n_keys=1024, knn=32, d=384):
     g = torch.Generator().manual_seed(seed)
     mem = ProductKeyMemory(d, d, n_keys=n_keys, heads=4, knn=knn, k_dim=512)

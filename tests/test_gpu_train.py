@@ -206,6 +206,8 @@ def _ref_grads(mem, x, G, idx):
     s2 = torch.einsum("nhd,hkd->nhk", q[..., kd // 2:], sd["keys"][:, 1])
     i = idx.cpu()
     scores = s1.gather(-1, i // NK) + s2.gather(-1, i % NK)
+    if "log_score_scale" in sd:          # score_scale="learned" (smlm/pkm.py:205-208)
+        scores = scores * sd["log_score_scale"].exp().view(1, H, 1)
     w = torch.softmax(scores, -1)
     out = torch.nn.functional.embedding_bag(i.view(N, -1), sd["values.weight"], per_sample_weights=w.view(N, -1),
                                             mode="sum")
@@ -213,19 +215,24 @@ def _ref_grads(mem, x, G, idx):
     return {k: v.grad for k, v in sd.items()}
 
 
-@pytest.mark.parametrize("value_grad", ["row_sparse", "dense"])
-def test_layer_training_step_matches_fp64_autograd(value_grad):
+@pytest.mark.parametrize("value_grad,score_scale", [("row_sparse", "none"), ("dense", "none"),
+                                                     ("row_sparse", "learned")])
+def test_layer_training_step_matches_fp64_autograd(value_grad, score_scale):
     """A training forward + backward of ProductKeyMemory (fp32, no BatchNorm, no swilu) on the kernels: query /
     key gradients through the selection backward and the einsum, value gradients in the row store (row_sparse) or
     as a dense .grad, against fp64 autograd on the CPU given the same selection; then one LazyRowAdam step equals
-    the oracle on the accumulated rows."""
+    the oracle on the accumulated rows.  With score_scale="learned" the per-head scale (0.5 and 3 here) multiplies
+    the selected scores before the softmax and receives its own gradient."""
     from smlm_hip.pkm import ProductKeyMemory
     from smlm_hip.sparse_values import LazyRowAdam, row_store
-    note(f"layer training step value_grad={value_grad}")
+    note(f"layer training step value_grad={value_grad} score_scale={score_scale}")
     torch.manual_seed(0)
     N, d, H, kd, NK, knn = 48, 32, 2, 32, 64, 8
     mem = ProductKeyMemory(d, d, n_keys=NK, heads=H, knn=knn, k_dim=kd, query_norm="none", swilu=False,
-                           value_grad=value_grad).to(DEV).train()
+                           value_grad=value_grad, score_scale=score_scale).to(DEV).train()
+    if score_scale == "learned":
+        with torch.no_grad():
+            mem.log_score_scale.copy_(torch.tensor([0.5, 3.0]).log())
     g = torch.Generator().manual_seed(1)
     x = torch.randn(N, d, generator=g).to(DEV)
     G = torch.randn(N, d, generator=g)
@@ -234,7 +241,8 @@ def test_layer_training_step_matches_fp64_autograd(value_grad):
     (out * G.to(DEV)).sum().backward()
     idx = mem.last_indices
     ref = _ref_grads(mem, x, G, idx)
-    for name in ("query_proj.weight", "query_proj.bias", "keys"):
+    names = ("query_proj.weight", "query_proj.bias", "keys") + (("log_score_scale",) if score_scale == "learned" else ())
+    for name in names:
         got = dict(mem.named_parameters())[name].grad.double().cpu()
         scale = ref[name].abs().max()
         assert float((got - ref[name]).abs().max()) <= 1e-5 * float(scale), name
