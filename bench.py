@@ -99,9 +99,7 @@ def time_generations(model, B, reps, warmup, dev, prompt_len=128, new_tokens=GEN
         dec.hist[:, :P] = prompt
 
         def start():
-            dec.hist[:, P] = first
-            dec.tok.copy_(first.view(B, 1))
-            dec.pos.fill_(P)
+            dec.start(first, P)
 
         for _ in range(warmup):
             start()
@@ -369,15 +367,11 @@ def time_decode_eager(model, B, steps, dev, seed=1, prompt_len=128):
         dec = model._decoder(B, P + steps + 3, dev)
         logits = model(prompt, kv_caches=dec.caches, pos0=0)
         dec.hist[:, :P] = prompt
-        dec.hist[:, P] = logits[:, -1].argmax(-1)
-        dec.tok.copy_(dec.hist[:, P:P + 1])
-        dec.pos.fill_(P)
-        for _ in range(2):
-            dec._step()
+        dec.start(logits[:, -1].argmax(-1), P)
+        dec.steps(2)
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
-        for _ in range(steps):
-            dec._step()
+        dec.steps(steps)
         torch.cuda.synchronize(dev)
         dt = time.perf_counter() - t0
     return B * steps / dt, 1000.0 * dt / steps

@@ -254,6 +254,13 @@ int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *
  *                                    delta[m, q, :]) from fp32 (M, delta_parts, K) parts, summed in q order: the
  *                                    per-head output projections of smlm_decode_attention_proj (1 <= delta_parts
  *                                    <= 8; not with SMLM_LIN_ARGMAX)
+ *            SMLM_LIN_EMBED_ARGMAX   as SMLM_LIN_EMBED_RMSNORM with tok[m] = the column of the largest key of
+ *                                    tok_partial[m, 0..tok_blocks), the previous step's SMLM_LIN_ARGMAX partials
+ *                                    (the greedy choice of smlm/train.py:297-301 made at the start of the next
+ *                                    step, so no smlm_argmax_finish launch between steps); the workgroups of
+ *                                    column block 0 write it to tok_out[m] (if not NULL) and to hist[m, *pos] (if
+ *                                    hist is not NULL and 0 <= *pos < hist_len).  A row without keys (all 0) gets
+ *                                    the id 2^32 - 1, outside the embedding: a NaN row, as in SMLM_LIN_EMBED_RMSNORM
  *            with an RMSNorm prologue, xs is also written to x_out (if not NULL): the residual stream
  *   epilogue SMLM_LIN_STORE          v = bf16(acc + bias); on columns < n_affine v = bf16(v * scale + shift) (eval
  *                                    BatchNorm of the memory query); columns < n_split to out, the rest to out2
@@ -261,7 +268,10 @@ int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *
  *                                    (w13 followed by the SwiGLU activation, smlm/model.py:110-118)
  *            SMLM_LIN_ARGMAX         no logits are written: partial[m, b] = the largest (order16(bf16 logit) << 32 |
  *                                    ~column) over column block b of smlm_linear_argmax_blocks(N) blocks of 128;
- *                                    smlm_argmax_finish turns them into tokens (lm_head + greedy argmax)
+ *                                    smlm_argmax_finish or the next step's SMLM_LIN_EMBED_ARGMAX prologue turns
+ *                                    them into tokens (lm_head + greedy argmax); if pos_advance is not NULL, one
+ *                                    thread adds 1 to *pos_advance (the decode position; nothing else in the
+ *                                    launch reads it)
  * Shapes: W (N, K) bf16 row-major (nn.Linear.weight), K a multiple of 32, N a multiple of 16 (SWIGLU: 32);
  * RMSNorm prologues need K <= 480; x rows at x + m*x_stride; delta, x_out (M, K) dense; bias (N,) bf16;
  * scale/shift (n_affine,) fp32; out/out2 bf16 with row strides in elements.  All inputs 16-byte aligned, outputs
@@ -271,7 +281,8 @@ typedef enum smlm_linear_prologue {
   SMLM_LIN_PLAIN = 0,
   SMLM_LIN_RMSNORM = 1,
   SMLM_LIN_EMBED_RMSNORM = 2,
-  SMLM_LIN_RMSNORM_PARTS = 3
+  SMLM_LIN_RMSNORM_PARTS = 3,
+  SMLM_LIN_EMBED_ARGMAX = 4
 } smlm_linear_prologue;
 
 typedef enum smlm_linear_epilogue {
@@ -308,6 +319,15 @@ typedef struct smlm_linear_args {
   uint64_t *partial;        /* ARGMAX: (M, >= smlm_linear_argmax_blocks(N)) */
   int64_t partial_stride;
   int delta_parts;          /* RMSNORM_PARTS: number of fp32 parts of delta */
+  const uint64_t *tok_partial;  /* EMBED_ARGMAX: (M, >= tok_blocks) keys, even row stride, 16-byte aligned */
+  int64_t tok_partial_stride;
+  int tok_blocks;
+  int64_t *tok_out;         /* EMBED_ARGMAX: (M,) or NULL */
+  int64_t *hist;            /* EMBED_ARGMAX: (M, hist_len) rows at hist + m*hist_stride, or NULL */
+  int64_t hist_stride;
+  int64_t hist_len;
+  const int64_t *pos;       /* EMBED_ARGMAX with hist: the history slot */
+  int64_t *pos_advance;     /* ARGMAX: NULL, or the position to advance by one (M >= 1) */
 } smlm_linear_args;
 
 /* Number of 128-column blocks of the ARGMAX epilogue for N columns (the width partial needs). */

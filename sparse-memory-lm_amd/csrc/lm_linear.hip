@@ -6,6 +6,9 @@
 //             RMSNORM        xs = bf16(x + delta) (delta optional), h = bf16(xs * rsqrt(mean(xs^2) + eps) * g):
 //                            the residual add and the RMSNorm of the next sublayer
 //             EMBED_RMSNORM  xs = emb[tok[m]] (the token embedding), then as RMSNORM
+//             EMBED_ARGMAX   as EMBED_RMSNORM with tok[m] = the greedy choice from the previous step's ARGMAX
+//                            partial keys (each row reduced by the 16 lanes that gather its embedding); column
+//                            block 0 writes the tokens and their history slot: no separate argmax launch per step
 //             RMSNORM_PARTS  as RMSNORM with delta = bf16(sum_q parts[m, q, :]), fp32 parts summed in q order (the
 //                            per-head output projections the attention kernel wrote: wo costs no launch)
 //                            xs is written once to x_out (the residual stream), by the column block 0.
@@ -85,9 +88,37 @@ struct ActIn {
   bool bad[MTB];
 };
 
+// The greedy token of row m from ARGMAX partial keys (order16(bf16 logit) << 32 | ~column, 0 = no key): the column
+// of the row's largest key, found by the 16 lanes of a quarter wavefront (lane `sub` reads the 16-byte key pairs
+// sub, sub + 16, ..., all of a round's loads in flight, then a 4-step butterfly).  The same maximum over the same
+// keys as argmax_finish_kernel, so the same token.
+constexpr int kTokLoads = 8;   // key pairs per lane and round: 256 keys (32,768 columns) per round
+
+__device__ __forceinline__ int64_t row_argmax_token(const smlm_linear_args &a, int64_t m, int sub) {
+  const uint64_t *row = a.tok_partial + m * a.tok_partial_stride;
+  const int nb = a.tok_blocks, npairs = (nb + 1) / 2;
+  uint64_t best = 0;
+  for (int c0 = 0; c0 < npairs; c0 += 16 * kTokLoads) {
+    uint4 v[kTokLoads];
+#pragma unroll
+    for (int j = 0; j < kTokLoads; ++j) v[j] = *(const uint4 *)(row + 2 * min(c0 + sub + 16 * j, npairs - 1));
+#pragma unroll
+    for (int j = 0; j < kTokLoads; ++j) {
+      const int c = min(c0 + sub + 16 * j, npairs - 1);      // a clamped pair repeats a pair: same maximum
+      const uint64_t k0 = ((uint64_t)v[j].y << 32) | v[j].x;
+      const uint64_t k1 = 2 * c + 1 < nb ? ((uint64_t)v[j].w << 32) | v[j].z : 0;  // odd tail: the stride's pad
+      best = max(best, max(k0, k1));
+    }
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) best = max(best, (uint64_t)__shfl_xor((unsigned long long)best, o, 16));
+  return (int64_t)(0xFFFFFFFFu - (uint32_t)best);
+}
+
 template <int PRO, int CPQ, int MTB>
 __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
-                                                 ActIn<CPQ, MTB> &in) {
+                                                 bool first_block, ActIn<CPQ, MTB> &in) {
+  constexpr bool EMB = PRO == SMLM_LIN_EMBED_RMSNORM || PRO == SMLM_LIN_EMBED_ARGMAX;
   const int K = a.K, CH = K / 8;
   const int wave = threadIdx.x / kWave, lane = lane_id();
   const int quarter = lane >> 4, sub = lane & 15;
@@ -97,6 +128,9 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
   auto &dv = in.dv;
   auto &gv = in.gv;
   auto &bad = in.bad;
+  // EMBED_ARGMAX: column block 0 writes each row's token (and history slot *pos, read before anything else)
+  const bool writer = PRO == SMLM_LIN_EMBED_ARGMAX && first_block;
+  const int64_t hslot = writer && a.hist ? *a.pos : -1;
 #pragma unroll
   for (int j = 0; j < CPQ; ++j) gv[j] = *(const uint4 *)(nw + min(sub + 16 * j, CH - 1) * 8);
 #pragma unroll
@@ -106,8 +140,17 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
     const int rr = p * 16 + wave * 4 + quarter;
     const int64_t m = m0 + min(rr, nrows - 1);      // rows past the end re-read the last row (written as zero)
     const uint16_t *src;
-    if constexpr (PRO == SMLM_LIN_EMBED_RMSNORM) {
-      const int64_t t = a.tok[m];
+    if constexpr (EMB) {
+      int64_t t;
+      if constexpr (PRO == SMLM_LIN_EMBED_ARGMAX) {
+        t = row_argmax_token(a, m, sub);
+        if (writer && sub == 0 && rr < nrows) {
+          if (a.tok_out) a.tok_out[m] = t;
+          if (hslot >= 0 && hslot < a.hist_len) a.hist[m * a.hist_stride + hslot] = t;
+        }
+      } else {
+        t = a.tok[m];
+      }
       bad[p] = t < 0 || t >= a.emb_rows;
       src = (const uint16_t *)a.emb + (bad[p] ? 0 : t) * (int64_t)K;
     } else {
@@ -335,8 +378,11 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   // 1. the prologue's loads, then the weight fragments (rows past N and steps past the slice re-read valid memory;
   // their products are unused): the prologue's arithmetic then overlaps the weights' arrival
   ActIn<CPQ, PRO == SMLM_LIN_PLAIN ? 1 : MTB> act;
+  // ARGMAX with pos_advance: the first workgroup reads the position now and writes it + 1 at its end
+  const bool advance = ARG && a.pos_advance != nullptr && blockIdx.x == 0;
+  const int64_t pos_now = advance ? *a.pos_advance : 0;
   if constexpr (PRO != SMLM_LIN_PLAIN && PRO != SMLM_LIN_RMSNORM_PARTS)
-    load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, act);
+    load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, cb == 0, act);
   PartsIn<CPQ> parts_in;
   if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) load_parts<CPQ>(a, m0, nrows, parts_in);
   uint4 areg[NT][MAXS];
@@ -507,6 +553,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       const uint32_t col = (uint32_t)cb * kArgCols + (0xFFFFu - (best & 0xFFFFu));
       a.partial[(m0 + tid) * a.partial_stride + cb] = ((uint64_t)(best >> 16) << 32) | (uint64_t)(0xFFFFFFFFu - col);
     }
+    if (advance && tid == 0) *a.pos_advance = pos_now + 1;
   }
 }
 
@@ -621,7 +668,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   const smlm_linear_args &A = *a;
   const int pro = A.prologue, epi = A.epilogue;
   if (pro != SMLM_LIN_PLAIN && pro != SMLM_LIN_RMSNORM && pro != SMLM_LIN_EMBED_RMSNORM &&
-      pro != SMLM_LIN_RMSNORM_PARTS)
+      pro != SMLM_LIN_RMSNORM_PARTS && pro != SMLM_LIN_EMBED_ARGMAX)
     return fail(SMLM_EINVAL, "smlm_decode_linear: unknown prologue %d", pro);
   if (epi != SMLM_LIN_STORE && epi != SMLM_LIN_SWIGLU && epi != SMLM_LIN_ARGMAX)
     return fail(SMLM_EINVAL, "smlm_decode_linear: unknown epilogue %d", epi);
@@ -639,6 +686,15 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   if (pro == SMLM_LIN_EMBED_RMSNORM) {
     if (!A.tok || !A.emb || A.emb_rows < 1 || !aligned16(A.emb))
       return fail(SMLM_EINVAL, "smlm_decode_linear: EMBED_RMSNORM needs tok, a 16-byte aligned emb, emb_rows");
+  } else if (pro == SMLM_LIN_EMBED_ARGMAX) {
+    if (!A.emb || A.emb_rows < 1 || !aligned16(A.emb))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: EMBED_ARGMAX needs a 16-byte aligned emb and emb_rows");
+    if (!A.tok_partial || !aligned16(A.tok_partial) || A.tok_blocks < 1 || A.tok_partial_stride < A.tok_blocks ||
+        A.tok_partial_stride % 2)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: EMBED_ARGMAX needs 16-byte aligned tok_partial keys with "
+                  "tok_blocks >= 1 and an even row stride >= tok_blocks");
+    if (A.hist && (!A.pos || A.hist_len < 0 || A.hist_stride < A.hist_len))
+      return fail(SMLM_EINVAL, "smlm_decode_linear: EMBED_ARGMAX hist needs pos and hist_stride >= hist_len >= 0");
   } else {
     if (!A.x || !aligned16(A.x) || A.x_stride < A.K || A.x_stride % 8)
       return fail(SMLM_EINVAL, "smlm_decode_linear: x must be 16-byte aligned with x_stride >= K, a multiple of 8");
@@ -674,7 +730,11 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
     if (!A.partial || A.partial_stride < smlm_linear_argmax_blocks(A.N) || (uintptr_t)A.partial % 8)
       return fail(SMLM_EINVAL, "smlm_decode_linear: ARGMAX needs partial (M, >= %d) uint64",
                   smlm_linear_argmax_blocks(A.N));
+    if (A.pos_advance && A.M == 0)
+      return fail(SMLM_EINVAL, "smlm_decode_linear: pos_advance needs M >= 1 (an empty launch runs nothing)");
   }
+  if (A.pos_advance && epi != SMLM_LIN_ARGMAX)
+    return fail(SMLM_EINVAL, "smlm_decode_linear: pos_advance belongs to the ARGMAX epilogue");
   if (A.M == 0) return SMLM_OK;
   // 16-token groups (more workgroups, shorter per-workgroup chains: decode is latency-bound), except the ARGMAX
   // epilogue over more than 16 rows: 32-row groups (each workgroup normalises its rows in the prologue, so 64-row
@@ -700,7 +760,8 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   if (pro == SMLM_LIN_PLAIN) launch_linear_pro<SMLM_LIN_PLAIN>(A, lg, s);
   else if (pro == SMLM_LIN_RMSNORM) launch_linear_pro<SMLM_LIN_RMSNORM>(A, lg, s);
   else if (pro == SMLM_LIN_RMSNORM_PARTS) launch_linear_pro<SMLM_LIN_RMSNORM_PARTS>(A, lg, s);
-  else launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, lg, s);
+  else if (pro == SMLM_LIN_EMBED_RMSNORM) launch_linear_pro<SMLM_LIN_EMBED_RMSNORM>(A, lg, s);
+  else launch_linear_pro<SMLM_LIN_EMBED_ARGMAX>(A, lg, s);
   return launch_status("smlm_decode_linear");
 }
 

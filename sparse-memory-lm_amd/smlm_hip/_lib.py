@@ -19,7 +19,7 @@ OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
 _p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # smlm_linear_prologue / smlm_linear_epilogue
-LIN_PLAIN, LIN_RMSNORM, LIN_EMBED_RMSNORM, LIN_RMSNORM_PARTS = range(4)
+LIN_PLAIN, LIN_RMSNORM, LIN_EMBED_RMSNORM, LIN_RMSNORM_PARTS, LIN_EMBED_ARGMAX = range(5)
 LIN_STORE, LIN_SWIGLU, LIN_ARGMAX = range(3)
 
 
@@ -31,6 +31,8 @@ class LinearArgs(ctypes.Structure):
         ("norm_w", _p), ("eps", ctypes.c_float), ("x_out", _p), ("w", _p), ("bias", _p), ("scale", _p),
         ("shift", _p), ("n_affine", _i), ("n_split", _i), ("out", _p), ("out_stride", _i64), ("out2", _p),
         ("out2_stride", _i64), ("partial", _p), ("partial_stride", _i64), ("delta_parts", _i),
+        ("tok_partial", _p), ("tok_partial_stride", _i64), ("tok_blocks", _i), ("tok_out", _p), ("hist", _p),
+        ("hist_stride", _i64), ("hist_len", _i64), ("pos", _p), ("pos_advance", _p),
     ]
 
 # name -> (restype, argtypes); every function declared in include/smlm_pkm.h

@@ -486,36 +486,69 @@ def _rms_eps(norm):
 
 
 def decode_linear(weight, x=None, *, delta=None, norm=None, tok=None, emb=None, write_x=False, bias=None,
-                  affine=None, n_split=None, swiglu=False, argmax=False):
+                  affine=None, n_split=None, swiglu=False, argmax=False, tok_partial=None, tok_out=None, hist=None,
+                  pos=None, partial_out=None, advance_pos=None):
     """Fused small-M linear layer of the decode step (smlm_decode_linear): y = h @ weight.T on the matrix cores.
 
     h is x (M, K) bf16 (unit column stride); with `norm` (an nn.RMSNorm over K with a bf16 weight) it is
     norm(xs), xs = bf16(x + delta) (delta (M, K) bf16 or None; or (M, P, K) fp32 parts from decode_attention_proj,
     then delta = bf16(sum over P in order), P <= 8, not with argmax), or xs = emb[tok] when `tok` (M,) int64 and
-    `emb` (V, K) bf16 are given instead of x.  The epilogue is one of
+    `emb` (V, K) bf16 are given instead of x.  With `tok_partial` (M, nblk) int64 instead of tok, the tokens are
+    the greedy choice from those argmax partial keys (the previous step's), and the launch also writes them to
+    `tok_out` (M,) int64 and to hist[:, pos] (hist (M, L) int64 with pos a one-element int64 tensor; skipped
+    outside the history) when given.  The epilogue is one of
       default   bf16(y + bias) (bias (N,) bf16 or None); `affine` = (scale, shift) fp32 tensors applied as
                 bf16(v * scale + shift) to the first len(scale) columns; with `n_split`, columns [0, n_split) and
                 [n_split, N) are returned as two tensors;
       swiglu    bf16(bf16(silu(a)) * b) with a | b the two halves of y (weight (2*hidden, K)) -> (M, hidden);
       argmax    no logits: (M, smlm_linear_argmax_blocks(N)) int64 tensor of uint64 partial keys for
-                argmax_finish.
+                argmax_finish or the next step's tok_partial (written into `partial_out` when given); with
+                `advance_pos` (one-element int64 tensor) the launch also adds 1 to it.
     With write_x (an RMSNorm prologue) returns (xs, result)."""
-    _need_cuda("decode_linear", weight, x, delta, tok, emb, bias)
+    _need_cuda("decode_linear", weight, x, delta, tok, emb, bias, tok_partial, tok_out, hist, pos, partial_out,
+               advance_pos)
     if weight.dtype != torch.bfloat16 or weight.dim() != 2 or not weight.is_contiguous():
         raise ValueError("decode_linear: weight must be a contiguous (N, K) bf16 tensor")
     N, K = weight.shape
     args = _lib.LinearArgs()
     args.N, args.K = N, K
-    if tok is not None:
-        if norm is None or emb is None or x is not None or delta is not None:
-            raise ValueError("decode_linear: tok needs emb and norm, and excludes x and delta")
-        if tok.dtype != torch.int64 or tok.dim() != 1 or emb.dtype != torch.bfloat16 or emb.dim() != 2 \
-                or emb.shape[1] != K or not emb.is_contiguous():
-            raise ValueError("decode_linear: tok must be (M,) int64 and emb a contiguous (V, K) bf16 tensor")
-        tok = tok.contiguous()
-        M, dev = tok.shape[0], tok.device
-        args.prologue = _lib.LIN_EMBED_RMSNORM
-        args.tok, args.emb, args.emb_rows = tok.data_ptr(), emb.data_ptr(), emb.shape[0]
+    keep = []
+    if tok is not None or tok_partial is not None:
+        if norm is None or emb is None or x is not None or delta is not None or (tok is not None
+                                                                                and tok_partial is not None):
+            raise ValueError("decode_linear: tok or tok_partial needs emb and norm, and excludes x and delta")
+        if emb.dtype != torch.bfloat16 or emb.dim() != 2 or emb.shape[1] != K or not emb.is_contiguous():
+            raise ValueError("decode_linear: emb must be a contiguous (V, K) bf16 tensor")
+        args.emb, args.emb_rows = emb.data_ptr(), emb.shape[0]
+        if tok is not None:
+            if tok.dtype != torch.int64 or tok.dim() != 1:
+                raise ValueError("decode_linear: tok must be (M,) int64")
+            tok = tok.contiguous()
+            M, dev = tok.shape[0], tok.device
+            args.prologue, args.tok = _lib.LIN_EMBED_RMSNORM, tok.data_ptr()
+        else:
+            if tok_partial.dtype != torch.int64 or tok_partial.dim() != 2 or tok_partial.stride(1) != 1 \
+                    or tok_partial.stride(0) % 2 or tok_partial.data_ptr() % 16:
+                raise ValueError("decode_linear: tok_partial must be (M, nblk) int64 with an even row stride, "
+                                 "16-byte aligned")
+            M, dev = tok_partial.shape[0], tok_partial.device
+            args.prologue = _lib.LIN_EMBED_ARGMAX
+            args.tok_partial, args.tok_partial_stride = tok_partial.data_ptr(), tok_partial.stride(0)
+            args.tok_blocks = tok_partial.shape[1]
+            if tok_out is not None:
+                if tok_out.dtype != torch.int64 or tok_out.numel() != M or not tok_out.is_contiguous():
+                    raise ValueError("decode_linear: tok_out must be (M,) int64 contiguous")
+                args.tok_out = tok_out.data_ptr()
+            if hist is not None:
+                if hist.dtype != torch.int64 or hist.dim() != 2 or hist.shape[0] != M or hist.stride(1) != 1 \
+                        or pos is None or pos.dtype != torch.int64 or pos.numel() != 1:
+                    raise ValueError("decode_linear: hist must be (M, L) int64 with unit column stride, with pos "
+                                     "one int64")
+                args.hist, args.hist_stride, args.hist_len = hist.data_ptr(), hist.stride(0), hist.shape[1]
+                args.pos = pos.data_ptr()
+        keep += [tok, tok_partial, emb]
+    elif tok_out is not None or hist is not None or pos is not None:
+        raise ValueError("decode_linear: tok_out, hist and pos come with tok_partial")
     else:
         if x is None or x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != K:
             raise ValueError(f"decode_linear: x must be a (M, {K}) bf16 tensor")
@@ -545,11 +578,23 @@ def decode_linear(weight, x=None, *, delta=None, norm=None, tok=None, emb=None, 
     elif write_x:
         raise ValueError("decode_linear: write_x needs an RMSNorm prologue")
     args.w = weight.data_ptr()
-    keep = [x, delta, tok, emb, weight]
+    keep += [x, delta, weight]
+    if (partial_out is not None or advance_pos is not None) and not argmax:
+        raise ValueError("decode_linear: partial_out and advance_pos belong to argmax")
     if argmax:
         nblk = _lib.lib().smlm_linear_argmax_blocks(N)
-        res = torch.empty(M, nblk, dtype=torch.int64, device=dev)
-        args.epilogue, args.partial, args.partial_stride = _lib.LIN_ARGMAX, res.data_ptr(), nblk
+        if partial_out is None:
+            res = torch.empty(M, nblk, dtype=torch.int64, device=dev)
+        elif partial_out.dtype != torch.int64 or partial_out.dim() != 2 or partial_out.shape[0] != M \
+                or partial_out.shape[1] < nblk or partial_out.stride(1) != 1:
+            raise ValueError(f"decode_linear: partial_out must be (M, >= {nblk}) int64 with unit column stride")
+        else:
+            res = partial_out
+        args.epilogue, args.partial, args.partial_stride = _lib.LIN_ARGMAX, res.data_ptr(), res.stride(0)
+        if advance_pos is not None:
+            if advance_pos.dtype != torch.int64 or advance_pos.numel() != 1:
+                raise ValueError("decode_linear: advance_pos must be one int64")
+            args.pos_advance = advance_pos.data_ptr()
     elif swiglu:
         res = torch.empty(M, N // 2, dtype=torch.bfloat16, device=dev)
         args.epilogue, args.out, args.out_stride = _lib.LIN_SWIGLU, res.data_ptr(), N // 2
@@ -580,6 +625,11 @@ def decode_linear(weight, x=None, *, delta=None, norm=None, tok=None, emb=None, 
     _lib.check(rc, "smlm_decode_linear")
     del keep
     return (x_out, res) if write_x else res
+
+
+def linear_argmax_blocks(N):
+    """Columns of the argmax partial keys decode_linear(..., argmax=True) writes for N output features."""
+    return int(_lib.lib().smlm_linear_argmax_blocks(int(N)))
 
 
 def argmax_finish(partial, pos, tok, hist=None, advance=True):

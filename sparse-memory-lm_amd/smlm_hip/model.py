@@ -436,7 +436,9 @@ class _FusedDecodeStep:
         [residual add + ffn_norm + query_proj | swilu_proj + eval BatchNorm] [sub-key scores]
         [selection + value bag + swilu] [value_proj]
     then [residual add + final norm + lm_head + argmax partials] [token, history slot, position + 1]; the first
-    block's prologue gathers the token embeddings.  These are the ops of Transformer.forward on bf16 weights
+    block's prologue gathers the token embeddings.  Chained steps (run(..., chain=keys), as _StepDecoder runs them)
+    drop the last launch: the first launch of the next step picks the token from the argmax partials, writes it and
+    its history slot, and the lm_head launch advances the position.  These are the ops of Transformer.forward on bf16 weights
     (smlm/model.py:63-118, 156-163, 266-293; smlm/pkm.py:186-228) with the same bf16 roundings: 5 launches per
     dense block, 7 per memory block and 2 for the head, instead of the ~10 PyTorch launches per block.
 
@@ -498,11 +500,18 @@ class _FusedDecodeStep:
                 self.mem[i] = (w, b)
         self._tag = self._params_tag()
 
-    def run(self, tok, pos, caches, hist, logits=False, record=None):
+    def run(self, tok, pos, caches, hist, logits=False, record=None, chain=None):
         """The step for tok (B, 1) at device position pos: writes the next token to tok and hist[:, pos + 1] and
         advances pos.  With logits=True it returns the (B, vocab) bf16 logits instead and changes none of tok,
         hist and pos (the KV caches get the same slot written).  With a dict `record`, record[layer] =
-        (s1, s2, scores, indices, weights) of each memory layer's lookup."""
+        (s1, s2, scores, indices, weights) of each memory layer's lookup.
+
+        With `chain` ((B, >= argmax blocks) int64 argmax keys, even row stride; not with logits) the step's token
+        is the greedy choice from the keys the previous chained step left in chain (or that _StepDecoder seeded):
+        the first launch writes it to tok and hist[:, pos]; the step then leaves its own keys in chain and advances
+        pos.  The next token reaches tok and hist in the next chained step (or in _StepDecoder.finish)."""
+        if chain is not None and logits:
+            raise ValueError("run: a chained step ends with argmax keys, not logits")
         model = self.model
         if not torch.cuda.is_current_stream_capturing() and self._params_tag() != self._tag:
             self._prepare()
@@ -511,7 +520,10 @@ class _FusedDecodeStep:
         x = delta = None
         for i, blk in enumerate(model.layers):
             at = blk.attn
-            if x is None:
+            if x is None and chain is not None:
+                x, qkv = kernels.decode_linear(at.wqkv.weight, tok_partial=chain, tok_out=tok.view(-1), hist=hist,
+                                               pos=pos, emb=model.tok_emb.weight, norm=blk.attn_norm, write_x=True)
+            elif x is None:
                 x, qkv = kernels.decode_linear(at.wqkv.weight, tok=tok.view(-1), emb=model.tok_emb.weight,
                                                norm=blk.attn_norm, write_x=True)
             else:
@@ -545,6 +557,10 @@ class _FusedDecodeStep:
                 delta = kernels.decode_linear(f.w2.weight, act)
         if logits:
             return kernels.decode_linear(model.lm_head.weight, x, delta=delta, norm=model.norm)
+        if chain is not None:
+            kernels.decode_linear(model.lm_head.weight, x, delta=delta, norm=model.norm, argmax=True,
+                                  partial_out=chain, advance_pos=pos)
+            return None
         partial = kernels.decode_linear(model.lm_head.weight, x, delta=delta, norm=model.norm, argmax=True)
         kernels.argmax_finish(partial, pos, tok.view(-1), hist)
         return None
@@ -553,7 +569,11 @@ class _FusedDecodeStep:
 class _StepDecoder:
     """Static buffers and the captured graphs of one decode step and of `steps_per_graph` steps in a row for batch
     B, sequences up to max_len.  A step reads its position and token from device memory and advances them itself,
-    so a run of steps is one graph replay: the replay boundary (about 15 us on MI355X) is paid once per run."""
+    so a run of steps is one graph replay: the replay boundary (about 15 us on MI355X) is paid once per run.
+
+    On the fused kernels the steps are chained through `chain`, the lm_head's argmax keys: a step's first launch
+    picks its token from the previous step's keys.  start() seeds the keys with the first token, finish() turns
+    the last step's keys into tok and its history slot; replay() and steps() end with it."""
 
     steps_per_graph = 8
 
@@ -573,10 +593,38 @@ class _StepDecoder:
         self.graph = None
         self.graph_run = None
         self.fused = _FusedDecodeStep(model) if _FusedDecodeStep.supported(model, dtype) else None
+        self.chain = None
+        if self.fused is not None:
+            nblk = kernels.linear_argmax_blocks(cfg.vocab_size)
+            self.chain = torch.zeros(B, nblk + nblk % 2, dtype=torch.long, device=device)   # even row stride
+
+    def _seed(self):
+        """Argmax keys whose greedy choice is tok: ~tok (above every logit key) in column 0, no key elsewhere."""
+        self.chain.zero_()
+        self.chain[:, 0] = ~self.tok.view(-1)
+
+    def start(self, first, P):
+        """The state a run of steps starts from: the first sampled token `first` (B,) at position P."""
+        self.hist[:, P] = first.view(-1)
+        self.tok.copy_(first.view(self.B, 1))
+        self.pos.fill_(P)
+        if self.chain is not None:
+            self._seed()
+
+    def finish(self):
+        """After chained steps: the last step's greedy token to tok and hist[:, pos] (pos is already advanced)."""
+        if self.chain is not None:
+            kernels.argmax_finish(self.chain, self.pos - 1, self.tok.view(-1), self.hist, advance=False)
+
+    def steps(self, n):
+        """n decode steps run eagerly (no graph), then finish()."""
+        for _ in range(n):
+            self._step()
+        self.finish()
 
     def _step(self):
         if self.fused is not None:
-            self.fused.run(self.tok, self.pos, self.caches, self.hist)
+            self.fused.run(self.tok, self.pos, self.caches, self.hist, chain=self.chain)
             return
         logits = self.model(self.tok, kv_caches=self.caches, pos0=self.pos)
         last = logits[:, -1]
@@ -594,6 +642,9 @@ class _StepDecoder:
         ctx = (torch.autocast("cuda", dtype=torch.get_autocast_dtype("cuda"), cache_enabled=False) if ac
                else torch.autocast("cuda", enabled=False))
         self.pos.fill_(0)
+        self.tok.zero_()
+        if self.chain is not None:
+            self._seed()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side), ctx:
@@ -612,7 +663,7 @@ class _StepDecoder:
             self.graph_run = run
 
     def replay(self, n):
-        """n decode steps as graph replays: runs of steps_per_graph, then single steps."""
+        """n decode steps as graph replays: runs of steps_per_graph, then single steps; then finish()."""
         if self.graph is None:
             self._capture()
         k = self.steps_per_graph if self.graph_run is not None else 1
@@ -620,6 +671,7 @@ class _StepDecoder:
             (self.graph_run if k > 1 else self.graph).replay()
         for _ in range(n - n // k * k):
             self.graph.replay()
+        self.finish()
 
     def run(self, prompt, new_tokens, use_graph, sync_every_step):
         B, P = prompt.shape
@@ -633,9 +685,7 @@ class _StepDecoder:
             self._capture()
         logits = self.model(prompt, kv_caches=self.caches, pos0=0)
         self.hist[:, :P] = prompt
-        self.hist[:, P] = logits[:, -1].argmax(-1)
-        self.tok.copy_(self.hist[:, P:P + 1])
-        self.pos.fill_(P)
+        self.start(logits[:, -1].argmax(-1), P)
         if use_graph and not sync_every_step:
             self.replay(new_tokens)
             return self.hist[:, P:P + new_tokens + 1].clone()
@@ -646,4 +696,5 @@ class _StepDecoder:
                 self._step()
             if sync_every_step:
                 torch.cuda.current_stream().synchronize()
+        self.finish()
         return self.hist[:, P:P + new_tokens + 1].clone()

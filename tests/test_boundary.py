@@ -152,6 +152,30 @@ def test_decode_linear_argument_checks():
     assert lib.smlm_argmax_finish(None, 1, 1, 1, fake, fake, None, 0, 0, 1, None) == _lib.EINVAL
 
 
+def test_embed_argmax_prologue_argument_checks():
+    """SMLM_LIN_EMBED_ARGMAX and pos_advance refuse bad arguments before any launch."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    a = _lib.LinearArgs()
+    a.prologue, a.epilogue, a.M, a.N, a.K = _lib.LIN_EMBED_ARGMAX, _lib.LIN_STORE, 2, 64, 384
+    a.w, a.norm_w, a.n_split, a.out, a.out_stride, a.emb, a.emb_rows = fake, fake, 64, fake, 64, fake, 100
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "tok_partial" in _lib.last_error()
+    a.tok_partial, a.tok_blocks, a.tok_partial_stride = fake, 5, 5          # odd row stride
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "even" in _lib.last_error()
+    a.tok_partial_stride = 4                                              # shorter than the blocks
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.tok_partial_stride, a.tok_partial = 6, ctypes.c_void_p(0x1008)      # keys not 16-byte aligned
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL
+    a.tok_partial, a.hist, a.hist_len, a.hist_stride = fake, fake, 10, 10  # hist without pos
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "pos" in _lib.last_error()
+    a.pos, a.M = fake, 0                                                  # valid; zero rows: a no-op
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.OK
+    a.pos_advance = fake                                                  # pos_advance without ARGMAX
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "pos_advance" in _lib.last_error()
+    a.epilogue, a.partial, a.partial_stride = _lib.LIN_ARGMAX, fake, 1   # ARGMAX with M = 0: nothing would advance
+    assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "M >= 1" in _lib.last_error()
+
+
 def test_parts_prologue_and_attention_proj_argument_checks():
     """The RMSNORM_PARTS prologue and smlm_decode_attention_proj refuse bad arguments before any launch."""
     lib = _lib.lib()

@@ -130,8 +130,7 @@ def decode_parity(model, B, P, steps, seed):
 
     # the whole-step graph from the same state gives the same tokens (runs of 8 steps, then single steps)
     dec.hist[:, P + 1:] = -1
-    dec.tok.copy_(first.view(B, 1))
-    dec.pos.fill_(P)
+    dec.start(first, P)
     dec.replay(steps)
     torch.cuda.synchronize()
     assert _StepDecoder.steps_per_graph == 8

@@ -174,6 +174,56 @@ def test_argmax_epilogue_and_finish(M, N):
     assert bool((hist[:, 5:] == -1).all())
 
 
+@pytest.mark.parametrize("M,N,pad", [(1, 32000, 0), (64, 32000, 0), (17, 640, 1), (5, 128, 1)])
+def test_embed_argmax_prologue_matches_finish_then_embed(M, N, pad):
+    """EMBED_ARGMAX (the token picked from the previous step's argmax keys inside the next step's first launch)
+    against argmax_finish followed by the EMBED_RMSNORM launch on its tokens: bit-identical residual rows and
+    outputs, the same tokens in tok_out and in hist[:, pos] (pos itself unchanged); an odd number of key blocks
+    (the row stride padded to even), a row without keys (id 2^32 - 1: a NaN row in both), keys seeded as ~token
+    (what the decoder's start() writes), a history slot outside the history (no write); and the lm_head launch's
+    pos_advance adds one without changing the keys."""
+    note(f"embed argmax prologue M={M} N={N}")
+    g = torch.Generator().manual_seed(M * 7 + N)
+    K_, V = 384, N
+    x = bf(torch.randn(M, K_, generator=g)).to(DEV)
+    w_lm = bf(torch.randn(N, K_, generator=g) * 0.05).to(DEV)
+    norm = make_norm(K_, g)
+    nblk = _lib.lib().smlm_linear_argmax_blocks(N)
+    keys = torch.zeros(M, nblk + pad, dtype=torch.int64, device=DEV)
+    partial = K.decode_linear(w_lm, x, norm=norm, argmax=True, partial_out=keys[:, :nblk])
+    assert partial.data_ptr() == keys.data_ptr()
+    pos = torch.tensor(5, device=DEV)
+    again = torch.zeros_like(keys)
+    K.decode_linear(w_lm, x, norm=norm, argmax=True, partial_out=again[:, :nblk], advance_pos=pos)
+    assert int(pos) == 6 and torch.equal(again, keys)
+    if M > 2:
+        keys[1] = 0                                        # no keys: id 2^32 - 1
+        keys[2] = 0
+        keys[2, 0] = ~torch.tensor(N - 3)                  # seeded: token N - 3
+    emb = bf(torch.randn(V, K_, generator=g) * 0.02).to(DEV)
+    w = bf(torch.randn(1152, K_, generator=g) * 0.05).to(DEV)
+    tok = torch.empty(M, dtype=torch.int64, device=DEV)
+    K.argmax_finish(keys, torch.tensor(0, device=DEV), tok, advance=False)
+    if M > 2:
+        assert int(tok[1]) == 2 ** 32 - 1 and int(tok[2]) == N - 3
+    xs_ref, y_ref = K.decode_linear(w, tok=tok, emb=emb, norm=norm, write_x=True)
+    L = 12
+    hist = torch.full((M, L), -1, dtype=torch.int64, device=DEV)
+    tok_out = torch.full((M,), -7, dtype=torch.int64, device=DEV)
+    xs, y = K.decode_linear(w, tok_partial=keys, tok_out=tok_out, hist=hist, pos=pos, emb=emb, norm=norm,
+                            write_x=True)
+    assert int(pos) == 6
+    assert torch.equal(xs.view(torch.int16), xs_ref.view(torch.int16))
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+    assert torch.equal(tok_out, tok)
+    assert torch.equal(hist[:, 6], tok) and bool((hist[:, :6] == -1).all()) and bool((hist[:, 7:] == -1).all())
+    if M > 2:
+        assert bool(xs[1].isnan().all()) and not bool(xs[0].isnan().any())
+    hist.fill_(-1)
+    K.decode_linear(w, tok_partial=keys, hist=hist, pos=torch.tensor(L, device=DEV), emb=emb, norm=norm)
+    assert bool((hist == -1).all())
+
+
 def test_argmax_all_equal_logits_gives_column_zero():
     M, N, K_ = 4, 640, 64
     w = torch.zeros(N, K_, dtype=torch.bfloat16, device=DEV)
