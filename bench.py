@@ -120,11 +120,11 @@ def time_generations(model, B, reps, warmup, dev, prompt_len=128, new_tokens=GEN
     return B * new_tokens * reps / total, ms_gen, ms_gen / new_tokens
 
 
-def chained_launch_us(dev, numel=384, kernels=272, replays=40):
+def chained_launch_us(dev, numel=384, kernels=264, replays=40):
     """Device time per kernel of a HIP graph of `kernels` back-to-back elementwise kernels, each reading the `numel`
     fp32 values its predecessor wrote (in-place adds): 384 values are one workgroup, the floor every kernel of a
     captured decode step pays whatever its work; 262,144 values spread one kernel over the whole chip.
-    272 = the 8 decode steps of one graph replay x 34 kernels."""
+    264 = the 8 decode steps of one graph replay x 33 kernels."""
     import torch
     x = torch.zeros(numel, dtype=torch.float32, device=dev)
     side = torch.cuda.Stream(dev)
@@ -200,8 +200,9 @@ def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
     HBM: the bytes a step must move — every weight matrix once (the tied embedding once as lm_head, plus B embedding
     rows), every memory layer's sub-keys, the B x heads x knn value rows (bf16 table), the K and V cache rows of
     positions 0..pos-1 read and row pos written per layer — over 8 TB/s.
-    Launch: the step's kernel count (5 per dense block, 7 per memory block, 2 for the head; one fewer per block
-    where the attention launch does wo as well) x the one-workgroup chained-kernel time of chained_launch_us."""
+    Launch: the step's kernel count (5 per dense block, 7 per memory block, 1 for the head — the token is picked in
+    the next step's first launch; one fewer per block where the attention launch does wo as well) x the
+    one-workgroup chained-kernel time of chained_launch_us."""
     from smlm_hip.model import _FusedDecodeStep
     cfg = model.cfg
     C = cfg.d_model
@@ -217,7 +218,7 @@ def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
     total = w + values + kv
     hbm_ms = total / (HBM_PEAK_GBS * 1e9) * 1e3
     fold = B <= _FusedDecodeStep.proj_max_batch and cfg.n_heads <= 8
-    launches = (4 if fold else 5) * (cfg.n_layers - n_mem) + (6 if fold else 7) * n_mem + 2
+    launches = (4 if fold else 5) * (cfg.n_layers - n_mem) + (6 if fold else 7) * n_mem + 1
     launch_ms = launches * launch_us / 1e3
     return {"bound": "launch" if launch_ms >= hbm_ms else "hbm", "ms_per_step": ms_per_step,
             "hbm_bytes_per_step": total, "weight_bytes": w, "value_row_bytes": values, "kv_cache_bytes": kv,
