@@ -5,12 +5,13 @@
 //      bf16 as the bf16 model holds them, by every wavefront for itself through its own LDS row (no workgroup
 //      barrier); k and v are written into the cache at the device-side position `pos`;
 //   2. scores s_t = q . k_t / sqrt(head_dim) for t = 0..pos, each cache row read with 16-byte loads by
-//      head_dim/8 lanes and reduced with lane shuffles; the keys and values of a group of passes of rows are in
-//      flight together (a decode step is latency-bound), issued after the new token's q, k, v and only for passes
-//      that hold rows (raw buffer loads bounded at row pos), so each pass is used as soon as its rows arrive;
+//      head_dim/8 lanes (bf16 pair dot products into fp32: q and k are bf16 values, so the products are exact) and
+//      reduced with lane shuffles; the keys and values of a group of passes of rows are in flight together (a
+//      decode step is latency-bound), issued after the new token's q, k, v and only for passes that hold rows (raw
+//      buffer loads bounded at row pos), so each pass is used as soon as its rows arrive;
 //   3. softmax in fp32, by each wavefront over its own rows and in registers: its maximum m_w, the exponentials
 //      p_t = exp(s_t - m_w) and their sum l_w (online over the groups of passes: a group that raises the maximum
-//      rescales what came before);
+//      rescales what came before).  Scores are kept in log2 units (s_t log2 e), so each exponential is one exp2;
 //   4. the wavefront's y_w = sum_t p_t v_t in registers; then one merge through LDS: m = max m_w,
 //      y = sum_w y_w exp(m_w - m) / sum_w l_w exp(m_w - m), written as bf16 into the (B, H*head_dim) layout the
 //      output projection reads.
@@ -26,6 +27,8 @@ namespace smlm {
 namespace {
 
 constexpr int kAttnUnroll = 8;    // passes of cache rows whose loads are in flight together
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -221,8 +224,9 @@ __global__ void __launch_bounds__(kAttnThreads)
   // the cache rows 0..P-1 of (b, h) as raw buffers: a row at or past P reads as zero without a memory access
   const BufferRows krows(k_cache + cache_row * HD, P * HD), vrows(v_cache + cache_row * HD, P * HD);
 
-  const float scale = rsqrtf((float)HD);
+  const float scale = 1.4426950408889634f * rsqrtf((float)HD);   // log2(e) / sqrt(head_dim): scores in log2 units
   float qf[8];                                   // this lane's 8 dims of the rotated q
+  bf16x2 qp[4];                                  // the same as bf16 pairs (exact: q is rounded to bf16)
   float m_run = -INFINITY, l_run = 0.f, acc[8] = {};  // the wavefront's running softmax
 
   // 1. RoPE (dim i < HALF: x_i c_i - x_{i+HALF} s_i, dim i + HALF: x_i s_i + x_{i+HALF} c_i, in fp32 with one bf16
@@ -260,6 +264,10 @@ __global__ void __launch_bounds__(kAttnThreads)
     wave_lds_sync();
 #pragma unroll
     for (int e = 0; e < 8; ++e) qf[e] = s_q[d0 + e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      qp[e] = __builtin_bit_cast(bf16x2, (__float_as_uint(qf[2 * e]) >> 16) |
+                                             (__float_as_uint(qf[2 * e + 1]) & 0xFFFF0000u));
     if (wave == 0) {
       float dd = 0.f;
 #pragma unroll
@@ -281,11 +289,10 @@ __global__ void __launch_bounds__(kAttnThreads)
 #pragma unroll
     for (int u = 0; u < NP; ++u) {
       const int t = t0 + u * RPB + slot;
-      float kf[8];
-      unpack8(kv[u], kf);
-      float dd = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dd = fmaf(qf[e], kf[e], dd);
+      float dd = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kv[u].x), qp[0], 0.f, false);
+      dd = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kv[u].y), qp[1], dd, false);
+      dd = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kv[u].z), qp[2], dd, false);
+      dd = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kv[u].w), qp[3], dd, false);
       dd = group_sum<LPR>(dd);
       d[u] = t < P ? dd * scale : -INFINITY;
       gm = fmaxf(gm, d[u]);
@@ -293,13 +300,13 @@ __global__ void __launch_bounds__(kAttnThreads)
     gm = strided_max<LPR>(gm);               // over the wavefront's row groups
     const float m_new = fmaxf(m_run, gm);
     if (m_new == -INFINITY) return;          // wavefront-uniform: none of its rows so far
-    const float corr = expf(m_run - m_new);  // 0 while the wavefront had no row
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 while the wavefront had no row
     l_run *= corr;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] *= corr;
 #pragma unroll
     for (int u = 0; u < NP; ++u) {
-      const float pt = expf(d[u] - m_new);  // 0 for rows at or past P
+      const float pt = __builtin_amdgcn_exp2f(d[u] - m_new);  // 0 for rows at or past P
       float vf[8];
       unpack8(vv[u], vf);
       l_run += pt;
@@ -355,7 +362,7 @@ __global__ void __launch_bounds__(kAttnThreads)
   float sum = 0.f;
 #pragma unroll
   for (int w = 0; w < kAttnWaves; ++w) {
-    fw[w] = expf(s_w[w] - mx);               // 0 for a wavefront without rows (maximum -inf)
+    fw[w] = __builtin_amdgcn_exp2f(s_w[w] - mx);  // 0 for a wavefront without rows (maximum -inf)
     sum += s_w[kAttnWaves + w] * fw[w];
   }
   const float inv = 1.0f / sum;
