@@ -383,9 +383,11 @@ __global__ void __launch_bounds__(kAttnThreads)
       s_y[i] = round_bf16(y * inv);
     }
     __syncthreads();
-    float yv[8];
+    bf16x2 yp[4];  // this lane's 8 columns of bf16(y) as bf16 pairs (exact), for pair dot products with wo
 #pragma unroll
-    for (int e = 0; e < 8; ++e) yv[e] = s_y[wc * 8 + e];
+    for (int e = 0; e < 4; ++e)
+      yp[e] = __builtin_bit_cast(bf16x2, (__float_as_uint(s_y[wc * 8 + 2 * e]) >> 16) |
+                                             (__float_as_uint(s_y[wc * 8 + 2 * e + 1]) & 0xFFFF0000u));
     for (int base = 0; base < n_out; base += WR * RPP) {
       if (base > 0) {
 #pragma unroll
@@ -398,11 +400,10 @@ __global__ void __launch_bounds__(kAttnThreads)
 #pragma unroll
       for (int i = 0; i < WR; ++i) {
         if (base + i * RPP >= n_out) break;  // workgroup-uniform
-        float wf[8];
-        unpack8(wreg[i], wf);
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(yv[e], wf[e], d);
+        float d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wreg[i].x), yp[0], 0.f, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wreg[i].y), yp[1], d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wreg[i].z), yp[2], d, false);
+        d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wreg[i].w), yp[3], d, false);
         d = group_sum<LPR>(d);
         const int n = base + wr0 + i * RPP;
         if (wc == 0 && n < n_out) po[n] = valid ? d : __builtin_nanf("");
