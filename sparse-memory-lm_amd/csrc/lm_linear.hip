@@ -90,34 +90,79 @@ struct ActIn {
 
 // The greedy token of row m from ARGMAX partial keys (order16(bf16 logit) << 32 | ~column, 0 = no key): the column
 // of the row's largest key, found by the 16 lanes of a quarter wavefront (lane `sub` reads the 16-byte key pairs
-// sub, sub + 16, ..., all of a round's loads in flight, then a 4-step butterfly).  The same maximum over the same
-// keys as argmax_finish_kernel, so the same token.
+// sub, sub + 16, ..., a round's loads in flight together, then a 4-step DPP maximum over the 16 lanes).  The same
+// maximum over the same keys as argmax_finish_kernel, so the same token.  The first round's loads are issued before
+// the weight fragments (TokKeys), the rest (vocabularies past 32,768 columns) when the keys are reduced.
 constexpr int kTokLoads = 8;   // key pairs per lane and round: 256 keys (32,768 columns) per round
 
-__device__ __forceinline__ int64_t row_argmax_token(const smlm_linear_args &a, int64_t m, int sub) {
-  const uint64_t *row = a.tok_partial + m * a.tok_partial_stride;
+template <int MTB>
+struct TokKeys {
+  uint4 v[MTB][kTokLoads];   // the first round of each pass's row
+};
+
+__device__ __forceinline__ uint4 key_pairs(const smlm_linear_args &a, int64_t m, int c) {
+  const int npairs = (a.tok_blocks + 1) / 2;
+  return *(const uint4 *)(a.tok_partial + m * a.tok_partial_stride + 2 * min(c, npairs - 1));
+}
+
+template <int MTB>
+__device__ __forceinline__ void load_token_keys(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
+                                                TokKeys<MTB> &keys) {
+  const int wave = threadIdx.x / kWave, lane = lane_id();
+  const int quarter = lane >> 4, sub = lane & 15;
+#pragma unroll
+  for (int p = 0; p < MTB; ++p) {
+    if (p > 0 && p >= pad_rows / 16) continue;     // wavefront-uniform (pass 0 always has a row: no branch)
+    const int64_t m = m0 + min(p * 16 + wave * 4 + quarter, nrows - 1);
+#pragma unroll
+    for (int j = 0; j < kTokLoads; ++j) keys.v[p][j] = key_pairs(a, m, sub + 16 * j);
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// The largest key of a round of pairs c0 + sub + 16 j (pairs past the row repeat its last pair; a pair's second key
+// past tok_blocks is the stride's pad and counts as 0).
+__device__ __forceinline__ uint64_t max_of_pairs(const smlm_linear_args &a, const uint4 *v, int c0, int sub,
+                                                 uint64_t best) {
   const int nb = a.tok_blocks, npairs = (nb + 1) / 2;
-  uint64_t best = 0;
-  for (int c0 = 0; c0 < npairs; c0 += 16 * kTokLoads) {
+#pragma unroll
+  for (int j = 0; j < kTokLoads; ++j) {
+    const int c = min(c0 + sub + 16 * j, npairs - 1);
+    const uint64_t k0 = ((uint64_t)v[j].y << 32) | v[j].x;
+    const uint64_t k1 = 2 * c + 1 < nb ? ((uint64_t)v[j].w << 32) | v[j].z : 0;
+    best = max(best, max(k0, k1));
+  }
+  return best;
+}
+
+// All 64 lanes active: every lane ends with the maximum of its 16-lane row (the lane patterns of row16_sum).
+__device__ __forceinline__ int64_t row_argmax_token(const smlm_linear_args &a, int64_t m, int sub,
+                                                    const uint4 *first) {
+  const int npairs = (a.tok_blocks + 1) / 2;
+  uint64_t best = max_of_pairs(a, first, 0, sub, 0);
+  for (int c0 = 16 * kTokLoads; c0 < npairs; c0 += 16 * kTokLoads) {
     uint4 v[kTokLoads];
 #pragma unroll
-    for (int j = 0; j < kTokLoads; ++j) v[j] = *(const uint4 *)(row + 2 * min(c0 + sub + 16 * j, npairs - 1));
-#pragma unroll
-    for (int j = 0; j < kTokLoads; ++j) {
-      const int c = min(c0 + sub + 16 * j, npairs - 1);      // a clamped pair repeats a pair: same maximum
-      const uint64_t k0 = ((uint64_t)v[j].y << 32) | v[j].x;
-      const uint64_t k1 = 2 * c + 1 < nb ? ((uint64_t)v[j].w << 32) | v[j].z : 0;  // odd tail: the stride's pad
-      best = max(best, max(k0, k1));
-    }
+    for (int j = 0; j < kTokLoads; ++j) v[j] = key_pairs(a, m, c0 + sub + 16 * j);
+    best = max_of_pairs(a, v, c0, sub, best);
   }
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) best = max(best, (uint64_t)__shfl_xor((unsigned long long)best, o, 16));
+  best = max(best, dpp_u64<0xB1>(best));
+  best = max(best, dpp_u64<0x4E>(best));
+  best = max(best, dpp_u64<0x141>(best));
+  best = max(best, dpp_u64<0x140>(best));
   return (int64_t)(0xFFFFFFFFu - (uint32_t)best);
 }
 
 template <int PRO, int CPQ, int MTB>
 __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int64_t m0, int nrows, int pad_rows,
-                                                 bool first_block, ActIn<CPQ, MTB> &in) {
+                                                 bool first_block, ActIn<CPQ, MTB> &in,
+                                                 const TokKeys<MTB> *keys = nullptr) {
   constexpr bool EMB = PRO == SMLM_LIN_EMBED_RMSNORM || PRO == SMLM_LIN_EMBED_ARGMAX;
   const int K = a.K, CH = K / 8;
   const int wave = threadIdx.x / kWave, lane = lane_id();
@@ -143,7 +188,7 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
     if constexpr (EMB) {
       int64_t t;
       if constexpr (PRO == SMLM_LIN_EMBED_ARGMAX) {
-        t = row_argmax_token(a, m, sub);
+        t = row_argmax_token(a, m, sub, keys->v[p]);
         if (writer && sub == 0 && rr < nrows) {
           if (a.tok_out) a.tok_out[m] = t;
           if (hslot >= 0 && hslot < a.hist_len) a.hist[m * a.hist_stride + hslot] = t;
@@ -381,7 +426,11 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   // ARGMAX with pos_advance: the first workgroup reads the position now and writes it + 1 at its end
   const bool advance = ARG && a.pos_advance != nullptr && blockIdx.x == 0;
   const int64_t pos_now = advance ? *a.pos_advance : 0;
-  if constexpr (PRO != SMLM_LIN_PLAIN && PRO != SMLM_LIN_RMSNORM_PARTS)
+  // EMBED_ARGMAX: the keys, then the weight fragments (in flight during the keys' reduction and the embedding rows'
+  // round trip), then the rows
+  TokKeys<PRO == SMLM_LIN_EMBED_ARGMAX ? MTB : 1> keys;
+  if constexpr (PRO == SMLM_LIN_EMBED_ARGMAX) load_token_keys<MTB>(a, m0, nrows, MT * 16, keys);
+  if constexpr (PRO != SMLM_LIN_PLAIN && PRO != SMLM_LIN_RMSNORM_PARTS && PRO != SMLM_LIN_EMBED_ARGMAX)
     load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, cb == 0, act);
   PartsIn<CPQ> parts_in;
   if constexpr (PRO == SMLM_LIN_RMSNORM_PARTS) load_parts<CPQ>(a, m0, nrows, parts_in);
@@ -396,6 +445,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       const int step = min(s_lo + min(s, ns - 1), nsteps - 1);
       areg[t][s] = *(const uint4 *)(wp + max(step, 0) * 32);
     }
+  }
+  if constexpr (PRO == SMLM_LIN_EMBED_ARGMAX) {
+    __builtin_amdgcn_sched_barrier(0);   // the keys' reduction stays behind the weight loads
+    load_activations<PRO, CPQ, MTB>(a, m0, nrows, MT * 16, cb == 0, act, &keys);
   }
 
   // 2. activations: PLAIN rows straight into registers; otherwise the prologue into LDS
