@@ -4,14 +4,17 @@
 // keys 0 .. S - T + t; y = softmax(q k^T / sqrt(hd)) v, bf16 in and out, fp32 statistics and accumulation.
 //
 // One workgroup = 128 queries of one (batch, head), 4 wavefronts x 32 queries; the keys go by in tiles of 64,
-// staged in LDS (keys row-major, values transposed).  Per tile each wavefront computes S^T = K Q^T on
-// v_mfma_f32_16x16x32_bf16 with the keys as the M operand and its queries as N, so a lane (r, g) holds keys
-// 4g..4g+3 of each 16-key tile for ONE query (r): the online softmax (running max m, sum l, rescale of the
-// output) is per lane, with the cross-lane max / sum over the four lane groups by permlane swaps.  Then
+// staged in LDS row-major (two buffers up to head_dim 64: one barrier per tile).  Per tile each wavefront computes
+// S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the keys as the M operand and its queries as N, so a lane (r, g)
+// holds keys 4g..4g+3 of each 16-key tile for ONE query (r): the online softmax (running max m, sum l, rescale of
+// the output) is per lane, with the cross-lane max / sum over the four lane groups by permlane swaps.  Then
 // O^T = V^T P^T with P^T straight from the score registers (rounded to bf16): the k slots of a 32-key step are
 // keys {4g..4g+3, 16+4g..16+4g+3} in lane group g for both operands, so the lane's own exp-scores ARE its B
-// operand, and V^T's A operand is two 8-byte reads of the transposed value tile.  The output fragment holds
-// d = 4g..4g+3 of query r, the same query as the statistics, so the final 1/l is per lane too.
+// operand, and V^T's A operand is two transposing 8-byte LDS reads (ds_read_b64_tr_b16) of the row-major value
+// tile: in each 16-lane group, lane i receives element i % 4 of the 8-byte chunks that lanes i / 4 + 4 j point
+// at (j = 0..3), so lane s pointing at value row key0 + s / 4, dims 16 mt + 4 (s % 4) .. +3 hands lane r the
+// four keys key0 .. key0 + 3 of dim 16 mt + r.  The output fragment holds d = 4g..4g+3 of query r, the same
+// query as the statistics, so the final 1/l is per lane too.
 #include <algorithm>
 
 #include "pkm_common.h"
@@ -21,6 +24,13 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// 4 consecutive 16-bit values of one column of a row-major LDS tile, transposed across lanes (see above)
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) short4_t *)(p)));
+}
 
 constexpr int kFaBM = 128;  // queries per workgroup
 constexpr int kFaBN = 64;   // keys per tile
@@ -43,10 +53,10 @@ __global__ void __launch_bounds__(256)
   constexpr int MT = HD / 16;           // 16-wide d tiles of the output
   constexpr int CPR = HD / 8;           // 16-byte chunks per key / value row
   constexpr int LPT = kFaBN * CPR / 256;  // chunks per thread per tile (of K, and of V)
-  constexpr int RS = HD + 8;            // sK row stride (bf16)
-  constexpr int VS = kFaBN + 8;         // sVt row stride (bf16)
-  __shared__ __align__(16) uint16_t sK[kFaBN * RS];
-  __shared__ __align__(16) uint16_t sVt[HD * VS];
+  constexpr int RS = HD + 8;            // sK / sV row stride (bf16)
+  constexpr int NBUF = HD <= 64 ? 2 : 1;  // tile buffers (static LDS stays under 64 KB)
+  __shared__ __align__(16) uint16_t sK[NBUF][kFaBN * RS];
+  __shared__ __align__(16) uint16_t sV[NBUF][kFaBN * RS];
 
   const int BH = B * H;
   const int ntq = (T + kFaBM - 1) / kFaBM;
@@ -117,119 +127,136 @@ __global__ void __launch_bounds__(256)
       vr[u] = key < S ? vv : uint4{0u, 0u, 0u, 0u};
     }
   };
-  load_tile(0);
-
-  for (int tk = 0; tk < ntk; ++tk) {
-    const int kv0 = tk * kFaBN;
-    __syncthreads();  // every wavefront is done with the previous tile
+  auto store_tile = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
       const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
-      *(uint4 *)&sK[row * RS + 8 * c] = kr[u];
-      const uint32_t w4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sVt[(8 * c + 2 * e) * VS + row] = (uint16_t)(w4[e] & 0xFFFFu);
-        sVt[(8 * c + 2 * e + 1) * VS + row] = (uint16_t)(w4[e] >> 16);
-      }
+      *(uint4 *)&sK[buf][row * RS + 8 * c] = kr[u];
+      *(uint4 *)&sV[buf][row * RS + 8 * c] = vr[u];
     }
-    if (tk + 1 < ntk) load_tile(kv0 + kFaBN);  // in flight during this tile's products
+  };
+  load_tile(0);
+  if constexpr (NBUF == 2) {  // tile 0 in buffer 0, tile 1 in flight
+    store_tile(0);
+    if (ntk > 1) load_tile(kFaBN);
     __syncthreads();
+  }
 
-    // wavefront-uniform: skip tiles none of this wavefront's queries reaches
-    if (!wave_on || kv0 > qpos_hi) continue;
-    const bool masked = kv0 + kFaBN - 1 > qpos_lo;
-
-    // S^T tile: sacc[kt][j][i] = q(query qw + 16 j + r) . k(key kv0 + 16 kt + 4 g + i)
-    floatx4 sacc[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) sacc[kt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      bf16x8 a[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) a[kt] = *(const bf16x8 *)&sK[(16 * kt + r) * RS + 32 * s + 8 * g];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          sacc[kt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kt], bq[j][s], sacc[kt][j], 0, 0, 0);
+  for (int tk = 0; tk < ntk; ++tk) {
+    const int kv0 = tk * kFaBN;
+    const int buf = NBUF == 2 ? tk & 1 : 0;
+    if constexpr (NBUF == 1) {
+      __syncthreads();  // every wavefront is done with the previous tile
+      store_tile(0);
+      if (tk + 1 < ntk) load_tile(kv0 + kFaBN);  // in flight during this tile's products
+      __syncthreads();
     }
 
-    // online softmax per query (lane), in the log2 domain.  The reference point m of the exponentials is raised
-    // (and the output and sum rescaled) only when some query of the wavefront has a tile maximum more than 2^8
-    // above it: until then the probabilities exp2(s - m) stay below 256, exact enough in fp32 and bf16, and the
-    // rescale, which costs as much as a tile's products, is skipped.  Every query sees key 0 in tile 0, so m is
-    // finite from the first tile on.
-    float mx[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int qpos = offset + qw + 16 * j + r;
-      if (masked) {
-#pragma unroll
+    // wavefront-uniform: tiles none of this wavefront's queries reaches are skipped
+    if (wave_on && kv0 <= qpos_hi) {
+      const bool masked = kv0 + kFaBN - 1 > qpos_lo;
+
+      // S^T tile: sacc[kt][j][i] = q(query qw + 16 j + r) . k(key kv0 + 16 kt + 4 g + i)
+      floatx4 sacc[4][2];
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int j = 0; j < 2; ++j) sacc[kt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        bf16x8 a[4];
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt) a[kt] = *(const bf16x8 *)&sK[buf][(16 * kt + r) * RS + 32 * s + 8 * g];
+  #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kv0 + 16 * kt + 4 * g + i;
-            if (key > qpos || key >= S) sacc[kt][j][i] = -__builtin_inff();
-          }
+  #pragma unroll
+          for (int j = 0; j < 2; ++j)
+            sacc[kt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kt], bq[j][s], sacc[kt][j], 0, 0, 0);
       }
-      float a = fmaxf(fmaxf(sacc[0][j][0], sacc[0][j][1]), fmaxf(sacc[0][j][2], sacc[0][j][3]));
-#pragma unroll
-      for (int kt = 1; kt < 4; ++kt)
-        a = fmaxf(a, fmaxf(fmaxf(sacc[kt][j][0], sacc[kt][j][1]), fmaxf(sacc[kt][j][2], sacc[kt][j][3])));
-      a = fmaxf(a, xor_lane_f(a, 16));
-      mx[j] = fmaxf(a, xor_lane_f(a, 32)) * scale_log2;
-    }
-    if (__builtin_amdgcn_ballot_w64(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {  // wavefront-uniform
-#pragma unroll
+
+      // online softmax per query (lane), in the log2 domain.  The reference point m of the exponentials is raised
+      // (and the output and sum rescaled) only when some query of the wavefront has a tile maximum more than 2^8
+      // above it: until then the probabilities exp2(s - m) stay below 256, exact enough in fp32 and bf16, and the
+      // rescale, which costs as much as a tile's products, is skipped.  Every query sees key 0 in tile 0, so m is
+      // finite from the first tile on.
+      float mx[2];
+  #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const float mnew = fmaxf(m[j], mx[j]);
-        const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
-        l[j] *= alpha;
-        m[j] = mnew;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
-      }
-    }
-    bf16x8 bp[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float ls = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - m[j]);
-          sacc[kt][j][i] = p;
-          ls += p;
+        const int qpos = offset + qw + 16 * j + r;
+        if (masked) {
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = kv0 + 16 * kt + 4 * g + i;
+              if (key > qpos || key >= S) sacc[kt][j][i] = -__builtin_inff();
+            }
         }
-      ls += xor_lane_f(ls, 16);
-      l[j] += xor_lane_f(ls, 32) + ls;
-      // P^T as B fragments: 32-key step ks = key tiles 2 ks and 2 ks + 1
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const floatx4 lo = sacc[2 * ks][j], hi = sacc[2 * ks + 1][j];
-        const uint4 pk{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
-                       pack_bf16x2(hi[2], hi[3])};
-        bp[j][ks] = __builtin_bit_cast(bf16x8, pk);
+        float a = fmaxf(fmaxf(sacc[0][j][0], sacc[0][j][1]), fmaxf(sacc[0][j][2], sacc[0][j][3]));
+  #pragma unroll
+        for (int kt = 1; kt < 4; ++kt)
+          a = fmaxf(a, fmaxf(fmaxf(sacc[kt][j][0], sacc[kt][j][1]), fmaxf(sacc[kt][j][2], sacc[kt][j][3])));
+        a = fmaxf(a, xor_lane_f(a, 16));
+        mx[j] = fmaxf(a, xor_lane_f(a, 32)) * scale_log2;
       }
+      if (__builtin_amdgcn_ballot_w64(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {  // wavefront-uniform
+  #pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float mnew = fmaxf(m[j], mx[j]);
+          const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
+          l[j] *= alpha;
+          m[j] = mnew;
+  #pragma unroll
+          for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
+        }
+      }
+      bf16x8 bp[2][2];
+  #pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float ls = 0.f;
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - m[j]);
+            sacc[kt][j][i] = p;
+            ls += p;
+          }
+        ls += xor_lane_f(ls, 16);
+        l[j] += xor_lane_f(ls, 32) + ls;
+        // P^T as B fragments: 32-key step ks = key tiles 2 ks and 2 ks + 1
+  #pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const floatx4 lo = sacc[2 * ks][j], hi = sacc[2 * ks + 1][j];
+          const uint4 pk{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
+                         pack_bf16x2(hi[2], hi[3])};
+          bp[j][ks] = __builtin_bit_cast(bf16x8, pk);
+        }
+      }
+
+      // O^T += V^T P^T: A fragment of d tile mt = values of d = 16 mt + r at the step's keys (same slot order),
+      // keys 32 ks + 4 g .. +3 (lo) and 32 ks + 16 + 4 g .. +3 (hi), by transposing reads (lane r % 4 of each
+      // quarter-row group points at row key0 + r / 4, dims 16 mt + 4 (r % 4) .. +3)
+  #pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+  #pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint16_t *src = &sV[buf][(32 * ks + 4 * g + r / 4) * RS + 16 * mt + 4 * (r % 4)];
+          const uint2 lo = lds_read_tr16(src), hi = lds_read_tr16(src + 16 * RS);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
+  #pragma unroll
+          for (int j = 0; j < 2; ++j)
+            oacc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[j][ks], oacc[mt][j], 0, 0, 0);
+        }
     }
 
-    // O^T += V^T P^T: A fragment of d tile mt = values of d = 16 mt + r at the step's keys (same slot order)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint16_t *row = &sVt[(16 * mt + r) * VS + 32 * ks + 4 * g];
-        const uint2 lo = *(const uint2 *)row, hi = *(const uint2 *)(row + 16);
-        const bf16x8 a = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          oacc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[j][ks], oacc[mt][j], 0, 0, 0);
+    if constexpr (NBUF == 2) {  // the next tile into the other buffer (free since the last barrier), one ahead
+      if (tk + 1 < ntk) {
+        store_tile(buf ^ 1);
+        if (tk + 2 < ntk) load_tile(kv0 + 2 * kFaBN);
       }
+      __syncthreads();
+    }
   }
 
   // y[query][d]: lane (r, g) holds d = 16 mt + 4 g .. +3 of query qw + 16 j + r
