@@ -6,8 +6,9 @@
 // One workgroup = 128 queries of one (batch, head), 4 wavefronts x 32 queries; the keys go by in tiles of 64,
 // staged in LDS row-major (two buffers up to head_dim 64: one barrier per tile).  Per tile each wavefront computes
 // S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with the keys as the M operand and its queries as N, so a lane (r, g)
-// holds keys 4g..4g+3 of each 16-key tile for ONE query (r): the online softmax (running max m, sum l, rescale of
-// the output) is per lane, with the cross-lane max / sum over the four lane groups by permlane swaps.  Then
+// holds keys 4g..4g+3 of each 16-key tile for ONE query (r): the online softmax (running max m, rescale of the
+// output) is per lane, with the cross-lane max over the four lane groups by permlane swaps, and the sums of the
+// probabilities accumulate on the matrix cores (a 1.0 operand times P^T).  Then
 // O^T = V^T P^T with P^T straight from the score registers (rounded to bf16): the k slots of a 32-key step are
 // keys {4g..4g+3, 16+4g..16+4g+3} in lane group g for both operands, so the lane's own exp-scores ARE its B
 // operand, and V^T's A operand is two transposing 8-byte LDS reads (ds_read_b64_tr_b16) of the row-major value
@@ -43,7 +44,7 @@ __device__ __forceinline__ float xor_lane_f(float v, int j) {
 }
 
 template <int HD>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 64 ? 3 : 2)))
     flash_attn_kernel(const uint16_t *__restrict__ q, int64_t qsb, int64_t qsh, int64_t qst,
                       const uint16_t *__restrict__ k, int64_t ksb, int64_t ksh, int64_t kst,
                       const uint16_t *__restrict__ v, int64_t vsb, int64_t vsh, int64_t vst,
@@ -90,7 +91,10 @@ __global__ void __launch_bounds__(256)
   const int qpos_hi = offset + min(T - 1, qw + 31);  // ... and of its last
 
   float m[2] = {-__builtin_inff(), -__builtin_inff()};
-  float l[2] = {0.f, 0.f};
+  // the sums of the probabilities come from the matrix cores: a 1.0 A operand times P^T puts each query's sum of
+  // its (bf16) probabilities in every row of the output tile, so no VALU additions or lane reductions are needed
+  floatx4 lacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   floatx4 oacc[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -158,18 +162,18 @@ __global__ void __launch_bounds__(256)
 
       // S^T tile: sacc[kt][j][i] = q(query qw + 16 j + r) . k(key kv0 + 16 kt + 4 g + i)
       floatx4 sacc[4][2];
-  #pragma unroll
+#pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < 2; ++j) sacc[kt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  #pragma unroll
+#pragma unroll
       for (int s = 0; s < KS; ++s) {
         bf16x8 a[4];
-  #pragma unroll
+#pragma unroll
         for (int kt = 0; kt < 4; ++kt) a[kt] = *(const bf16x8 *)&sK[buf][(16 * kt + r) * RS + 32 * s + 8 * g];
-  #pragma unroll
+#pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 2; ++j)
             sacc[kt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kt], bq[j][s], sacc[kt][j], 0, 0, 0);
       }
@@ -180,71 +184,65 @@ __global__ void __launch_bounds__(256)
       // rescale, which costs as much as a tile's products, is skipped.  Every query sees key 0 in tile 0, so m is
       // finite from the first tile on.
       float mx[2];
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int qpos = offset + qw + 16 * j + r;
         if (masked) {
-  #pragma unroll
+#pragma unroll
           for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
+#pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int key = kv0 + 16 * kt + 4 * g + i;
               if (key > qpos || key >= S) sacc[kt][j][i] = -__builtin_inff();
             }
         }
         float a = fmaxf(fmaxf(sacc[0][j][0], sacc[0][j][1]), fmaxf(sacc[0][j][2], sacc[0][j][3]));
-  #pragma unroll
+#pragma unroll
         for (int kt = 1; kt < 4; ++kt)
           a = fmaxf(a, fmaxf(fmaxf(sacc[kt][j][0], sacc[kt][j][1]), fmaxf(sacc[kt][j][2], sacc[kt][j][3])));
         a = fmaxf(a, xor_lane_f(a, 16));
         mx[j] = fmaxf(a, xor_lane_f(a, 32)) * scale_log2;
       }
       if (__builtin_amdgcn_ballot_w64(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {  // wavefront-uniform
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < 2; ++j) {
           const float mnew = fmaxf(m[j], mx[j]);
           const float alpha = __builtin_amdgcn_exp2f(m[j] - mnew);
-          l[j] *= alpha;
+          lacc[j] *= alpha;
           m[j] = mnew;
-  #pragma unroll
+#pragma unroll
           for (int mt = 0; mt < MT; ++mt) oacc[mt][j] *= alpha;
         }
       }
       bf16x8 bp[2][2];
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < 2; ++j) {
-        float ls = 0.f;
-  #pragma unroll
+#pragma unroll
         for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - m[j]);
-            sacc[kt][j][i] = p;
-            ls += p;
-          }
-        ls += xor_lane_f(ls, 16);
-        l[j] += xor_lane_f(ls, 32) + ls;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sacc[kt][j][i] = __builtin_amdgcn_exp2f(sacc[kt][j][i] * scale_log2 - m[j]);
         // P^T as B fragments: 32-key step ks = key tiles 2 ks and 2 ks + 1
-  #pragma unroll
+#pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           const floatx4 lo = sacc[2 * ks][j], hi = sacc[2 * ks + 1][j];
           const uint4 pk{pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
                          pack_bf16x2(hi[2], hi[3])};
           bp[j][ks] = __builtin_bit_cast(bf16x8, pk);
+          lacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, bp[j][ks], lacc[j], 0, 0, 0);
         }
       }
 
       // O^T += V^T P^T: A fragment of d tile mt = values of d = 16 mt + r at the step's keys (same slot order),
       // keys 32 ks + 4 g .. +3 (lo) and 32 ks + 16 + 4 g .. +3 (hi), by transposing reads (lane r % 4 of each
       // quarter-row group points at row key0 + r / 4, dims 16 mt + 4 (r % 4) .. +3)
-  #pragma unroll
+#pragma unroll
       for (int ks = 0; ks < 2; ++ks)
-  #pragma unroll
+#pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const uint16_t *src = &sV[buf][(32 * ks + 4 * g + r / 4) * RS + 16 * mt + 4 * (r % 4)];
           const uint2 lo = lds_read_tr16(src), hi = lds_read_tr16(src + 16 * RS);
           const bf16x8 a = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < 2; ++j)
             oacc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bp[j][ks], oacc[mt][j], 0, 0, 0);
         }
@@ -265,7 +263,7 @@ __global__ void __launch_bounds__(256)
   for (int j = 0; j < 2; ++j) {
     const int t = qw + 16 * j + r;
     if (t >= T) continue;
-    const float inv = 1.0f / l[j];
+    const float inv = 1.0f / lacc[j][0];
     uint16_t *yr = y + b * ysb + h * ysh + (int64_t)t * yst;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
