@@ -235,7 +235,8 @@ int smlm_rope_qkv(const void *qkv, int64_t qkv_row_stride, const void *rope_cos,
  * bf16 operands, fp32 scores / softmax statistics / accumulation, probabilities rounded to bf16 for the value
  * product, y rounded to bf16.  Element (b, h, t, d) of q is at q + b*q_strides[0] + h*q_strides[1] + t*q_strides[2]
  * + d (d contiguous); likewise k, v (t < S) and y with its own strides.  q, k, v 16-byte aligned with strides that
- * are multiples of 8 elements; y 8-byte aligned, strides multiples of 4.  head_dim in {32, 64, 128}; S >= T.
+ * are multiples of 8 elements; y 8-byte aligned, strides multiples of 4.  head_dim in {32, 64, 128}; S >= T;
+ * (S + 64) x the larger key / value token stride x 2 bytes below 2^31 (SMLM_EUNSUPPORTED otherwise).
  */
 int smlm_prefill_attention(const void *q, const int64_t *q_strides, const void *k, const int64_t *k_strides,
                            const void *v, const int64_t *v_strides, void *y, const int64_t *y_strides, int64_t B,

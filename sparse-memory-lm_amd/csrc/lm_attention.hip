@@ -54,10 +54,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 
   constexpr int MT = HD / 16;           // 16-wide d tiles of the output
   constexpr int CPR = HD / 8;           // 16-byte chunks per key / value row
   constexpr int LPT = kFaBN * CPR / 256;  // chunks per thread per tile (of K, and of V)
-  constexpr int RS = HD + 8;            // sK / sV row stride (bf16)
-  constexpr int NBUF = HD <= 64 ? 2 : 1;  // tile buffers (static LDS stays under 64 KB)
-  __shared__ __align__(16) uint16_t sK[NBUF][kFaBN * RS];
-  __shared__ __align__(16) uint16_t sV[NBUF][kFaBN * RS];
+  constexpr int RB = CPR * 16;          // bytes per key / value row in LDS
+  constexpr int SW = CPR < 8 ? CPR : 8;  // chunk c of row r sits in slot c ^ (r % SW): conflict-free fragment reads
+  __shared__ __align__(16) uint16_t sK[2][kFaBN * HD];
+  __shared__ __align__(16) uint16_t sV[2][kFaBN * HD];
 
   const int BH = B * H;
   const int ntq = (T + kFaBM - 1) / kFaBM;
@@ -101,60 +101,34 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 
 #pragma unroll
     for (int j = 0; j < 2; ++j) oacc[mt][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // tile loads: chunk id = tid + 256 u -> row id / CPR, 16-byte chunk id % CPR.  Whole tiles read through row
-  // pointers set up once; the last, partial tile clamps its rows into range and loads rows past S as zeros.
-  uint4 kr[LPT], vr[LPT];
-  const uint16_t *kp[LPT], *vp[LPT];
-#pragma unroll
-  for (int u = 0; u < LPT; ++u) {
-    const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
-    kp[u] = kb + row * kst + 8 * c;
-    vp[u] = vb + row * vst + 8 * c;
-  }
-  auto load_tile = [&](int kv0) {
-    if (kv0 + kFaBN <= S) {  // workgroup-uniform
-#pragma unroll
-      for (int u = 0; u < LPT; ++u) {
-        kr[u] = *(const uint4 *)(kp[u] + kv0 * kst);
-        vr[u] = *(const uint4 *)(vp[u] + kv0 * vst);
-      }
-      return;
-    }
+  // tile loads straight into LDS (buffer loads with the LDS bit: lane i of a wavefront's load writes bytes 16 i ..
+  // 16 i + 15 of the wavefront's 1 KB piece): LDS chunk id = tid + 256 u is slot id % CPR of row id / CPR, which
+  // holds the row's global chunk slot ^ (row % SW).  The buffers end at row S - 1, so the rows of a partial last
+  // tile past S read as zeros.
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)kb, (short)0, (int)(((int64_t)(S - 1) * kst + HD) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)vb, (short)0, (int)(((int64_t)(S - 1) * vst + HD) * 2), 0x00020000);
+  auto load_tile = [&](int kv0, int buf) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
-      const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
+      const int id = tid + 256 * u, row = id / CPR, c = (id % CPR) ^ (row % SW);
       const int key = kv0 + row;
-      const int64_t kk = min(key, S - 1);
-      const uint4 kv = *(const uint4 *)(kb + kk * kst + 8 * c);
-      const uint4 vv = *(const uint4 *)(vb + kk * vst + 8 * c);
-      kr[u] = key < S ? kv : uint4{0u, 0u, 0u, 0u};
-      vr[u] = key < S ? vv : uint4{0u, 0u, 0u, 0u};
+      const int piece = (256 * u + wave * kWave) * 16;  // this wavefront's 1 KB of the tile
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (__attribute__((address_space(3))) void *)((char *)sK[buf] + piece),
+                                               16, (int)((key * kst + 8 * c) * 2), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (__attribute__((address_space(3))) void *)((char *)sV[buf] + piece),
+                                               16, (int)((key * vst + 8 * c) * 2), 0, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int id = tid + 256 * u, row = id / CPR, c = id % CPR;
-      *(uint4 *)&sK[buf][row * RS + 8 * c] = kr[u];
-      *(uint4 *)&sV[buf][row * RS + 8 * c] = vr[u];
-    }
-  };
-  load_tile(0);
-  if constexpr (NBUF == 2) {  // tile 0 in buffer 0, tile 1 in flight
-    store_tile(0);
-    if (ntk > 1) load_tile(kFaBN);
-    __syncthreads();
-  }
+  load_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's pieces of tile 0 are in LDS ...
+  __syncthreads();                // ... and everyone's
 
   for (int tk = 0; tk < ntk; ++tk) {
     const int kv0 = tk * kFaBN;
-    const int buf = NBUF == 2 ? tk & 1 : 0;
-    if constexpr (NBUF == 1) {
-      __syncthreads();  // every wavefront is done with the previous tile
-      store_tile(0);
-      if (tk + 1 < ntk) load_tile(kv0 + kFaBN);  // in flight during this tile's products
-      __syncthreads();
-    }
+    const int buf = tk & 1;
+    if (tk + 1 < ntk) load_tile(kv0 + kFaBN, buf ^ 1);  // into the buffer every wavefront left at the last barrier
 
     // wavefront-uniform: tiles none of this wavefront's queries reaches are skipped
     if (wave_on && kv0 <= qpos_hi) {
@@ -170,7 +144,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 
       for (int s = 0; s < KS; ++s) {
         bf16x8 a[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) a[kt] = *(const bf16x8 *)&sK[buf][(16 * kt + r) * RS + 32 * s + 8 * g];
+        for (int kt = 0; kt < 4; ++kt) {
+        const int row = 16 * kt + r;
+        a[kt] = *(const bf16x8 *)((const char *)sK[buf] + row * RB + (((4 * s + g) ^ (row % SW)) * 16));
+      }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -239,8 +216,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const uint16_t *src = &sV[buf][(32 * ks + 4 * g + r / 4) * RS + 16 * mt + 4 * (r % 4)];
-          const uint2 lo = lds_read_tr16(src), hi = lds_read_tr16(src + 16 * RS);
+          const int row = 32 * ks + 4 * g + r / 4, dim = 16 * mt + 4 * (r % 4);
+          const char *src = (const char *)sV[buf] + row * RB + (((dim / 8) ^ (row % SW)) * 16) + (dim % 8) * 2;
+          const uint2 lo = lds_read_tr16((const uint16_t *)src),
+                      hi = lds_read_tr16((const uint16_t *)(src + 16 * RB));  // row + 16: the same swizzle
           const bf16x8 a = __builtin_bit_cast(bf16x8, uint4{lo.x, lo.y, hi.x, hi.y});
 #pragma unroll
           for (int j = 0; j < 2; ++j)
@@ -248,13 +227,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD <= 
         }
     }
 
-    if constexpr (NBUF == 2) {  // the next tile into the other buffer (free since the last barrier), one ahead
-      if (tk + 1 < ntk) {
-        store_tile(buf ^ 1);
-        if (tk + 2 < ntk) load_tile(kv0 + 2 * kFaBN);
-      }
-      __syncthreads();
-    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's pieces of the next tile are in LDS ...
+    __syncthreads();                // ... and everyone's; every wavefront is done with this tile
   }
 
   // y[query][d]: lane (r, g) holds d = 16 mt + 4 g .. +3 of query qw + 16 j + r
@@ -442,6 +416,11 @@ extern "C" int smlm_prefill_attention(const void *q, const int64_t *q_strides, c
                                  "for y); got %lld", (long long)st[a][i]);
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) % 16 || (uintptr_t)y % 8)
     return fail(SMLM_EINVAL, "smlm_prefill_attention: q, k, v must be 16-byte and y 8-byte aligned");
+  // the key / value tiles are read through 32-bit buffer offsets from each (batch, head)'s first row
+  const int64_t row_stride = k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2];
+  if (((int64_t)S + kFaBN) * row_stride * 2 + 2 * head_dim > 0x7FFFFFFFLL)
+    return fail(SMLM_EUNSUPPORTED, "smlm_prefill_attention: S=%d keys x row stride %lld elements exceed the 2 GB a "
+                "(batch, head)'s key or value rows may span", S, (long long)row_stride);
   if (B == 0 || T == 0) return SMLM_OK;
   hipStream_t s = (hipStream_t)stream;
   const int b = (int)B;
