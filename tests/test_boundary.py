@@ -176,6 +176,21 @@ def test_embed_argmax_prologue_argument_checks():
     assert lib.smlm_decode_linear(ctypes.byref(a), None) == _lib.EINVAL and "M >= 1" in _lib.last_error()
 
 
+def test_prefill_attention_argument_checks():
+    """smlm_prefill_attention refuses bad arguments before any launch, among them key / value rows that a 32-bit
+    buffer offset from a (batch, head)'s first row cannot reach."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    st = (ctypes.c_int64 * 3)(6 * 4096 * 64, 4096 * 64, 64)            # (B, H, S, 64) contiguous
+    args = [fake, st, fake, st, fake, st, fake, st]
+    assert lib.smlm_prefill_attention(*args, 0, 6, 128, 4096, 64, None) == _lib.OK          # B = 0: a no-op
+    assert lib.smlm_prefill_attention(*args, 0, 6, 128, 4096, 48, None) == _lib.EUNSUPPORTED  # head_dim
+    assert lib.smlm_prefill_attention(*args, 0, 6, 5000, 4096, 64, None) == _lib.EINVAL       # S < T
+    big = (ctypes.c_int64 * 3)(0, 0, 1 << 20)                            # 2^14 keys x 2 MB per row
+    assert lib.smlm_prefill_attention(fake, st, fake, big, fake, st, fake, st, 0, 1, 1, 1 << 14, 64,
+                                      None) == _lib.EUNSUPPORTED and "2 GB" in _lib.last_error()
+
+
 def test_parts_prologue_and_attention_proj_argument_checks():
     """The RMSNORM_PARTS prologue and smlm_decode_attention_proj refuse bad arguments before any launch."""
     lib = _lib.lib()
