@@ -122,10 +122,10 @@ __device__ __forceinline__ void unpack8(const uint4 v, float *f) {
 }
 
 // Passes of wo rows the projection (PROJ) holds in registers, loaded before the cache rows are used (one pass =
-// threads / (head_dim / 8) rows: with 1024 threads and head_dim 64, 3 passes = 384 rows, a d_model 384 model's
-// whole slice; more would spill registers of the 1024-thread workgroup).
+// threads / (head_dim / 8) rows: with 512 threads and head_dim 64, 6 passes = 384 rows, a d_model 384 model's
+// whole slice).
 template <int kAttnThreads>
-constexpr int wo_regs() { return kAttnThreads >= 1024 ? 3 : kAttnThreads >= 512 ? 6 : 12; }
+constexpr int wo_regs() { return kAttnThreads >= 512 ? 6 : 12; }
 
 template <int N>
 struct IntC {
@@ -172,9 +172,8 @@ __global__ void __launch_bounds__(kAttnThreads)
   constexpr int HALF = HD / 2;           // RoPE rotates dim i with dim i + HALF
   constexpr int WR = wo_regs<kAttnThreads>();
   constexpr int RPP = kAttnThreads / LPR;  // wo rows per projection pass (LPR lanes per row, 8 columns each)
-  // (the projection's wo registers leave room for 6 passes under the 128 VGPRs of a 1024-thread workgroup)
   // (the online softmax rescales per group, so the plain and PROJ variants group alike to reach the same y)
-  constexpr int U = kAttnThreads >= 1024 ? 6 : kAttnUnroll;
+  constexpr int U = kAttnUnroll;
   extern __shared__ __align__(16) float smem[];
   float *s_y = smem;                     // [HD] the bf16-rounded output (PROJ)
   float *s_red = s_y + HD;               // [kAttnWaves][HD] the wavefronts' rotated q, later their sums of p * v
@@ -446,14 +445,15 @@ int launch_attention_nt(const AttnArgs &a, hipStream_t stream) {
   return launch_status("smlm_decode_attention");
 }
 
-// 256 threads per (sequence, head) when those workgroups fill the chip twice over; 512 from one workgroup per CU up
-// (two of them still fit a CU: batch 64 x 6 heads, 0.212 -> 0.206 ms per decode step); otherwise (small decode
-// batches) 1024, so each workgroup's rows are spread over more lanes and its chain of loads and reductions is shorter.
+// 256 threads per (sequence, head) when those workgroups fill the chip twice over, 512 below that (batch 64 x 6
+// heads: 0.212 -> 0.206 ms per decode step against 256).  Small batches ran 1024 threads per head until the
+// per-wavefront work (its own RoPE, the row-group sums before the merge) outweighed the per-pass arithmetic: with 16
+// wavefronts the CU's SIMDs each ran four of those fixed costs; 512 threads measured 127.6 -> 126.6 us per step at
+// batch 1 and 135.8 -> 134.0 / 139.6 -> 138.2 / 156.3 -> 155.6 us at batches 8 / 16 / 32 (256: 130.2 at batch 1).
 template <int HD, bool PROJ>
 int launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (a.B * a.H >= 512) return launch_attention_nt<HD, 256, PROJ>(a, stream);
-  if (a.B * a.H >= 256) return launch_attention_nt<HD, 512, PROJ>(a, stream);
-  return launch_attention_nt<HD, 1024, PROJ>(a, stream);
+  return launch_attention_nt<HD, 512, PROJ>(a, stream);
 }
 
 template <bool PROJ>

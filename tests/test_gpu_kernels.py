@@ -364,10 +364,10 @@ def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
                                                     (2, 6, 64, 800, 768, "bf16"), (2, 6, 64, 800, 769, "f32"),
                                                     (100, 6, 64, 300, 256, "bf16"), (100, 6, 64, 300, 257, "bf16")])
 def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
-    """1024 / 512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the
-    last slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second
-    round trip); positions on and just past a pass or a group boundary of each thread count (512 threads: 64 rows a
-    pass, 512 a group; 1024: 128 and 768; 256: 32 and 256)."""
+    """512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the last
+    slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second round
+    trip); positions on and just past a pass or a group boundary of each thread count (512 threads: 64 rows a pass,
+    512 a group; 256: 32 and 256)."""
     note(f"decode attention B={B} H={H} hd={hd} max_len={max_len} P={P}")
     g = torch.Generator().manual_seed(B * 1000 + P)
     C = H * hd
