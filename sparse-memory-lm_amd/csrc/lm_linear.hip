@@ -420,6 +420,23 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int col0 = ARG ? cb * kArgCols + wave * kArgTiles * 16 : cb * 16;
   const uint16_t *W = (const uint16_t *)a.w;
 
+  // STORE epilogue parameters (bias, affine scale / shift) of wavefront 0's 4 columns, loaded before everything
+  // else: read in the epilogue they would add a memory round trip of their own after the products
+  float ep_bias[4] = {0.f, 0.f, 0.f, 0.f}, ep_sc[4] = {1.f, 1.f, 1.f, 1.f}, ep_sh[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (EPI == SMLM_LIN_STORE) {
+    const int c = col0 + 4 * g;
+    if (ks == 0 && c < cols) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (a.bias) ep_bias[e] = bf16_bits_to_f32(((const uint16_t *)a.bias)[c + e]);
+        if (c < a.n_affine) {
+          ep_sc[e] = a.scale[c + e];
+          ep_sh[e] = a.shift[c + e];
+        }
+      }
+    }
+  }
+
   // 1. the prologue's loads, then the weight fragments (rows past N and steps past the slice re-read valid memory;
   // their products are unused): the prologue's arithmetic then overlaps the weights' arrival
   ActIn<CPQ, PRO == SMLM_LIN_PLAIN ? 1 : MTB> act;
@@ -537,16 +554,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int c = col0 + 4 * g;  // this lane's 4 columns c .. c+3 of tile 0 (cols % 16 == 0: all in or all out)
   if constexpr (EPI == SMLM_LIN_STORE) {
     if (c >= cols) return;
-    float bias[4] = {0.f, 0.f, 0.f, 0.f}, sc[4] = {1.f, 1.f, 1.f, 1.f}, sh[4] = {0.f, 0.f, 0.f, 0.f};
     const bool affine = c < a.n_affine;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (a.bias) bias[e] = bf16_bits_to_f32(((const uint16_t *)a.bias)[c + e]);
-      if (affine) {
-        sc[e] = a.scale[c + e];
-        sh[e] = a.shift[c + e];
-      }
-    }
     const bool first = c < a.n_split;
     uint16_t *dst = first ? (uint16_t *)a.out + c : (uint16_t *)a.out2 + (c - a.n_split);
     const int64_t stride = first ? a.out_stride : a.out2_stride;
@@ -557,8 +565,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        v[e] = acc[0][mt][e] + bias[e];
-        if (affine) v[e] = fmaf(round_bf16_hw(v[e]), sc[e], sh[e]);
+        v[e] = acc[0][mt][e] + ep_bias[e];
+        if (affine) v[e] = fmaf(round_bf16_hw(v[e]), ep_sc[e], ep_sh[e]);
       }
       *(uint2 *)(dst + (m0 + tok) * stride) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }

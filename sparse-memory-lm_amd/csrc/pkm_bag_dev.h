@@ -85,15 +85,21 @@ __device__ __forceinline__ void stage_lookups(const void *__restrict__ idx, cons
   }
 }
 
-__device__ __forceinline__ void store_out(void *out, int64_t o, float a, bool bad, const uint16_t *pre,
-                                          bool out_bf16) {
+// out[o] = a (NaN for a bad token), times bf16(silu(pre)) when has_pre (pre_bits = the bf16 bits of pre[o])
+__device__ __forceinline__ void store_out_bits(void *out, int64_t o, float a, bool bad, bool has_pre,
+                                               uint16_t pre_bits, bool out_bf16) {
   if (bad) a = __builtin_nanf("");
-  if (pre) {
-    const float p = bf16_bits_to_f32(pre[o]);
+  if (has_pre) {
+    const float p = bf16_bits_to_f32(pre_bits);
     a *= round_bf16(p / (1.0f + expf(-p)));  // bf16(silu(pre)), as smlm/kernels.py:304-307
   }
   if (out_bf16) ((uint16_t *)out)[o] = (uint16_t)bf16_bits_rtne(a);
   else ((float *)out)[o] = a;
+}
+
+__device__ __forceinline__ void store_out(void *out, int64_t o, float a, bool bad, const uint16_t *pre,
+                                          bool out_bf16) {
+  store_out_bits(out, o, a, bad, pre != nullptr, pre ? pre[o] : (uint16_t)0, out_bf16);
 }
 
 // Rows of a token's staged lookups [0, kc) accumulated by a workgroup laid out as row slots x cpr chunk columns:

@@ -649,6 +649,9 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   const int64_t row = n * H + h;
   const size_t esz = F32 ? 4 : 2;
   if (tid == 0) s_bad = 0;
+  // the swilu input of the first output column this thread stores, loaded now: read at the end it would add a
+  // memory round trip after the gather
+  const uint16_t pre_first = pre && tid < D ? pre[n * D + tid] : (uint16_t)0;
   const void *src = (const char *)(p ? s2 : s1) + row * (int64_t)NK * esz;
   Key *sel = s_sel + wave * kMaxKnn, *top = s_top + wave * kMaxKnn;
   uint32_t pc[kMaxPairSlots];
@@ -698,7 +701,8 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   for (int col = tid; col < D; col += blockDim.x) {
     float a = 0.f;
     for (int r = 0; r < rpr; ++r) a += s_red[r * D + col];
-    bag::store_out(out, n * D + col, a, bad, pre, out_bf16 != 0);
+    const uint16_t pb = col == tid ? pre_first : pre ? pre[n * D + col] : (uint16_t)0;
+    bag::store_out_bits(out, n * D + col, a, bad, pre != nullptr, pb, out_bf16 != 0);
   }
 }
 
