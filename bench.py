@@ -36,6 +36,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 import traceback
 
@@ -228,21 +229,25 @@ def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
             "launch_frac": launch_ms / ms_per_step}
 
 
-def time_prefill(model, B, T, reps, dev, seed=3):
+def time_prefill(model, B, T, reps, dev, seed=3, graphed=False):
     """Config 2 prefill: the LM forward (no cache) over B uniform prompts of T tokens; median wall time of `reps`
-    forwards after 2 warm-ups, each synchronised."""
+    forwards after 2 warm-ups, each synchronised.  graphed: Transformer.forward_graphed (the same kernels, the
+    pass captured once and replayed; the capture happens in the warm-ups)."""
     import torch
     g = torch.Generator(device=dev).manual_seed(seed)
     prompt = torch.randint(0, model.cfg.vocab_size, (B, T), generator=g, device=dev)
+    fwd = model.forward_graphed if graphed else model
     times = []
     with torch.no_grad():
         for i in range(2 + reps):
             torch.cuda.synchronize(dev)
             t0 = time.perf_counter()
-            model(prompt)
+            fwd(prompt)
             torch.cuda.synchronize(dev)
             if i >= 2:
                 times.append(time.perf_counter() - t0)
+    if graphed:
+        model.drop_graphs()
     times.sort()
     ms = 1000.0 * times[len(times) // 2]
     return B * T / ms * 1e3, ms
@@ -917,10 +922,20 @@ def main():
 
         def prefill():
             m2 = build_lm(lm_config(2048, 2048), dev)
-            tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
-            out = {"tok_s": tok_s, "ms_per_forward": ms, "batch": 8, "seq_len": 2048,
+            import torch.cuda.tunable as tunable
+            # PyTorch's TunableOp: the dense GEMMs (hipBLASLt / rocBLAS candidates) timed per shape at first use,
+            # in the warm-up forwards, before the graph capture
+            tunable.enable(True)
+            tunable.tuning_enable(True)
+            tunable.set_filename(os.path.join(tempfile.gettempdir(), f"smlm_tunableop_{os.getpid()}.csv"))
+            tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev, graphed=True)
+            tok_e, ms_e = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
+            tunable.enable(False)
+            out = {"tok_s": tok_s, "ms_per_forward": ms, "graphed": True, "tunableop": True, "eager_tok_s": tok_e,
+                   "eager_ms_per_forward": ms_e, "batch": 8, "seq_len": 2048,
                    "table": "4,194,304 x 384 bf16 (B-4M)", "attention": prefill_attention_kernel(dev, args.reps)}
-            log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward)")
+            log(f"prefill config 2 (B-4M, 8 x 2048): {tok_s:.0f} tok/s ({ms:.2f} ms per forward, graph replay; "
+                f"eager {tok_e:.0f} tok/s, {ms_e:.2f} ms)")
             if "cpu" in phases:
                 out["cpu_baseline"] = cpu_prefill_c2(m2)
                 log(f"cpu baseline config 2: {out['cpu_baseline']}")

@@ -294,6 +294,7 @@ class Transformer(nn.Module):
         self.ngram = (NgramHash(cfg.vocab_size, cfg.eng_orders, cfg.eng_heads, cfg.eng_rows, cfg.eng_hash_seed,
                                 canon=ngram_canon) if cfg.eng_layers else None)
         self._decoders = {}
+        self._fwd_graphs = {}
         self._init_weights()
 
     @torch.no_grad()
@@ -361,6 +362,7 @@ class Transformer(nn.Module):
             else:
                 raise ValueError(kind)
         self._decoders.clear()
+        self._fwd_graphs.clear()
 
     def forward(self, idx, targets=None, kv_caches=None, pos0=0):
         """Logits (B, T, vocab), or (logits, loss) with targets (smlm/model.py:266-293)."""
@@ -377,6 +379,39 @@ class Transformer(nn.Module):
             return logits
         loss = F.cross_entropy(logits.float().view(-1, logits.size(-1)), targets.reshape(-1))
         return logits, loss
+
+    @torch.no_grad()
+    def forward_graphed(self, idx):
+        """forward(idx) (logits, no cache, no targets) from a HIP graph captured once per input shape, device and
+        autocast state and replayed: the same kernels as the eager forward without a host launch per op (a prompt
+        pass of ~60 launches).  The returned logits are the graph's static output, overwritten by the next call
+        with the same shape; clone them to keep them.  Parameters are read where they live, so updated weights
+        are seen; set_memory_inference_table drops the graphs."""
+        ac = torch.is_autocast_enabled("cuda")
+        key = (tuple(idx.shape), str(idx.device), ac, torch.get_autocast_dtype("cuda") if ac else None)
+        entry = self._fwd_graphs.get(key)
+        if entry is None:
+            static_idx = idx.clone()
+            ctx = (torch.autocast("cuda", dtype=key[3], cache_enabled=False) if ac
+                   else torch.autocast("cuda", enabled=False))
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side), ctx:
+                for _ in range(2):             # lazily built state (library handles, cached affines) first
+                    self(static_idx)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph), ctx:
+                static_out = self(static_idx)
+            entry = self._fwd_graphs[key] = (graph, static_idx, static_out)
+        graph, static_idx, static_out = entry
+        static_idx.copy_(idx)
+        graph.replay()
+        return static_out
+
+    def drop_graphs(self):
+        """Forget the captured forward graphs (and their memory)."""
+        self._fwd_graphs.clear()
 
     def _ngram_rows(self, idx, kv_caches):
         """Engram rows of this chunk (smlm/model.py:270-279): the hash sees the last history tokens before the

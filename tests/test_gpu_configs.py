@@ -215,6 +215,28 @@ def test_config2_prefill_forward_b4m():
     torch.cuda.empty_cache()
 
 
+@torch.no_grad()
+def test_forward_graphed_equals_eager():
+    """Transformer.forward_graphed (the prompt pass captured once per shape and replayed) gives the eager forward's
+    logits bit for bit: the configs' LM with a small memory table, two prompts of one shape replayed in turn with
+    eager forwards between the replays, and a second shape (its own graph)."""
+    note("forward_graphed: configs LM, NK 256")
+    model = build_lm(256, 512)
+    g = torch.Generator().manual_seed(5)
+    p1, p2 = (torch.randint(0, 32000, (2, 300), generator=g).to(DEV) for _ in range(2))
+    p3 = torch.randint(0, 32000, (3, 100), generator=g).to(DEV)
+    e1, e2, e3 = model(p1), model(p2), model(p3)
+    for prompt, eager in ((p1, e1), (p2, e2), (p1, e1), (p3, e3), (p2, e2)):
+        got = model.forward_graphed(prompt).clone()
+        model(p3)                                       # eager work between the replays
+        assert np.array_equal(bits(got), bits(eager))
+    assert len(model._fwd_graphs) == 2
+    model.set_memory_inference_table("bf16")             # a table switch drops the graphs
+    assert len(model._fwd_graphs) == 0
+    del model
+    torch.cuda.empty_cache()
+
+
 # --------------------------------------------------------------------------------------------- config 4
 @torch.no_grad()
 def test_config4_full_int8_table_gather():
