@@ -85,7 +85,7 @@ def time_generations(model, B, reps, warmup, dev, prompt_len=128, new_tokens=GEN
     """The decode loop of smlm/train.py:283-301 at batch B: prefill B uniform prompts of prompt_len tokens once
     (untimed), then `warmup` untimed and `reps` timed generations of `new_tokens` greedy tokens each, every one
     starting from the prompt's first sampled token and bracketed by synchronisations.  A generation is
-    new_tokens / steps_per_graph replays of the captured whole-step graph (each step reads and advances its
+    new_tokens / 32 replays of the captured 32-step graph (_StepDecoder.run_lengths; each step reads and advances its
     position and token on the device).  Greedy decoding is deterministic, so every repetition must produce the
     same tokens; that is checked.  Returns (tok/s, ms per generation, ms per token step)."""
     import torch

@@ -128,12 +128,12 @@ def decode_parity(model, B, P, steps, seed):
         worst = max(worst, err)
     note(f"  logits within {worst:.2e} of their scale ({sub.shape[0]} distinct rows pulled)")
 
-    # the whole-step graph from the same state gives the same tokens (runs of 8 steps, then single steps)
+    # the whole-step graphs from the same state give the same tokens (runs of 8 steps, then single steps)
     dec.hist[:, P + 1:] = -1
     dec.start(first, P)
     dec.replay(steps)
     torch.cuda.synchronize()
-    assert _StepDecoder.steps_per_graph == 8
+    assert 8 in _StepDecoder.run_lengths
     assert torch.equal(dec.hist[:, P:P + steps + 1], eager), "graph replays differ from the eager steps"
 
 

@@ -422,20 +422,20 @@ def test_fused_step_head_counts(n_heads):
 @pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
 def test_fused_generate_multi_step_graph_matches_eager(monkeypatch, proj_max):
-    """generate() on the fused step: the graph of steps_per_graph steps in a row plus single-step replays (19
-    tokens = 2 runs of 8 + 3 single steps) gives the eager loop's tokens exactly, on every call."""
+    """generate() on the fused step: the graphs of several steps in a row plus single-step replays (45 tokens =
+    a run of 32 + a run of 8 + 5 single steps) give the eager loop's tokens exactly, on every call."""
     from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep, _StepDecoder
     monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=1024, d_model=384, n_layers=3, n_heads=6, ffn_hidden=1024, max_seq_len=64)
     torch.manual_seed(1)
     m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
-    assert _StepDecoder.steps_per_graph == 8
+    assert _StepDecoder.run_lengths == (32, 8)
     prompt = torch.randint(0, 1024, (2, 9), generator=torch.Generator().manual_seed(5)).to(DEV)
     note(f"fused generate multi-step graph B=2 proj_max_batch={proj_max}")
-    eager = m.generate(prompt, 19, use_graph=False)
-    graph = m.generate(prompt, 19, use_graph=True)
-    graph2 = m.generate(prompt, 19, use_graph=True)
-    assert eager.shape == (2, 20)
+    eager = m.generate(prompt, 45, use_graph=False)
+    graph = m.generate(prompt, 45, use_graph=True)
+    graph2 = m.generate(prompt, 45, use_graph=True)
+    assert eager.shape == (2, 46)
     assert torch.equal(graph, eager) and torch.equal(graph2, eager)
 
 
