@@ -928,8 +928,8 @@ def main():
             tunable.enable(True)
             tunable.tuning_enable(True)
             tunable.set_filename(os.path.join(tempfile.gettempdir(), f"smlm_tunableop_{os.getpid()}.csv"))
-            tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev, graphed=True)
             tok_e, ms_e = time_prefill(m2, 8, 2048, args.prefill_reps, dev)
+            tok_s, ms = time_prefill(m2, 8, 2048, args.prefill_reps, dev, graphed=True)
             tunable.enable(False)
             out = {"tok_s": tok_s, "ms_per_forward": ms, "graphed": True, "tunableop": True, "eager_tok_s": tok_e,
                    "eager_ms_per_forward": ms_e, "batch": 8, "seq_len": 2048,
