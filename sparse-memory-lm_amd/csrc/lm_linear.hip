@@ -223,6 +223,10 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
 // between the sum and the norm, and the group's rows are normalised by four wavefronts at once.
 constexpr int kMaxParts = 8;
 constexpr int kPartsRows = kLinWaves;
+// PLAIN prologue over more than 384 inputs (the FFN down projection): 8-row token groups, so that each workgroup
+// pulls half the activation rows through its CU
+constexpr int kSmallRows = 8;
+#define PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ((PRO) == SMLM_LIN_PLAIN && (EPI) == SMLM_LIN_STORE && (MAXS) > 4 && (MTB) == 1)
 
 template <int CPQ>
 struct PartsIn {
@@ -399,7 +403,8 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int K = a.K, KP = K + 8;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
-  constexpr int TB = PRO == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : MTB * 16;  // token rows per group
+  constexpr int TB = PRO == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ? kSmallRows
+                                                                                                  : MTB * 16;
   int cb = (int)blockIdx.x, tg = 0;
   if (ntg > 1) {  // id = ((cb / 8) * ntg + tg) * 8 + cb % 8: the token groups of a column block on one XCD
     const int q = (int)blockIdx.x / kXcds;
@@ -802,7 +807,10 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   // groups measured 1% slower per batch-64 decode step; 16-row groups re-read the 24.6 MB of lm_head weights 4x)
   LinGrid lg;
   lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
-  const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : lg.mtb * 16;
+  const int per_wave_steps = (A.K / 32 + kLinWaves - 1) / kLinWaves;
+  const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows
+                 : pro == SMLM_LIN_PLAIN && epi == SMLM_LIN_STORE && per_wave_steps > 4 && lg.mtb == 1 ? kSmallRows
+                 : lg.mtb * 16;
   const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
   lg.ncb = (cols + cols_per_block - 1) / cols_per_block;
   lg.ntg = (int)((A.M + tb - 1) / tb);
