@@ -223,10 +223,10 @@ __device__ __forceinline__ void load_activations(const smlm_linear_args &a, int6
 // between the sum and the norm, and the group's rows are normalised by four wavefronts at once.
 constexpr int kMaxParts = 8;
 constexpr int kPartsRows = kLinWaves;
-// PLAIN prologue over more than 384 inputs (the FFN down projection): 8-row token groups, so that each workgroup
-// pulls half the activation rows through its CU
+// PLAIN prologue (the attention output, FFN down and value projections): 8-row token groups, so that each
+// workgroup pulls half the activation rows through its CU
 constexpr int kSmallRows = 8;
-#define PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ((PRO) == SMLM_LIN_PLAIN && (EPI) == SMLM_LIN_STORE && (MAXS) > 4 && (MTB) == 1)
+#define PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ((PRO) == SMLM_LIN_PLAIN && (EPI) == SMLM_LIN_STORE && (MTB) == 1)
 
 template <int CPQ>
 struct PartsIn {
@@ -809,7 +809,7 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
   const int per_wave_steps = (A.K / 32 + kLinWaves - 1) / kLinWaves;
   const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows
-                 : pro == SMLM_LIN_PLAIN && epi == SMLM_LIN_STORE && per_wave_steps > 4 && lg.mtb == 1 ? kSmallRows
+                 : pro == SMLM_LIN_PLAIN && epi == SMLM_LIN_STORE && lg.mtb == 1 ? kSmallRows
                  : lg.mtb * 16;
   const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
   lg.ncb = (cols + cols_per_block - 1) / cols_per_block;
