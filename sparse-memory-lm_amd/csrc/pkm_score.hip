@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(512)
 // bf16 decode sizes (N <= 64, half <= 256): a workgroup = 4 wavefronts x 32 sub-keys = 128 sub-keys against 16 * MT
 // tokens.  The query tile is loaded once per workgroup into LDS (the four wavefronts share it), each wavefront's
 // sub-key rows go straight into registers, and every load is issued before the first product.
-template <int MT>
+template <int MT, int KT = 2>
 __global__ void __launch_bounds__(256)
     score_decode_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
                         int H, int NK, int half, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
@@ -548,21 +548,21 @@ __global__ void __launch_bounds__(256)
   __shared__ __align__(16) uint16_t sQ[16 * MT * RS];
   const int z = blockIdx.z, h = z >> 1, p = z & 1;
   const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64, r = lane & 15, g = lane >> 4;
-  const int key0 = blockIdx.x * 128 + wave * 32;
+  const int key0 = blockIdx.x * (64 * KT) + wave * (16 * KT);   // KT 16-key tiles per wavefront
   const int tok0 = blockIdx.y * (16 * MT);
   const uint16_t *kbase = keys + (int64_t)z * NK * half;
   const uint16_t *qbase = q + (int64_t)h * 2 * half + (int64_t)p * half;
   const int nst = (half + 31) / 32;
 
   // 1. this wavefront's sub-key fragments (steps past half and keys past NK load valid memory, then zero)
-  uint4 a[MAXST][2];
+  uint4 a[MAXST][KT];
 #pragma unroll
   for (int st = 0; st < MAXST; ++st) {
     if (st >= nst) continue;  // workgroup-uniform
     const int kk = st * 32 + g * 8;
     const bool kin = kk < half;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < KT; ++i) {
       const int key = key0 + i * 16 + r;
       a[st][i] = load16_or_zero(kbase + (int64_t)min(key, NK - 1) * half + (kin ? kk : 0), kin && key < NK);
     }
@@ -593,9 +593,9 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
 
   // 3. products
-  floatx4 acc[2][MT];
+  floatx4 acc[KT][MT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < KT; ++i)
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -605,7 +605,7 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < MT; ++j) {
       const uint4 b = *(const uint4 *)&sQ[(j * 16 + r) * RS + st * 32 + g * 8];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < KT; ++i)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[st][i]),
                                                             __builtin_bit_cast(bf16x8, b), acc[i][j], 0, 0, 0);
     }
@@ -614,7 +614,7 @@ __global__ void __launch_bounds__(256)
   // 4. scores: lane (r, g) holds sub-keys key0 + 16 i + 4g .. +3 of token tok0 + 16 j + r
   uint16_t *out = p ? s2 : s1;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < KT; ++i)
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const int tok = tok0 + j * 16 + r;
@@ -645,13 +645,16 @@ template <bool F32>
 void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                     void *s2, hipStream_t stream) {
   if (!F32 && N <= 64 && half <= 256) {  // decode: 128 sub-keys x 16 or 64 tokens, query tile shared in LDS
-    const dim3 grid((unsigned)((NK + 127) / 128), (unsigned)((N + (N <= 16 ? 15 : 63)) / (N <= 16 ? 16 : 64)),
+    // more than 16 tokens: 64 sub-keys per workgroup (one 16-key tile per wavefront), twice the workgroups, so
+    // that each CU pulls half the sub-key bytes
+    const int kb = N <= 16 ? 128 : 64;
+    const dim3 grid((unsigned)((NK + kb - 1) / kb), (unsigned)((N + (N <= 16 ? 15 : 63)) / (N <= 16 ? 16 : 64)),
                     (unsigned)(2 * H));  // x: sub-key blocks, y: token blocks, z: (head, half)
     if (N <= 16)
-      hipLaunchKernelGGL((score_decode_kernel<1>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+      hipLaunchKernelGGL((score_decode_kernel<1, 2>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
                          (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
     else
-      hipLaunchKernelGGL((score_decode_kernel<4>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+      hipLaunchKernelGGL((score_decode_kernel<4, 1>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
                          (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
   } else if (N <= 16) {  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
     launch_score<F32, 2, 1, 4, 1, F32 ? 0 : 8>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
