@@ -226,7 +226,13 @@ constexpr int kPartsRows = kLinWaves;
 // PLAIN prologue (the attention output, FFN down and value projections): 8-row token groups, so that each
 // workgroup pulls half the activation rows through its CU
 constexpr int kSmallRows = 8;
-#define PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ((PRO) == SMLM_LIN_PLAIN && (EPI) == SMLM_LIN_STORE && (MTB) == 1)
+
+// token rows per group of a launch (the kernel's TB and the host's grid agree through this one function)
+__host__ __device__ constexpr int group_rows(int pro, int epi, int mtb) {
+  return pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows
+         : pro == SMLM_LIN_PLAIN && epi == SMLM_LIN_STORE && mtb == 1 ? kSmallRows
+         : mtb * 16;
+}
 
 template <int CPQ>
 struct PartsIn {
@@ -403,8 +409,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_kernel(const smlm_linear_a
   const int K = a.K, KP = K + 8;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int r = lane & 15, g = lane >> 4;
-  constexpr int TB = PRO == SMLM_LIN_RMSNORM_PARTS ? kPartsRows : PLAIN_WIDE_K(PRO, EPI, MAXS, MTB) ? kSmallRows
-                                                                                                  : MTB * 16;
+  constexpr int TB = group_rows(PRO, EPI, MTB);  // token rows per group
   int cb = (int)blockIdx.x, tg = 0;
   if (ntg > 1) {  // id = ((cb / 8) * ntg + tg) * 8 + cb % 8: the token groups of a column block on one XCD
     const int q = (int)blockIdx.x / kXcds;
@@ -804,13 +809,11 @@ extern "C" int smlm_decode_linear(const smlm_linear_args *a, void *stream) {
   if (A.M == 0) return SMLM_OK;
   // 16-token groups (more workgroups, shorter per-workgroup chains: decode is latency-bound), except the ARGMAX
   // epilogue over more than 16 rows: 32-row groups (each workgroup normalises its rows in the prologue, so 64-row
-  // groups measured 1% slower per batch-64 decode step; 16-row groups re-read the 24.6 MB of lm_head weights 4x)
+  // groups measured 1% slower per batch-64 decode step; 16-row groups re-read the 24.6 MB of lm_head weights 4x),
+  // and the PLAIN prologue with the STORE epilogue: 8-row groups (group_rows)
   LinGrid lg;
   lg.mtb = epi == SMLM_LIN_ARGMAX && A.M > 16 ? kMaxTiles : 1;
-  const int per_wave_steps = (A.K / 32 + kLinWaves - 1) / kLinWaves;
-  const int tb = pro == SMLM_LIN_RMSNORM_PARTS ? kPartsRows
-                 : pro == SMLM_LIN_PLAIN && epi == SMLM_LIN_STORE && lg.mtb == 1 ? kSmallRows
-                 : lg.mtb * 16;
+  const int tb = group_rows(pro, epi, lg.mtb);
   const int cols_per_block = epi == SMLM_LIN_ARGMAX ? kArgCols : 16;
   lg.ncb = (cols + cols_per_block - 1) / cols_per_block;
   lg.ntg = (int)((A.M + tb - 1) / tb);
