@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(512)
 // bf16 decode sizes (N <= 64, half <= 256): a workgroup = 4 wavefronts x 32 sub-keys = 128 sub-keys against 16 * MT
 // tokens.  The query tile is loaded once per workgroup into LDS (the four wavefronts share it), each wavefront's
 // sub-key rows go straight into registers, and every load is issued before the first product.
-template <int MT, int KT = 2>
+template <int MT, int KT = 1>
 __global__ void __launch_bounds__(256)
     score_decode_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
                         int H, int NK, int half, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
@@ -645,18 +645,18 @@ template <bool F32>
 void dispatch_score(const void *q, int64_t q_stride, const void *keys, int64_t N, int H, int NK, int half, void *s1,
                     void *s2, hipStream_t stream) {
   if (!F32 && N <= 64 && half <= 256) {  // decode: 128 sub-keys x 16 or 64 tokens, query tile shared in LDS
-    // more than 16 tokens: 64 sub-keys per workgroup (one 16-key tile per wavefront), twice the workgroups, so
-    // that each CU pulls half the sub-key bytes
-    const int kb = N <= 16 ? 128 : 64;
+    // 64 sub-keys per workgroup (one 16-key tile per wavefront): 512 workgroups at 4,096 sub-keys per half, each
+    // CU pulling 32 KB of sub-keys
+    const int kb = 64;
     const dim3 grid((unsigned)((NK + kb - 1) / kb), (unsigned)((N + (N <= 16 ? 15 : 63)) / (N <= 16 ? 16 : 64)),
                     (unsigned)(2 * H));  // x: sub-key blocks, y: token blocks, z: (head, half)
     if (N <= 16)
-      hipLaunchKernelGGL((score_decode_kernel<1, 2>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
+      hipLaunchKernelGGL((score_decode_kernel<1, 1>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
                          (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
     else
       hipLaunchKernelGGL((score_decode_kernel<4, 1>), grid, dim3(256), 0, stream, (const uint16_t *)q, q_stride,
                          (const uint16_t *)keys, (int)N, H, NK, half, (uint16_t *)s1, (uint16_t *)s2);
-  } else if (N <= 16) {  // decode: 128 sub-keys x 16 tokens per workgroup, spread over many workgroups
+  } else if (N <= 16) {  // (fp32 or half > 256) decode: 128 sub-keys x 16 tokens per workgroup
     launch_score<F32, 2, 1, 4, 1, F32 ? 0 : 8>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
   } else if (!F32 && N <= 64) {  // decode batches: 128 sub-keys x 64 tokens, operands preloaded
     launch_score<F32, 4, 2, 2, 2, F32 ? 0 : 8>(q, q_stride, keys, N, H, NK, half, s1, s2, stream);
