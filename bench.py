@@ -125,7 +125,7 @@ def chained_launch_us(dev, numel=384, kernels=264, replays=40):
     """Device time per kernel of a HIP graph of `kernels` back-to-back elementwise kernels, each reading the `numel`
     fp32 values its predecessor wrote (in-place adds): 384 values are one workgroup, the floor every kernel of a
     captured decode step pays whatever its work; 262,144 values spread one kernel over the whole chip.
-    264 = the 8 decode steps of one graph replay x 33 kernels."""
+    264 = 8 decode steps of 33 kernels (the graph length does not change the per-kernel floor)."""
     import torch
     x = torch.zeros(numel, dtype=torch.float32, device=dev)
     side = torch.cuda.Stream(dev)
