@@ -479,14 +479,14 @@ class _FusedDecodeStep:
 
     At batches up to proj_max_batch the attention launch also does wo, per head (decode_attention_proj), and the
     next launch's prologue sums the heads: 4 launches per dense block, 6 per memory block (MI355X, config 3:
-    0.155 -> 0.144 ms per step at batch 1, 0.177 -> 0.173 at 32).  Larger batches keep the wo launch: the summing
-    prologue works on 4-token groups, and from 48 tokens up re-reading the weights per group costs more than the
-    launch (0.196 -> 0.236 ms at 64).
+    0.155 -> 0.144 ms per step at batch 1).  Larger batches keep the wo launch: the summing prologue works on
+    4-token groups, which re-read the weights per group, and with the wo launch on 8-token groups the fold loses
+    from batch 20 up (139.4 -> 133.3 us per step at batch 16 folded, 147.3 -> 150.4 at 24, 150.1 -> 153.8 at 32).
 
     Derived weights (the concatenated query_proj | swilu_proj and its bias) are built at construction and rebuilt
     on an eager run after a parameter changed; a captured graph keeps what it was captured with."""
 
-    proj_max_batch = 32
+    proj_max_batch = 16
 
     @staticmethod
     def supported(model, dtype):
