@@ -445,14 +445,16 @@ int launch_attention_nt(const AttnArgs &a, hipStream_t stream) {
   return launch_status("smlm_decode_attention");
 }
 
-// 256 threads per (sequence, head) when those workgroups fill the chip twice over, 512 below that (batch 64 x 6
-// heads: 0.212 -> 0.206 ms per decode step against 256).  Small batches ran 1024 threads per head until the
+// 256 threads per (sequence, head) when those workgroups fill the chip twice over, 384 when they fill it once
+// (batch 64 x 6 heads: 177.4 -> 176.6 us per decode step against 512; 512 had measured 0.212 -> 0.206 ms against
+// 256 there), 512 below that.  The plain and wo-folded variants pick alike, so they reach the same y.  Small batches ran 1024 threads per head until the
 // per-wavefront work (its own RoPE, the row-group sums before the merge) outweighed the per-pass arithmetic: with 16
 // wavefronts the CU's SIMDs each ran four of those fixed costs; 512 threads measured 127.6 -> 126.6 us per step at
 // batch 1 and 135.8 -> 134.0 / 139.6 -> 138.2 / 156.3 -> 155.6 us at batches 8 / 16 / 32 (256: 130.2 at batch 1).
 template <int HD, bool PROJ>
 int launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (a.B * a.H >= 512) return launch_attention_nt<HD, 256, PROJ>(a, stream);
+  if (a.B * a.H >= 256) return launch_attention_nt<HD, 384, PROJ>(a, stream);
   return launch_attention_nt<HD, 512, PROJ>(a, stream);
 }
 
