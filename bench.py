@@ -8,7 +8,7 @@ order they run (the headline ones first):
   decode         value: config 3 decode tok/s at batch 64 -- the 21M LM (d=384, 6 layers, vocab 32000) with the
                  B-16M memory (4096^2 = 16,777,216 x 384 bf16 values, 12.9 GB) replacing layer 3's FFN,
                  128-token prompts (prefilled once, untimed), then 256 greedy tokens.  A step is one such
-                 256-token generation (32 replays of the captured 8-step whole-step HIP graph); W untimed and K
+                 256-token generation (8 replays of the captured 32-step whole-step HIP graph); W untimed and K
                  timed generations, each bracketed by synchronisations (the loop of smlm/train.py:283-301).
                  value = 64 * 256 * K / time.  The same at batch 1, and each token step against its floors
                  (decode_roofline: HBM bytes / 8 TB/s; kernel count x the chained-launch time).
@@ -16,7 +16,9 @@ order they run (the headline ones first):
                  (3,439,329,280 algorithmic bytes per call), and the uniform-index control of the same shapes.
                  roofline: the control's algorithmic GB/s (= its physical traffic: no row repeats in cache) over
                  HBM peak, from HIP events on the launch stream; roofline.zipf: the Zipf call's algorithmic rate
-                 and its physical rate from the committed rocprofv3 counters (profiles/gather_config4_pmc.txt).
+                 and its physical rate from the committed rocprofv3 counters (profiles/gather_config4_pmc.txt, used
+                 only while it names the sha256 of the gather's present sources).  The box's own ceilings beside
+                 them (csrc/bench/ceiling.hip): sequential read / write / copy and random 384-byte row reads.
   cpu            cpu_baseline: the reference's torch path (oracle/torch_path.py) on the host cores, config 3 at
                  batch 64 (and 1), a bounded sample of the 256 steps; config 4 on the host (chunked int8 gather and
                  dequantise + embedding_bag) over 2,048 tokens; config 2 over one 2048-token prompt.
@@ -139,61 +141,6 @@ def chained_launch_us(dev, numel=384, kernels=264, replays=40):
         for _ in range(kernels):
             x.add_(1.0)
     return 1000.0 * event_time_ms(graph.replay, replays) / kernels
-
-
-def device_handoff(dev, stages=64, replays=20):
-    """Device time per dependent stage (every workgroup reads the whole 2 KB vector its predecessors wrote and
-    writes its slice of the next) when the stages are kernels back to back in a HIP graph, against one persistent
-    kernel whose workgroups hand off to each other on the device (csrc/bench/handoff.hip): one atomic counter,
-    per-XCD-group counters under a top counter, a flag per workgroup (release / acquire fences), and flags with
-    device-coherent data accesses and no fences.  Waits are bounded; a run whose waits gave up raises."""
-    import ctypes
-    import torch
-    from smlm_hip import build as hip_build
-    lib = ctypes.CDLL(hip_build.BENCH_LIB_PATH)
-    vp = ctypes.c_void_p
-    n = lib.smlm_bench_handoff_vec()
-    v0, v1 = torch.zeros(n, device=dev), torch.zeros(n, device=dev)
-    ctr = torch.zeros(576, dtype=torch.int32, device=dev)
-    abort = torch.zeros(1, dtype=torch.int32, device=dev)
-    out = {"stages": stages, "vector_bytes": 4 * n}
-
-    def stream():
-        return vp(torch.cuda.current_stream(dev).cuda_stream)
-
-    def chain(nwg):
-        rc = lib.smlm_bench_handoff_chain(vp(v0.data_ptr()), vp(v1.data_ptr()), stages, nwg, stream())
-        if rc != 0:
-            raise RuntimeError(f"smlm_bench_handoff_chain: {rc}")
-
-    for nwg in (64, 256):
-        flags = torch.zeros(nwg, dtype=torch.int32, device=dev)
-        side = torch.cuda.Stream(dev)
-        side.wait_stream(torch.cuda.current_stream(dev))
-        with torch.cuda.stream(side):
-            chain(nwg)
-        torch.cuda.current_stream(dev).wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            chain(nwg)
-        res = {"kernel_chain_us": 1000.0 * event_time_ms(graph.replay, replays) / stages}
-        for kind, name in ((0, "one_counter_us"), (1, "group_counters_us"), (2, "flags_fenced_us"),
-                           (3, "flags_coherent_us")):
-            def run(k=stages, kind=kind):
-                ctr.zero_()
-                flags.zero_()
-                rc = lib.smlm_bench_handoff_persistent(vp(v0.data_ptr()), vp(v1.data_ptr()), k, nwg, kind,
-                                                       vp(ctr.data_ptr()), vp(flags.data_ptr()),
-                                                       vp(abort.data_ptr()), stream())
-                if rc != 0:
-                    raise RuntimeError(f"smlm_bench_handoff_persistent: {rc}")
-            full, one = event_time_ms(run, replays), event_time_ms(lambda: run(1), replays)
-            if int(abort.item()):
-                raise RuntimeError(f"handoff kind {kind} at {nwg} workgroups: a wait gave up")
-            res[name] = 1000.0 * (full - one) / (stages - 1)
-        out[f"wg{nwg}"] = res
-        log(f"dependent stage at {nwg} workgroups: " + ", ".join(f"{k} {v:.2f}" for k, v in res.items()))
-    return out
 
 
 def decode_roofline(model, B, ms_per_step, mean_pos, launch_us, wide_launch_us):
@@ -324,6 +271,8 @@ def gather_stress(dev, reps, cpu_tokens=0):
     res = {"tokens": N, "lookups_per_token": Kl, "table": "16,777,216 x 384 int8 + fp16 row scales",
            "alg_bytes_per_call": alg_bytes, "ms_zipf": ms_zipf, "ms_uniform": ms_uni,
            "alg_GBps_zipf": alg_bytes / ms_zipf / 1e6, "alg_GBps_uniform": alg_bytes / ms_uni / 1e6}
+    res["ceilings"] = memory_ceilings(dev, max(5, reps // 2), codes, codes, uni)
+    log(f"memory ceilings: " + ", ".join(f"{k} {v['GBps']:.0f} GB/s" for k, v in res["ceilings"].items()))
     if cpu_tokens:
         out = K.bag_infer(idx, w, codes, scales)
         torch.cuda.synchronize(dev)
@@ -333,6 +282,76 @@ def gather_stress(dev, reps, cpu_tokens=0):
     del codes, scales, idx, w, uni, out
     torch.cuda.empty_cache()
     return res
+
+
+def _bench_lib():
+    import ctypes
+    from smlm_hip import build as hip_build
+    lib = ctypes.CDLL(hip_build.BENCH_LIB_PATH)
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.smlm_bench_stream.argtypes = [ci, vp, vp, i64, ci, vp, vp]
+    lib.smlm_bench_random_rows.argtypes = [vp, i64, vp, i64, ci, ci, vp, vp]
+    return lib
+
+
+def memory_ceilings(dev, reps, read_buf, rows_table, rows_idx):
+    """The box's own memory ceilings, from kernels that only move bytes (csrc/bench/ceiling.hip):
+      read / write / copy  sequential 16-byte accesses over buffers far larger than the 256 MB of caches: read over
+                           `read_buf` (the config-4 int8 table, 6.44 GB), write and copy over 2 GiB buffers; best of
+                           four grid sizes; GB/s = bytes read + written / HIP-event time;
+      random rows          whole rows of `rows_table` at the indices `rows_idx` (the uniform-index control of config
+                           4: 8,388,608 lookups of 384-byte int8 rows), no arithmetic, no output; best of the launch
+                           shapes (row slots per workgroup x rows in flight per thread); GB/s counts the row bytes
+                           and the 8-byte indices."""
+    import ctypes
+    import torch
+    lib = _bench_lib()
+    vp = ctypes.c_void_p
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def stream():
+        return vp(torch.cuda.current_stream(dev).cuda_stream)
+
+    def run_stream(op, src, dst, nbytes, grid):
+        rc = lib.smlm_bench_stream(op, vp(src), vp(dst), nbytes, grid, vp(sink.data_ptr()), stream())
+        if rc != 0:
+            raise RuntimeError(f"smlm_bench_stream({op}): {rc}")
+
+    out = {}
+    read_bytes = read_buf.numel() * read_buf.element_size() // (1 << 20) * (1 << 20)
+    big = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    big2 = torch.empty_like(big)
+    for op, name, src, dst, nbytes, moved in (
+            (0, "read", read_buf.data_ptr(), 0, read_bytes, read_bytes),
+            (1, "write", 0, big.data_ptr(), big.numel(), big.numel()),
+            (2, "copy", big.data_ptr(), big2.data_ptr(), big.numel(), 2 * big.numel())):
+        best = None
+        for grid in (1024, 2048, 4096, 8192):
+            ms = event_time_ms(lambda: run_stream(op, src, dst, nbytes, grid), reps)
+            if best is None or ms < best[0]:
+                best = (ms, grid)
+        out[name] = {"bytes": moved, "ms": best[0], "grid": best[1], "GBps": moved / best[0] / 1e6}
+    del big, big2
+    n = rows_idx.numel()
+    rows, row_bytes = rows_table.shape[0], rows_table.shape[1] * rows_table.element_size()
+    shapes = {}
+    for sh in range(lib.smlm_bench_random_row_shapes()):
+        code = lib.smlm_bench_random_row_shape(sh)
+
+        def run(sh=sh):
+            rc = lib.smlm_bench_random_rows(vp(rows_idx.data_ptr()), n, vp(rows_table.data_ptr()), rows, row_bytes,
+                                            sh, vp(sink.data_ptr()), stream())
+            if rc != 0:
+                raise RuntimeError(f"smlm_bench_random_rows(shape {sh}): {rc}")
+        ms = event_time_ms(run, reps)
+        shapes[f"slots{code // 1000}_rows{code % 1000}"] = {"ms": ms, "GBps": n * (row_bytes + 8) / ms / 1e6}
+    best = min(shapes, key=lambda k: shapes[k]["ms"])
+    out["random_rows"] = {"lookups": n, "row_bytes": row_bytes, "bytes": n * (row_bytes + 8),
+                          "best_shape": best, "ms": shapes[best]["ms"], "GBps": shapes[best]["GBps"],
+                          "shapes": shapes}
+    if int(sink.abs().sum()):
+        raise RuntimeError("ceiling kernels: the never-taken store was taken")
+    return out
 
 
 def lookup_prefill(dev, reps):
@@ -755,16 +774,38 @@ def cpu_prefill_c2(model, tokens=2048):
             "sample": f"1 of the 8 prompts: LM forward over {tokens} tokens ({dt:.1f} s), reference torch path"}
 
 
+GATHER_SOURCES = ("sparse-memory-lm_amd/csrc/pkm_bag.hip", "sparse-memory-lm_amd/csrc/pkm_bag_dev.h")
+
+
+def gather_sources_sha256():
+    """sha256 over the sources of the config-4 gather kernel: ties a committed counter summary to the code it
+    measured."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in GATHER_SOURCES:
+        with open(os.path.join(REPO, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
 def read_traffic():
     """HBM bytes per launch of the config-4 gather (uniform control, Zipf) from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel); None where absent."""
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel).  The summary names the sha256 of the
+    gather's sources it was measured on; when that is absent or differs from the sources here, the counters
+    belong to other code and the traffic is None (with "stale": True)."""
     path = os.path.join(REPO, "profiles", "gather_config4_pmc.txt")
-    out = {"uniform": None, "zipf": None}
-    if os.path.exists(path):
-        for line in open(path):
-            for k in out:
-                if line.startswith(f"traffic_bytes_per_launch_{k}:"):
-                    out[k] = float(line.split(":", 1)[1])
+    out = {"uniform": None, "zipf": None, "stale": True}
+    if not os.path.exists(path):
+        return out
+    vals, sha = {}, None
+    for line in open(path):
+        if line.startswith("gather_sources_sha256:"):
+            sha = line.split(":", 1)[1].strip()
+        for k in ("uniform", "zipf"):
+            if line.startswith(f"traffic_bytes_per_launch_{k}:"):
+                vals[k] = float(line.split(":", 1)[1])
+    if sha is not None and sha == gather_sources_sha256():
+        out.update(vals, stale=False)
     return out
 
 
@@ -781,7 +822,7 @@ def calibration_copy(dev, nbytes=1 << 30):
 
 
 HEADLINE_PHASES = "decode,gather,cpu,config1,config0,prefill,lookup"
-OPTIONAL_PHASES = "offload,train,engram,handoff"
+OPTIONAL_PHASES = "offload,train,engram"
 
 
 def main():
@@ -881,14 +922,23 @@ def main():
         if ga is not None:
             traffic = read_traffic()
             tz = traffic["zipf"]
+            ce = ga["ceilings"]
+            read_c, rows_c = ce["read"]["GBps"], ce["random_rows"]["GBps"]
+            line["hbm_read_ceiling_GBps"] = read_c
+            line["random_row_ceiling_GBps"] = rows_c
             line["roofline"] = {
                 "kernel": "bag_rows_kernel<int8> (config-4 shapes, uniform-index control)", "bound": "hbm",
                 "achieved": ga["alg_GBps_uniform"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ga["alg_GBps_uniform"] / HBM_PEAK_GBS, "traffic": traffic["uniform"],
+                "traffic_stale": traffic["stale"],
                 "alg_bytes_per_launch": ga["alg_bytes_per_call"], "ms_per_launch": ga["ms_uniform"],
+                "frac_of_read_ceiling": ga["alg_GBps_uniform"] / read_c,
+                "frac_of_random_row_ceiling": ga["alg_GBps_uniform"] / rows_c,
+                "time_vs_random_row_ceiling": ce["random_rows"]["ms"] / ga["ms_uniform"],
                 "zipf": {"ms_per_launch": ga["ms_zipf"], "alg_GBps": ga["alg_GBps_zipf"], "traffic": tz,
                          "physical_GBps": tz / ga["ms_zipf"] / 1e6 if tz else None,
-                         "physical_frac": tz / ga["ms_zipf"] / 1e6 / HBM_PEAK_GBS if tz else None}}
+                         "physical_frac": tz / ga["ms_zipf"] / 1e6 / HBM_PEAK_GBS if tz else None,
+                         "physical_frac_of_read_ceiling": tz / ga["ms_zipf"] / 1e6 / read_c if tz else None}}
 
         def cpu():
             sd = host_state(model)
@@ -958,7 +1008,6 @@ def main():
                     v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
         line["train_kernels"] = tr
         line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps))
-        line["device_handoff"] = phase("handoff", lambda: device_handoff(dev))
     finally:
         if errors:
             line["phase_errors"] = errors

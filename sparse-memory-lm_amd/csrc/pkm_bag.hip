@@ -4,12 +4,14 @@
 //
 // The gather is HBM-bound: every lookup reads one whole table row (768 B for a 384-wide bf16 row).  One
 // workgroup owns one token.  A row is cut into 16-byte chunks (cpr chunks per row) and the workgroup's threads
-// are laid out as rpr row slots x cpr chunk columns, so one "round" of the workgroup reads rpr whole rows with
-// coalesced 16-byte loads and every lane is busy (384-wide rows: 192 threads = 4 bf16 / 8 int8 / 2 fp32 /
-// 16 q4 rows per round).  Each thread keeps the fp32 partial sums of its chunk's columns over the rows of its
-// slot and issues kUnroll independent row loads at a time; the rpr partial sums per column are added through
-// LDS at the end, followed by the epilogue.  Lookups (row offsets, weights premultiplied by the row scale) are
-// staged in LDS first, so each row load depends on one LDS read only.
+// are laid out as rpr row slots x cpr chunk columns (bag::bag_threads: 8 int8 / 16 q4 rows of 384 values in 192
+// threads, 8 bf16 / 4 fp32 rows in 384), so each round reads rpr whole rows with coalesced 16-byte loads and every
+// lane is busy.  Each thread keeps the fp32 partial sums of its chunk's columns over the rows of its slot and
+// issues kUnroll independent row loads at a time; the rpr partial sums per column are added through LDS at the
+// end, followed by the epilogue.  Lookups (row offsets, weights premultiplied by the row scale) are staged in LDS
+// first, one per thread, so each row load depends on one LDS read only.  Loading each lookup's index, weight and
+// scale in every lane of its slot instead of staging them measured 0.87 against 0.65 ms at config 4 (uniform):
+// three redundant memory instructions per row load.
 #include "pkm_bag_dev.h"
 
 namespace smlm {
@@ -18,12 +20,10 @@ namespace {
 using namespace bag;
 
 template <int TK, bool IDX64>
-__global__ void __launch_bounds__(256) bag_rows_kernel(const void *__restrict__ idx, const float *__restrict__ w,
-                                                       const uint8_t *__restrict__ table,
-                                                       const uint16_t *__restrict__ scales,
-                                                       const uint16_t *__restrict__ pre, void *__restrict__ out,
-                                                       int K, int D, int64_t rows, int row_bytes, int cpr,
-                                                       int out_bf16) {
+__global__ void __launch_bounds__(kBagMaxThreads)
+    bag_rows_kernel(const void *__restrict__ idx, const float *__restrict__ w, const uint8_t *__restrict__ table,
+                    const uint16_t *__restrict__ scales, const uint16_t *__restrict__ pre, void *__restrict__ out,
+                    int K, int D, int64_t rows, int row_bytes, int cpr, int out_bf16) {
   constexpr int VPC = vals_per_chunk<TK>();
   extern __shared__ __align__(16) unsigned char smem[];
   int64_t *s_off = (int64_t *)smem;           // [kStage]
@@ -98,8 +98,11 @@ int launch_bag(const void *idx, const float *w, int64_t N, int K, const void *ta
   const int row_bytes = (int)row_bytes64;
   const bool aligned = ((uintptr_t)table % 16) == 0;
   const int cpr = row_bytes / 16;
-  if (aligned && row_bytes % 16 == 0 && cpr >= 1 && cpr <= 256) {
+  if (aligned && row_bytes % 16 == 0 && cpr >= 1 && cpr <= kBagMaxChunks) {
     const int nthr = bag_threads(cpr);
+    if (nthr > kBagMaxThreads)
+      return fail(SMLM_EUNSUPPORTED, "smlm_pkm_bag: %d threads for %d-chunk rows exceed the kernel's %d", nthr,
+                  cpr, kBagMaxThreads);
     const int rpr = nthr / cpr;
     const size_t shmem = kStage * (sizeof(int64_t) + sizeof(float)) + (size_t)rpr * D * sizeof(float);
     hipLaunchKernelGGL((bag_rows_kernel<TK, IDX64>), dim3((unsigned)N), dim3(nthr), shmem, stream, idx, w,

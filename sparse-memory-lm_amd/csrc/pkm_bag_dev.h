@@ -102,9 +102,11 @@ __device__ __forceinline__ void store_out(void *out, int64_t o, float a, bool ba
   store_out_bits(out, o, a, bad, pre != nullptr, pre ? pre[o] : (uint16_t)0, out_bf16);
 }
 
-// Rows of a token's staged lookups [0, kc) accumulated by a workgroup laid out as row slots x cpr chunk columns:
-// thread (slot, c) adds w_j * chunk c of row j for j = slot, slot + rpr, ... in that order (UNROLL loads in
-// flight; the order of the additions does not depend on UNROLL).
+// Rows of a token's staged lookups [0, kc) accumulated by row slot `slot` of a layout of rpr row slots x cpr chunk
+// columns: thread (slot, c) adds w_j * chunk c of row j for j = slot, slot + rpr, ... in that order (UNROLL loads in
+// flight; the order of the additions does not depend on UNROLL).  The rounds are unpredicated: selecting a loaded
+// value under a lane condition made the compiler wait for each load before issuing the next (the config-4 Zipf
+// gather 386 -> 470 us, the decode step +3 us).
 template <int TK, int UNROLL = kUnroll>
 __device__ __forceinline__ void accumulate_rows(const uint8_t *__restrict__ colbase, int slot, int rpr, int kc,
                                                 const int64_t *s_off, const float *s_w, float *acc) {
@@ -119,21 +121,27 @@ __device__ __forceinline__ void accumulate_rows(const uint8_t *__restrict__ colb
   for (; j < kc; j += rpr) accumulate<TK>(acc, *(const uint4 *)(colbase + s_off[j]), s_w[j]);
 }
 
-// Threads of the row-slot layout for rows of cpr 16-byte chunks: lcm(cpr, 64) (whole wavefronts, every lane busy),
-// at least 128; if that exceeds 256, as many whole rows as fit in 256.  Row slots = threads / cpr.  The slot
-// count fixes the order of the fp32 additions, so every kernel that must agree bit for bit uses this layout.
-__host__ __device__ constexpr int bag_threads(int cpr) {
-  int g = cpr, b = kWave;
-  while (b) {
-    const int t = g % b;
-    g = b;
-    b = t;
-  }
-  int nthr = cpr / g * kWave;
-  if (nthr > 256) nthr = cpr * (256 / cpr);
-  while (nthr < 128) nthr *= 2;
-  return nthr;
+// Threads of the canonical row-slot layout for rows of cpr 16-byte chunks: as many whole rows (slots) as fit in
+// kBagThreads threads for rows of up to 32 chunks (int8 rows of 384 values, 24 chunks: 8 slots; q4, 12: 16), in
+// kBagThreadsWide for wider rows (bf16, 48: 8 slots; fp32, 96: 4), one slot at least.  The slot count fixes the
+// order of the fp32 additions (each slot sums its rows in order, then the slots are added in slot order), so every
+// kernel that must agree bit for bit uses this layout; a workgroup with fewer threads runs several slots per
+// thread (select_bag_kernel).  Measured (MI355X): 16 int8 slots in 384 threads took the config-4 gather 652 ->
+// 732 us (uniform) and 389 -> 588 us (Zipf); 8 bf16 slots instead of 4 took the decode step 177.1 -> 176.5 us
+// (batch 64) and 124.3 -> 123.5 us (batch 1) with the config-2 bf16 bag unchanged (279-280 us).
+constexpr int kBagThreads = 192;
+constexpr int kBagThreadsWide = 384;
+constexpr int kBagMaxChunks = 256;     // rows of more 16-byte chunks take the generic kernel
+constexpr int imax(int a, int b) { return a > b ? a : b; }
+// the most threads bag_threads returns for rows of at most kBagMaxChunks chunks (a slot budget, or one slot of
+// up to kBagMaxChunks threads): the launch bound of the kernels that run this layout in one workgroup (launching
+// more threads than a kernel's bound fails)
+constexpr int kBagMaxThreads = imax(kBagMaxChunks, imax(kBagThreads, kBagThreadsWide));
+
+__host__ __device__ constexpr int bag_slots(int cpr) {
+  return cpr >= (cpr <= 32 ? kBagThreads : kBagThreadsWide) ? 1 : (cpr <= 32 ? kBagThreads : kBagThreadsWide) / cpr;
 }
+__host__ __device__ constexpr int bag_threads(int cpr) { return bag_slots(cpr) * cpr; }
 
 }  // namespace bag
 }  // namespace smlm

@@ -59,21 +59,25 @@ extern "C" int smlm_pkm_lookup_noalloc(const void *q, int64_t q_row_stride, cons
     return fail(SMLM_EINVAL, "smlm_pkm_lookup_noalloc: dtype must be SMLM_BF16 or SMLM_F32, got %d", dtype);
   if (N < 0 || H < 1 || NK < 1)
     return fail(SMLM_EINVAL, "smlm_pkm_lookup_noalloc: bad shape N=%lld H=%d NK=%d", (long long)N, H, NK);
-  // s1 at the start of the array, s2 at the next 256-byte boundary after it
-  const int64_t elem = dtype == SMLM_F32 ? 4 : 2;
-  const int64_t one = N * H * NK * elem;
-  const int64_t s2_off = (one + 255) / 256 * 256;
-  if (N > (int64_t)SMLM_LOOKUP_SCRATCH_BYTES || s2_off + one > (int64_t)SMLM_LOOKUP_SCRATCH_BYTES)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_lookup_noalloc: N=%lld x H=%d x NK=%d scores need %lld bytes of "
-                "scratch; the static array holds %lld (use smlm_pkm_score + smlm_pkm_select_bag with buffers of "
-                "your own)", (long long)N, H, NK, (long long)(s2_off + one), (long long)SMLM_LOOKUP_SCRATCH_BYTES);
-  // every argument check of both steps before anything is launched: with N = 0 they validate and return
+  if (N > (int64_t)SMLM_LOOKUP_SCRATCH_BYTES)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_lookup_noalloc: N=%lld tokens exceed what the %lld-byte scratch "
+                "array can hold", (long long)N, (long long)SMLM_LOOKUP_SCRATCH_BYTES);
+  // every argument check of both steps before anything is sized or launched: with N = 0 they validate and return
+  // (among them H <= 32768 and NK <= 65536, which keep the size below within int64)
   const void *fake = table ? table : q;
   int rc = smlm_pkm_score(q, q_row_stride, keys, dtype, 0, H, NK, half, (void *)fake, (void *)fake, stream);
   if (rc != SMLM_OK) return rc;
   rc = smlm_pkm_select_bag(fake, fake, dtype, 0, H, NK, knn, table, table_dtype, rows, D, scales, pre, out,
                            out_dtype, nullptr, nullptr, nullptr, stream);
   if (rc != SMLM_OK) return rc;
+  // s1 at the start of the array, s2 at the next 256-byte boundary after it
+  const int64_t elem = dtype == SMLM_F32 ? 4 : 2;
+  const int64_t one = N * H * NK * elem;
+  const int64_t s2_off = (one + 255) / 256 * 256;
+  if (s2_off + one > (int64_t)SMLM_LOOKUP_SCRATCH_BYTES)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_lookup_noalloc: N=%lld x H=%d x NK=%d scores need %lld bytes of "
+                "scratch; the static array holds %lld (use smlm_pkm_score + smlm_pkm_select_bag with buffers of "
+                "your own)", (long long)N, H, NK, (long long)(s2_off + one), (long long)SMLM_LOOKUP_SCRATCH_BYTES);
   if (N == 0) return SMLM_OK;
   void *base = nullptr;
   rc = scratch_pointer(stream, &base);

@@ -614,9 +614,9 @@ void launch_select(const void *s1, const void *s2, int64_t rows, int NK, int knn
 // ---- selection fused with the value bag (decode): one workgroup per token, 2H wavefronts ----------------------
 // Wavefront (h, p) selects in s_p[n, h, :]; wavefront (h, 0) then does head h's Cartesian step and softmax and
 // stages its knn lookups (row offset, weight x row scale) in LDS; finally the workgroup gathers the token's H*knn
-// rows in the row-slot layout of bag_rows_kernel (bag_threads(cpr) threads, the rest idle), with twice the loads in
-// flight per thread, adds the slots through LDS (over the candidate buffers, no longer needed) and applies the bag
-// epilogue.  Same selection and the same bag additions in the same order as select_kernel followed by
+// rows in the canonical row-slot layout of bag_rows_kernel (bag::bag_slots(cpr) slots; threads past them idle, a
+// thread runs several slots when the workgroup has fewer), with twice the loads in flight per thread, adds the
+// slots through LDS (over the candidate buffers, no longer needed) and applies the bag epilogue.  Same selection and the same bag additions in the same order as select_kernel followed by
 // bag_rows_kernel, so the results are bit-identical; it saves the launch and the round trip of the lookups.
 constexpr int kFusedCapBytes = 4096;   // LDS candidate + staging bytes per half (1024 bf16 / 512 fp32 keys)
 
@@ -686,15 +686,18 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   }
   __syncthreads();
 
-  const int rpr = bag::bag_threads(cpr) / cpr, slot = tid / cpr, c = tid % cpr;
+  // the canonical slots of the bag layout; with fewer whole slots of threads than that, a thread runs several
+  const int rpr = bag::bag_slots(cpr), tslots = (int)blockDim.x / cpr, slot = tid / cpr, c = tid % cpr;
   float *s_red = (float *)smem;
-  float acc[VPC];
+  if (slot < tslots) {
+    for (int cs = slot; cs < rpr; cs += tslots) {
+      float acc[VPC];
 #pragma unroll
-  for (int e = 0; e < VPC; ++e) acc[e] = 0.f;
-  if (slot < rpr) {
-    bag::accumulate_rows<TK, 2 * bag::kUnroll>(table + (int64_t)c * 16, slot, rpr, H * knn, s_off, s_w, acc);
+      for (int e = 0; e < VPC; ++e) acc[e] = 0.f;
+      bag::accumulate_rows<TK, 2 * bag::kUnroll>(table + (int64_t)c * 16, cs, rpr, H * knn, s_off, s_w, acc);
 #pragma unroll
-    for (int e = 0; e < VPC; ++e) s_red[slot * D + bag::chunk_col<TK>(c, e, D)] = acc[e];
+      for (int e = 0; e < VPC; ++e) s_red[cs * D + bag::chunk_col<TK>(c, e, D)] = acc[e];
+    }
   }
   __syncthreads();
   const bool bad = s_bad != 0;
@@ -714,7 +717,7 @@ void launch_select_bag(const void *s1, const void *s2, int64_t N, int H, int NK,
   const int row_bytes = TK == bag::kF32 ? 4 * D : TK == bag::kBF16 ? 2 * D : TK == bag::kI8 ? D : D / 2;
   const int cpr = row_bytes / 16;
   const int nthr = 2 * H * kWave;
-  const int rpr = bag::bag_threads(cpr) / cpr;
+  const int rpr = bag::bag_slots(cpr);
   const size_t cand = (size_t)2 * H * kFusedCapBytes, red = (size_t)rpr * D * sizeof(float);
   const size_t union_bytes = (cand > red ? cand : red + 15) / 16 * 16;
   const size_t shmem = union_bytes + (size_t)2 * 2 * H * kMaxKnn * sizeof(Key) + (size_t)2 * H * kMaxKnn * 8 +
@@ -793,10 +796,9 @@ extern "C" int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, in
     return fail(SMLM_EINVAL, "smlm_pkm_select_bag: out_dtype must be SMLM_F32 or SMLM_BF16");
   const int64_t row_bytes = table_dtype == SMLM_F32 ? 4LL * D : table_dtype == SMLM_BF16 ? 2LL * D
                             : table_dtype == SMLM_I8 ? (int64_t)D : D / 2;
-  if (D < 1 || (table_dtype == SMLM_Q4 && D % 2) || row_bytes % 16 || rows < 1 ||
-      bag::bag_threads((int)(row_bytes / 16)) > 2 * H * kWave)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: rows of D=%d must be whole 16-byte chunks that the "
-                "%d-thread workgroup covers in the value bag's row-slot layout", D, 2 * H * kWave);
+  if (D < 1 || (table_dtype == SMLM_Q4 && D % 2) || row_bytes % 16 || rows < 1 || row_bytes / 16 > 2 * H * kWave)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: rows of D=%d must be whole 16-byte chunks, at most one per "
+                "thread of the %d-thread workgroup", D, 2 * H * kWave);
   if ((uintptr_t)table % 16)
     return fail(SMLM_EINVAL, "smlm_pkm_select_bag: the table must be 16-byte aligned");
   if (N == 0) return SMLM_OK;

@@ -3,8 +3,9 @@
     python -m smlm_hip.build            (from sparse-memory-lm_amd/)
 
 Every .hip file is compiled to an object in sparse-memory-lm_amd/_build/ (in parallel), then linked into
-smlm_hip/libsmlm_pkm.so next to this file, where smlm_hip._lib loads it.  The measurement kernels of bench.py
-(csrc/bench/*.hip) go into a separate smlm_hip/libsmlm_bench.so, so the lookup library holds only the product.
+smlm_hip/libsmlm_pkm.so next to this file, where smlm_hip._lib loads it.  The memory-ceiling kernels of bench.py
+(csrc/bench/*.hip: sequential read / write / copy and random-row reads) go into a separate smlm_hip/libsmlm_bench.so,
+so the lookup library holds only the product.
 """
 import os
 import subprocess

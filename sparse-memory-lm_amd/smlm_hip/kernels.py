@@ -158,24 +158,21 @@ def _bag(indices, weights, table, scales, pre, out_bf16, name):
 
 
 def bag_threads(row_bytes):
-    """Threads of the value bag's row-slot layout for rows of row_bytes (a multiple of 16): lcm(chunks, 64), at
-    least 128; whole rows within 256 if the lcm is larger (bag_threads of csrc/pkm_bag_dev.h)."""
+    """Threads of the value bag's canonical row-slot layout for rows of row_bytes (a multiple of 16): as many whole
+    rows of 16-byte chunks as fit in 192 threads for rows of up to 32 chunks, in 384 for wider rows, one at least
+    (bag_threads of csrc/pkm_bag_dev.h)."""
     cpr = row_bytes // 16
-    nthr = cpr // math.gcd(cpr, 64) * 64
-    if nthr > 256:
-        nthr = cpr * (256 // cpr)
-    while nthr < 128:
-        nthr *= 2
-    return nthr
+    budget = 192 if cpr <= 32 else 384
+    return (1 if cpr >= budget else budget // cpr) * cpr
 
 
 def select_bag_supported(heads, table, scales=None):
-    """Whether pk_select_bag takes this head count and table (at most 4 heads; the bag's row-slot layout must fit
-    in the 2 * heads wavefronts)."""
+    """Whether pk_select_bag takes this head count and table (at most 4 heads; a row's 16-byte chunks must not
+    outnumber the 2 * heads wavefronts' threads)."""
     if heads > 4 or table.dim() != 2:
         return False
     row_bytes = table.shape[1] * table.element_size()
-    return row_bytes % 16 == 0 and bag_threads(row_bytes) <= 2 * heads * 64
+    return row_bytes % 16 == 0 and row_bytes // 16 <= 2 * heads * 64
 
 
 def pk_select_bag(s1, s2, knn, table, scales=None, pre=None, out_bf16=False, record=False):

@@ -17,7 +17,7 @@ from torch import nn
 
 from . import kernels
 from .engram import EngramMemory, NgramHash
-from .pkm import ProductKeyMemory, inference_tables
+from .pkm import ProductKeyMemory, inference_tables, state_tag
 
 
 @dataclass
@@ -295,6 +295,7 @@ class Transformer(nn.Module):
                                 canon=ngram_canon) if cfg.eng_layers else None)
         self._decoders = {}
         self._fwd_graphs = {}
+        self._fwd_graphs_tag = None
         self._init_weights()
 
     @torch.no_grad()
@@ -385,8 +386,14 @@ class Transformer(nn.Module):
         """forward(idx) (logits, no cache, no targets) from a HIP graph captured once per input shape, device and
         autocast state and replayed: the same kernels as the eager forward without a host launch per op (a prompt
         pass of ~60 launches).  The returned logits are the graph's static output, overwritten by the next call
-        with the same shape; clone them to keep them.  Parameters are read where they live, so updated weights
-        are seen; set_memory_inference_table drops the graphs."""
+        with the same shape; clone them to keep them.  A graph reads the tensors it was captured with, among them
+        derived copies (cast sub-keys, the BatchNorm affine), so every graph is dropped and captured again when a
+        parameter or buffer has been replaced or written since (state_tag: an optimizer step, load_state_dict, new
+        BatchNorm statistics); set_memory_inference_table drops them too."""
+        tag = state_tag(self)
+        if tag != self._fwd_graphs_tag:
+            self._fwd_graphs.clear()
+            self._fwd_graphs_tag = tag
         ac = torch.is_autocast_enabled("cuda")
         key = (tuple(idx.shape), str(idx.device), ac, torch.get_autocast_dtype("cuda") if ac else None)
         entry = self._fwd_graphs.get(key)
@@ -412,6 +419,7 @@ class Transformer(nn.Module):
     def drop_graphs(self):
         """Forget the captured forward graphs (and their memory)."""
         self._fwd_graphs.clear()
+        self._fwd_graphs_tag = None
 
     def _ngram_rows(self, idx, kv_caches):
         """Engram rows of this chunk (smlm/model.py:270-279): the hash sees the last history tokens before the
@@ -538,8 +546,10 @@ class _FusedDecodeStep:
     def run(self, tok, pos, caches, hist, logits=False, record=None, chain=None):
         """The step for tok (B, 1) at device position pos: writes the next token to tok and hist[:, pos + 1] and
         advances pos.  With logits=True it returns the (B, vocab) bf16 logits instead and changes none of tok,
-        hist and pos (the KV caches get the same slot written).  With a dict `record`, record[layer] =
-        (s1, s2, scores, indices, weights) of each memory layer's lookup.
+        hist and pos (the KV caches get the same slot written).  With a dict `record`, record[layer] holds each
+        memory layer's lookup: "x" the residual stream entering its ffn_norm (B, d_model), "q" the query after the
+        BatchNorm and "pre" the swilu projection (bf16, as the kernels computed them), "s1", "s2" the sub-key scores,
+        "scores", "indices", "weights" the selection.
 
         With `chain` ((B, >= argmax blocks) int64 argmax keys, even row stride; not with logits) the step's token
         is the greedy choice from the keys the previous chained step left in chain (or that _StepDecoder seeded):
@@ -583,7 +593,8 @@ class _FusedDecodeStep:
                 else:
                     out, sc, idx, wt = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True,
                                                              record=True)
-                    record[i] = (s1, s2, sc, idx, wt)
+                    record[i] = {"x": x, "q": q, "pre": pre, "s1": s1, "s2": s2, "scores": sc, "indices": idx,
+                                 "weights": wt}
                 delta = kernels.decode_linear(m.value_proj.weight, out, bias=m.value_proj.bias)
             else:
                 f = blk.ffn
@@ -609,7 +620,11 @@ class _StepDecoder:
 
     On the fused kernels the steps are chained through `chain`, the lm_head's argmax keys: a step's first launch
     picks its token from the previous step's keys.  start() seeds the keys with the first token, finish() turns
-    the last step's keys into tok and its history slot; replay() and steps() end with it."""
+    the last step's keys into tok and its history slot; replay() and steps() end with it.
+
+    The graphs read the model's tensors and derived copies as they were at capture, so replay() captures them again
+    when a parameter or buffer has changed since (state_tag), and captures them at its first call if nothing did
+    before; a capture leaves the decoder's state (position, token, history, argmax keys, KV caches) as it found it."""
 
     run_lengths = (32, 8)   # graphs of this many steps in a row, longest first; then single steps
 
@@ -628,6 +643,7 @@ class _StepDecoder:
         self.hist = torch.zeros(B, max_len, dtype=torch.long, device=device)
         self.graph = None
         self.graph_runs = {}
+        self._graph_tag = None
         self.fused = _FusedDecodeStep(model) if _FusedDecodeStep.supported(model, dtype) else None
         self.chain = None
         if self.fused is not None:
@@ -674,9 +690,17 @@ class _StepDecoder:
         self.pos.add_(1)
 
     def _capture(self):
+        """Capture the single-step graph and the run graphs.  Two eager warm-up steps run first (library loads,
+        derived weights, allocator) from position 0; what they write -- position, token, history, argmax keys and
+        the KV cache slots 0 and 1 -- is saved before and restored after, so the state a caller set up (a prefilled
+        prompt, start()) survives a capture."""
         ac = torch.is_autocast_enabled("cuda")
         ctx = (torch.autocast("cuda", dtype=torch.get_autocast_dtype("cuda"), cache_enabled=False) if ac
                else torch.autocast("cuda", enabled=False))
+        warm = min(2, self.max_len)
+        saved = (self.pos.clone(), self.tok.clone(), self.hist.clone(),
+                 None if self.chain is None else self.chain.clone(),
+                 [(c.k[:, :, :warm].clone(), c.v[:, :, :warm].clone(), dict(c.extra)) for c in self.caches])
         self.pos.fill_(0)
         self.tok.zero_()
         if self.chain is not None:
@@ -684,9 +708,21 @@ class _StepDecoder:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side), ctx:
-            for _ in range(2):                      # warm-up: library loads, cached casts, allocator
+            for _ in range(warm):                   # warm-up: library loads, cached casts, allocator
                 self._step()
         torch.cuda.current_stream().wait_stream(side)
+        pos, tok, hist, chain, kv = saved
+        self.pos.copy_(pos)
+        self.tok.copy_(tok)
+        self.hist.copy_(hist)
+        if chain is not None:
+            self.chain.copy_(chain)
+        for c, (k, v, extra) in zip(self.caches, kv):
+            c.k[:, :, :warm].copy_(k)
+            c.v[:, :, :warm].copy_(v)
+            c.extra.clear()
+            c.extra.update(extra)
+        del saved, kv
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph), ctx:
             self._step()
@@ -699,11 +735,15 @@ class _StepDecoder:
                     for _ in range(k):
                         self._step()
                 self.graph_runs[k] = run
+        self._graph_tag = state_tag(self.model)
+
+    def _graphs_current(self):
+        return self.graph is not None and self._graph_tag == state_tag(self.model)
 
     def replay(self, n):
         """n decode steps as graph replays: as many runs of the longest run length as fit, then of the next, then
-        single steps; then finish()."""
-        if self.graph is None:
+        single steps; then finish().  Captures the graphs first if there are none or the model changed."""
+        if not self._graphs_current():
             self._capture()
         for k in sorted(self.graph_runs, reverse=True):
             for _ in range(n // k):
@@ -721,7 +761,7 @@ class _StepDecoder:
             use_graph = False               # Engram's conv and hash histories are new tensors every step
         for cache in self.caches:
             cache.extra.clear()             # no state of an earlier sequence
-        if use_graph and self.graph is None:
+        if use_graph and not self._graphs_current():
             self._capture()
         logits = self.model(prompt, kv_caches=self.caches, pos0=0)
         self.hist[:, :P] = prompt

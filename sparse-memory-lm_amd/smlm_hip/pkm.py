@@ -44,6 +44,16 @@ def inference_tables(values):
     return t
 
 
+def state_tag(module):
+    """(data_ptr, _version) of every parameter and buffer of `module`.  It changes whenever one of them is replaced
+    or written in place (an optimizer step, load_state_dict, new BatchNorm statistics), so a captured HIP graph,
+    which reads the tensors and the derived copies (cast sub-keys, BatchNorm affine) it was captured with, is
+    valid only while the tag it was captured under holds."""
+    out = [(t.data_ptr(), t._version) for t in module.parameters()]
+    out += [(t.data_ptr(), t._version) for t in module.buffers()]
+    return tuple(out)
+
+
 class ProductKeyMemory(nn.Module):
     """Same constructor as smlm/pkm.py:33-92 (impl defaults to "hip"; "torch" and "triton" are accepted)."""
 
@@ -105,9 +115,10 @@ class ProductKeyMemory(nn.Module):
         self.last_indices = None
         self.last_scores = None
         self.last_weights = None
+        self.last_lookup = None     # with record, also the no-grad lookup's input, query and sub-key scores
         self.decode_graph = False
         self._graph = None
-        self._keys_cache = None
+        self._keys_cache = {}
         self._bn_cache = None
         self.reset_parameters()
 
@@ -137,14 +148,16 @@ class ProductKeyMemory(nn.Module):
 
     # ---- lookup pieces -----------------------------------------------------------------------------------
     def _keys_as(self, dtype):
-        """The sub-keys in the scoring dtype; a cast copy is cached until the parameter changes."""
+        """The sub-keys in the scoring dtype; a cast copy per dtype is cached until the parameter changes (one per
+        dtype, so that asking for another dtype does not free a copy a captured graph reads)."""
         k = self.keys
         if k.dtype == dtype:
             return k.detach()
-        tag = (k.data_ptr(), k._version, dtype)
-        if self._keys_cache is None or self._keys_cache[0] != tag:
-            self._keys_cache = (tag, k.detach().to(dtype).contiguous())
-        return self._keys_cache[1]
+        tag = (k.data_ptr(), k._version)
+        hit = self._keys_cache.get(dtype)
+        if hit is None or hit[0] != tag:
+            hit = self._keys_cache[dtype] = (tag, k.detach().to(dtype).contiguous())
+        return hit[1]
 
     def subkey_scores(self, query):
         """query (N, heads, k_dim) -> scores against both sub-key sets, each (N, heads, n_keys)."""
@@ -173,10 +186,10 @@ class ProductKeyMemory(nn.Module):
     def _graph_forward(self, x):
         """Replay a HIP graph of _forward captured for this input shape (any token count): the same kernels as
         the eager path without the per-op launch cost.  Re-captured when the shape, dtype, autocast state or
-        inference table changes."""
+        inference table changes, or when a parameter or buffer was replaced or written (state_tag)."""
         ac = torch.is_autocast_enabled("cuda")
         tag = (tuple(x.shape), x.dtype, ac, torch.get_autocast_dtype("cuda") if ac else None,
-               id(getattr(self.values, "infer_table", None)))
+               id(getattr(self.values, "infer_table", None)), state_tag(self))
         if self._graph is None or self._graph[0] != tag:
             static_x = x.clone()
             ctx = (torch.autocast("cuda", dtype=tag[3], cache_enabled=False) if ac
@@ -273,6 +286,7 @@ class ProductKeyMemory(nn.Module):
             weights = torch.softmax(scores.float() * scale, dim=-1)
         if self.record:
             self.last_indices, self.last_scores, self.last_weights = indices, scores, weights
+            self.last_lookup = {"x": x, "q": q, "s1": s1, "s2": s2}
         idx, w = indices.view(N, -1), weights.view(N, -1)
         if self.swilu and bf16:
             # fused inference bag: value rows (bf16 / fp32 / int8 / q4 table) * bf16(silu(pre)), bf16 out

@@ -65,6 +65,28 @@ def test_argument_checks_return_status_codes():
     assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 0, 4, 1024, 32, fake, fake, fake, None) == _lib.OK
 
 
+def test_noalloc_lookup_validates_before_sizing():
+    """smlm_pkm_lookup_noalloc checks every argument of its two steps before it computes the scratch size, so
+    absurd head or key counts (whose N * H * NK product would overflow int64) are refused with a status code."""
+    lib = _lib.lib()
+    fake = 256
+    args = dict(q_row_stride=1 << 20, half=256, knn=32, table_dtype=_lib.BF16, rows=1 << 20, D=384)
+
+    def call(N, H, NK, **kw):
+        a = dict(args, **kw)
+        return lib.smlm_pkm_lookup_noalloc(fake, a["q_row_stride"], fake, _lib.BF16, N, H, NK, a["half"], a["knn"],
+                                           fake, a["table_dtype"], a["rows"], a["D"], None, None, fake, _lib.F32,
+                                           None)
+
+    assert call(64, 1 << 30, 1 << 30) == _lib.EINVAL and "bad shape" in _lib.last_error()       # H > 32768
+    assert call(64, 4, 0x7FFFFFFF) == _lib.EUNSUPPORTED and "NK" in _lib.last_error()            # NK > 65536
+    assert call(64, 16, 1024) == _lib.EUNSUPPORTED and "H=16" in _lib.last_error()               # fused: H <= 8
+    assert call(1024, 4, 1024) == _lib.EUNSUPPORTED and "scratch" in _lib.last_error()           # valid, too big
+    assert call(1 << 40, 4, 1024) == _lib.EUNSUPPORTED and "scratch" in _lib.last_error()        # N alone
+    assert call(-1, 4, 1024) == _lib.EINVAL
+    assert call(0, 4, 1024) == _lib.OK                                                          # no-op, no HIP
+
+
 def test_status_becomes_python_exception():
     with pytest.raises(_lib.SmlmError, match="status -1"):
         _lib.check(_lib.lib().smlm_pkm_quantize(None, _lib.F32, 1, 8, _lib.I8, None, None, None),

@@ -22,6 +22,7 @@ import torch
 
 import oracle.pkm_oracle as O
 import oracle.torch_path as TP
+import query_check as QC
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -38,7 +39,8 @@ def bits(t):
 
 def build_lm(n_keys, max_seq_len, seed=0):
     """The LM of configs 1-3 with every matrix, the sub-keys and the value table drawn from N(0, 0.02), in bf16
-    (bench.py builds the same model)."""
+    (bench.py builds the same model), and the memory layer's BatchNorm given statistics and affine parameters away
+    from the identity (so that its query check can tell the columns apart)."""
     from smlm_hip.model import ModelConfig, Transformer
     cfg = ModelConfig(vocab_size=32000, d_model=384, n_layers=6, n_heads=6, ffn_hidden=1024,
                       max_seq_len=max_seq_len, mem_layers=[MEM_LAYER], mem_n_keys=n_keys, mem_heads=4, mem_knn=32,
@@ -51,6 +53,7 @@ def build_lm(n_keys, max_seq_len, seed=0):
             if p.dim() >= 2 or name.endswith("keys"):
                 p.normal_(0.0, 0.02)
     model = model.to(torch.bfloat16).eval()
+    QC.randomize_batchnorm(model.layers[MEM_LAYER].ffn.query_norm, seed + 100)
     torch.cuda.empty_cache()
     model.set_memory_inference_table("bf16")
     return model
@@ -103,14 +106,17 @@ def decode_parity(model, B, P, steps, seed):
         rec = {}
         toks.append(dec.tok.clone().cpu())
         lg = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec)
-        s1, s2, sc, idx, w = rec[MEM_LAYER]
+        r = rec[MEM_LAYER]
+        s1, s2, sc, idx, w = r["s1"], r["s2"], r["scores"], r["indices"], r["weights"]
+        QC.check_decode_step_query(model, MEM_LAYER, r)
         check_selection(s1, s2, sc, idx, w, cfg.mem_knn)
         got_logits.append(lg.float().cpu())
         sels.append((idx.clone(), w.clone()))
         dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist)
         assert int(dec.pos) == P + t + 1
     eager = dec.hist[:, P:P + steps + 1].clone()
-    note(f"  B={B} P={P}: {steps} fused steps, selections bit-exact; checking logits on the host")
+    note(f"  B={B} P={P}: {steps} fused steps, queries and scores within bounds, selections bit-exact; checking "
+         f"logits on the host")
 
     # the reference torch path on the same tokens with the same selections
     sub, remapped = compact_rows(mem.values.weight, [sel_prompt[0]] + [s[0] for s in sels])
@@ -188,8 +194,10 @@ def test_config2_scoring_and_selection_at_bench_shape():
 @torch.no_grad()
 def test_config2_prefill_forward_b4m():
     """Config 2: one forward of the LM with the B-4M memory over 8 x 2048 uniform prompt tokens (no cache).  The
-    memory layer's selection for every token is recorded; the reference torch path given that selection must
-    give the same logits within 1e-2 of their scale at 64 positions of every sequence."""
+    memory layer's lookup for every token is recorded; on 256 of them its query (from the layer's input through
+    query_proj and the BatchNorm) and its sub-key scores are recomputed on the host and the selection is checked
+    bit-exact against the oracle; the reference torch path given the selection must give the same logits within
+    1e-2 of their scale at 64 positions of every sequence."""
     cfg_keys, B, T = 2048, 8, 2048
     note("config 2 prefill: building the LM with the B-4M table")
     model = build_lm(cfg_keys, T)
@@ -200,6 +208,13 @@ def test_config2_prefill_forward_b4m():
     mem.record = False
     idx, w = mem.last_indices.clone(), mem.last_weights.clone()
     assert idx.shape == (B * T, 4, 32)
+    rows = torch.cat([torch.arange(0, 64), torch.arange(B * T - 64, B * T),
+                      torch.randint(0, B * T, (128,), generator=torch.Generator().manual_seed(32))]).to(DEV)
+    QC.check_layer_query(mem, rows)
+    check_selection(mem.last_lookup["s1"].index_select(0, rows), mem.last_lookup["s2"].index_select(0, rows),
+                    mem.last_scores.index_select(0, rows), idx.index_select(0, rows), w.index_select(0, rows), 32)
+    mem.last_lookup = None
+    note("  prompt-pass query, scores and selection of 256 tokens pinned")
     pos = torch.cat([torch.arange(0, 16), torch.arange(T - 48, T)])
     got = logits[:, pos.to(DEV)].float().cpu()
     del logits
@@ -233,6 +248,68 @@ def test_forward_graphed_equals_eager():
     assert len(model._fwd_graphs) == 2
     model.set_memory_inference_table("bf16")             # a table switch drops the graphs
     assert len(model._fwd_graphs) == 0
+    del model
+    torch.cuda.empty_cache()
+
+
+@torch.no_grad()
+def test_graphs_follow_parameter_changes():
+    """A captured graph reads the tensors and derived copies (cast sub-keys, BatchNorm affine, the concatenated
+    query | swilu weights) of its capture.  After the memory layer's BatchNorm statistics and sub-keys are written
+    in place, forward_graphed and the whole-step decode graphs must give what the eager forward and eager steps
+    give with the new values (they are captured again), on replays with eager work between them."""
+    note("graphs after parameter changes: configs LM, NK 256")
+    model = build_lm(256, 512)
+    mem = model.layers[MEM_LAYER].ffn
+    g = torch.Generator().manual_seed(6)
+    prompt = torch.randint(0, 32000, (2, 100), generator=g).to(DEV)
+    gen_prompt = torch.randint(0, 32000, (2, 20), generator=g).to(DEV)
+    before = model.forward_graphed(prompt).clone()
+    assert np.array_equal(bits(before), bits(model(prompt)))
+    gen_before = model.generate(gen_prompt, 40, use_graph=True)
+    assert torch.equal(gen_before, model.generate(gen_prompt, 40, use_graph=False))
+    for change in ("batchnorm", "keys"):
+        if change == "batchnorm":
+            mem.query_norm.running_var.mul_(3.0)
+            mem.query_norm.running_mean.add_(0.2)
+        else:
+            mem.keys.mul_(-1.0)
+        for rep in range(2):
+            got = model.forward_graphed(prompt).clone()
+            eager = model(prompt)
+            assert np.array_equal(bits(got), bits(eager)), f"forward_graphed after the {change} change, replay {rep}"
+        assert not np.array_equal(bits(got), bits(before)), f"the {change} change must change the logits"
+        gen_graph = model.generate(gen_prompt, 40, use_graph=True)
+        gen_eager = model.generate(gen_prompt, 40, use_graph=False)
+        assert torch.equal(gen_graph, gen_eager), f"decode graphs after the {change} change"
+    del model
+    torch.cuda.empty_cache()
+
+
+@torch.no_grad()
+def test_lazy_capture_in_replay_keeps_the_prompt_state():
+    """replay() on a decoder without graphs captures them first; the capture's warm-up steps write position 0 and
+    1 of the KV caches, the token, the position, the history and the argmax keys, and must put them back, so a
+    prompt prefilled and started before the first replay decodes as eager steps from the same state do."""
+    note("lazy capture in replay: configs LM, NK 256")
+    model = build_lm(256, 512)
+    B, P, n = 2, 30, 40
+    prompt = torch.randint(0, 32000, (B, P), generator=torch.Generator().manual_seed(8)).to(DEV)
+    out = []
+    for graphs in (False, True):
+        model._decoders.clear()
+        dec = model._decoder(B, P + n + 1, DEV)
+        assert dec.graph is None
+        logits = model(prompt, kv_caches=dec.caches, pos0=0)
+        dec.hist[:, :P] = prompt
+        dec.start(logits[:, -1].argmax(-1), P)
+        if graphs:
+            dec.replay(n)
+            assert dec.graph is not None
+        else:
+            dec.steps(n)
+        out.append(dec.hist[:, P:P + n + 1].clone())
+    assert torch.equal(out[0], out[1]), "the lazily captured replay differs from the eager steps"
     del model
     torch.cuda.empty_cache()
 

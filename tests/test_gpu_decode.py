@@ -317,9 +317,14 @@ def _tables(kind, rows, D, seed):
     (9, 3, 2048, 64, torch.bfloat16, "bf16", True, False),
     (4, 2, 2048, 32, torch.float32, "bf16", True, True),
     (2, 4, 8192, 32, torch.bfloat16, "bf16", True, True),     # rows beyond the register path: streaming search
+    (3, 1, 512, 16, torch.bfloat16, "bf16", True, True),      # 2 thread slots run the 8 bf16 slots
+    (4, 1, 256, 32, torch.bfloat16, "fp32", False, True),     # 1 thread slot runs the 4 fp32 slots
+    (6, 1, 1024, 32, torch.bfloat16, "int8", True, False),    # 5 thread slots run the 8 int8 slots
 ])
 def test_select_bag_bit_identical_to_select_then_bag(N, H, NK, knn, dtype, kind, with_pre, out_bf16):
-    """pk_select_bag == pk_select followed by bag_infer, bit for bit (same selection, same bag additions)."""
+    """pk_select_bag == pk_select followed by bag_infer, bit for bit (same selection, same bag additions in the
+    canonical row-slot order, also where the fused workgroup has fewer threads than the layout and runs several
+    slots per thread)."""
     note(f"select_bag N={N} H={H} NK={NK} knn={knn} {dtype} {kind}")
     g = torch.Generator().manual_seed(N * 31 + NK + knn)
     D = 384
@@ -345,10 +350,12 @@ def test_select_bag_rejects_unsupported():
     t = torch.zeros(64 * 64, 384, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
         K.pk_select_bag(s, s, 8, t)
-    s1 = torch.zeros(1, 1, 64, dtype=torch.bfloat16, device=DEV)               # 1 head: 128 threads < 192
-    assert not K.select_bag_supported(1, t)
+    s1 = torch.zeros(1, 1, 64, dtype=torch.bfloat16, device=DEV)               # 1 head: 128 threads
+    assert K.select_bag_supported(1, t)                                        # 48 chunks per row: fits
+    wide = torch.zeros(64 * 64, 640, dtype=torch.float32, device=DEV)          # 160 chunks per row: does not
+    assert not K.select_bag_supported(1, wide)
     with pytest.raises(_lib.SmlmError):
-        K.pk_select_bag(s1, s1, 8, t)
+        K.pk_select_bag(s1, s1, 8, wide)
 
 
 # ------------------------------------------------------------------------------------------- the fused decode step
@@ -442,13 +449,15 @@ def test_fused_generate_multi_step_graph_matches_eager(monkeypatch, proj_max):
 @pytest.mark.parametrize("proj_max", [0, 64])
 @torch.no_grad()
 def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
-    """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its selection is
-    bit-exact against the oracle on the step's own sub-key scores, and its logits are within 1e-2 of the fp32
-    torch path (oracle/torch_path.py) given that selection (the prompt pass does not reach the step through
-    the last block, so the caches agree)."""
+    """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its query and swilu
+    projection match the host recomputation from the step's residual row (tests/query_check.py), its sub-key
+    scores the fp64 products of that query, its selection is bit-exact against the oracle on those scores, and
+    its logits are within 1e-2 of the fp32 torch path (oracle/torch_path.py) given that selection (the prompt
+    pass does not reach the step through the last block, so the caches agree)."""
     import numpy as np
     import oracle.pkm_oracle as O
     import oracle.torch_path as TP
+    import query_check as QC
     from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
     monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=512, d_model=128, n_layers=3, n_heads=2, ffn_hidden=256, max_seq_len=64,
@@ -469,7 +478,9 @@ def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
         assert dec.fused is not None
         rec = {}
         got = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec).float().cpu()
-        s1, s2, sc, idx, w = rec[2]
+        r = rec[2]
+        s1, s2, sc, idx, w = r["s1"], r["s2"], r["scores"], r["indices"], r["weights"]
+        QC.check_decode_step_query(m, 2, r)
         rs, ri, rw = O.pk_select(_bits(s1), _bits(s2), cfg.mem_knn)
         assert np.array_equal(idx.cpu().numpy(), ri) and np.array_equal(_bits(sc), rs)
         np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)

@@ -218,7 +218,10 @@ def close(a, b):
 BAG_CASES = [("f32", 1 << 20, 384, 512, 128), ("bf16", 1 << 20, 384, 512, 128), ("i8", 1 << 20, 384, 512, 128),
              ("q4", 1 << 20, 384, 512, 128), ("bf16", 4096, 64, 32, 96), ("f32", 4096, 64, 32, 48),
              ("q4", 4096, 64, 32, 40), ("i8", 4096, 64, 32, 40), ("i8", 1000, 24, 16, 12), ("bf16", 1000, 24, 9, 7),
-             ("f32", 2048, 96, 64, 128), ("bf16", 300, 384, 3, 1), ("bf16", 1 << 16, 384, 2, 600)]
+             ("f32", 2048, 96, 64, 128), ("bf16", 300, 384, 3, 1), ("bf16", 1 << 16, 384, 2, 600),
+             # wide rows: 2 slots of 130 chunks, 1 slot of 200 and of 256 chunks (the row kernel's widest), 257
+             # chunks (the generic kernel)
+             ("bf16", 512, 1040, 3, 9), ("f32", 512, 800, 4, 17), ("f32", 512, 1024, 4, 33), ("f32", 256, 1028, 2, 5)]
 
 
 @pytest.mark.parametrize("kind,rows,D,N,K_", BAG_CASES)
@@ -362,12 +365,19 @@ def _attention_oracle(qkv, cos, sin, kc, vc, P, H, hd):
                                                     (1, 6, 64, 1100, 1050, "f32"), (64, 6, 64, 600, 64, "bf16"),
                                                     (64, 6, 64, 600, 512, "bf16"), (64, 6, 64, 600, 513, "f32"),
                                                     (2, 6, 64, 800, 768, "bf16"), (2, 6, 64, 800, 769, "f32"),
-                                                    (100, 6, 64, 300, 256, "bf16"), (100, 6, 64, 300, 257, "bf16")])
+                                                    (100, 6, 64, 300, 256, "bf16"), (100, 6, 64, 300, 257, "bf16"),
+                                                    (64, 6, 64, 400, 47, "bf16"), (64, 6, 64, 400, 48, "f32"),
+                                                    (64, 6, 64, 400, 49, "bf16"), (64, 6, 64, 400, 383, "bf16"),
+                                                    (64, 6, 64, 400, 384, "f32"), (64, 6, 64, 400, 385, "bf16"),
+                                                    (48, 6, 32, 800, 768, "bf16"), (48, 6, 32, 800, 97, "f32"),
+                                                    (64, 6, 128, 400, 192, "bf16"), (64, 6, 128, 400, 193, "f32"),
+                                                    (2, 6, 64, 800, 512, "bf16"), (2, 6, 64, 800, 513, "f32")])
 def test_decode_attention_matches_oracle(B, H, hd, max_len, P, rope):
-    """512 / 256 threads per (sequence, head), head_dim 16-128, fp32 and bf16 rope tables, position 0, the last
-    slot, and a cache longer than one group of row loads (the rows past the first group loaded in a second round
-    trip); positions on and just past a pass or a group boundary of each thread count (512 threads: 64 rows a pass,
-    512 a group; 256: 32 and 256)."""
+    """512 / 384 / 256 threads per (sequence, head) (B x H below 256, below 512, from 512), head_dim 16-128, fp32
+    and bf16 rope tables, position 0, the last slot, and a cache longer than one group of row loads (the rows past
+    the first group loaded in a second round trip); positions on and just past a pass or a group boundary of each
+    thread count: at head_dim 64, 512 threads take 64 rows a pass and 512 a group, 384 threads 48 and 384, 256
+    threads 32 and 256; at 384 threads head_dim 32 takes 96 and 768, head_dim 128 24 and 192."""
     note(f"decode attention B={B} H={H} hd={hd} max_len={max_len} P={P}")
     g = torch.Generator().manual_seed(B * 1000 + P)
     C = H * hd
@@ -405,8 +415,8 @@ def test_decode_attention_bad_position():
     assert not kc.any() and not vc.any()
 
 
-# B x H picks 1024 / 512 / 256 threads; the wo rows cover one or several loads of a workgroup's wo registers;
-# P past 768 makes the 1024-thread variant load its cache rows in two groups
+# B x H picks 512 / 384 / 256 threads; the wo rows cover one or several loads of a workgroup's wo registers;
+# P past 512 makes the 512-thread variant load its cache rows in two groups
 @pytest.mark.parametrize("B,H,hd,max_len,P,N", [(1, 6, 64, 394, 300, 384), (4, 6, 64, 1100, 767, 384),
                                                 (2, 6, 64, 1100, 1000, 1500), (64, 6, 64, 394, 200, 384),
                                                 (100, 6, 64, 64, 30, 384), (3, 4, 32, 100, 57, 200),

@@ -71,3 +71,22 @@ def test_noalloc_lookup_refuses_more_than_the_array(tables):
     assert rc == _lib.EUNSUPPORTED and "scratch" in _lib.last_error()
     torch.cuda.synchronize()
     assert bool((out == 7.0).all()), "a refused call must not launch anything"
+
+
+@torch.no_grad()
+def test_noalloc_lookup_refuses_absurd_shapes_before_sizing(tables):
+    """Head and key counts whose N * H * NK product would overflow int64 are refused by the argument checks of the
+    two steps, which run before the scratch size is computed; nothing is launched."""
+    table, _ = tables["bf16"]
+    q = torch.zeros(4, H, 2 * HALF, dtype=torch.bfloat16, device=DEV)
+    out = torch.full((4, D), 7.0, device=DEV)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    for h, nk, code in ((1 << 30, 1 << 30, _lib.EINVAL), (H, 0x7FFFFFFF, _lib.EUNSUPPORTED)):
+        note(f"lookup_noalloc refused shape: H={h} NK={nk}")
+        rc = lib.smlm_pkm_lookup_noalloc(q.data_ptr(), 1 << 20, q.data_ptr(), _lib.BF16, 4, h, nk, HALF, KNN,
+                                         table.data_ptr(), _lib.BF16, table.shape[0], D, None, None, out.data_ptr(),
+                                         _lib.F32, stream)
+        assert rc == code, _lib.last_error()
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all()), "a refused call must not launch anything"
