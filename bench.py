@@ -354,9 +354,57 @@ def memory_ceilings(dev, reps, read_buf, rows_table, rows_idx):
     return out
 
 
-def lookup_prefill(dev, reps):
+def cpu_lookup_c2(q, keys, table, pre, idx_gpu, tokens, reps=3):
+    """Config 2's lookup on the host cores over its first `tokens` tokens: the reference's torch path from the query
+    on (smlm/pkm.py:117-148, 205-223: the two sub-key einsums, topk per half, top-k over the knn^2 Cartesian sums,
+    softmax, the weighted bag of the bf16 rows, times silu of the swilu input), in fp32 on the same query, sub-keys
+    and bf16 table (oracle/torch_path.py's functions); median of `reps` timed runs after one untimed.  The selected
+    rows are compared with the GPU's (the fp32 einsum and the kernels' bf16 scores may order near-ties
+    differently)."""
+    import torch
+    import torch.nn.functional as F
+    import oracle.torch_path as TP
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    t0 = time.perf_counter()
+    qh = q[:tokens].float().cpu()
+    kh = keys.float().cpu()
+    th = table.cpu()
+    ph = pre[:tokens].float().cpu()
+    copy_s = time.perf_counter() - t0
+    N, H, kd = qh.shape
+    half = kd // 2
+
+    def run():
+        s1 = torch.einsum("nhd,hkd->nhk", qh[..., :half], kh[:, 0])
+        s2 = torch.einsum("nhd,hkd->nhk", qh[..., half:], kh[:, 1])
+        sc, idx = TP.pkm_select_torch(s1, s2, 32)
+        w = torch.softmax(sc, -1)
+        rows = F.embedding(idx.view(N, -1), th).float()
+        out = torch.einsum("nj,njd->nd", w.view(N, -1), rows)
+        return (out * F.silu(ph)).to(torch.bfloat16), idx
+
+    with torch.no_grad():
+        run()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            _, idx = run()
+            ts.append(time.perf_counter() - t)
+    ts.sort()
+    dt = ts[len(ts) // 2]
+    g = idx_gpu[:tokens].cpu()
+    same = float((idx.sort(-1).values == g.sort(-1).values).double().mean())
+    return {"value": tokens / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the first {tokens} of the 16,384 tokens: query -> scores -> selection -> softmax -> bag "
+                      f"(x silu) in fp32 on the bf16 table, median of {reps} ({dt:.2f} s each; host copies "
+                      f"{copy_s:.1f} s untimed), reference torch path restated in oracle/torch_path.py",
+            "selected_rows_equal_to_gpu_frac": same}
+
+
+def lookup_prefill(dev, reps, cpu_tokens=0):
     """Config 2 PKM lookup: 8 x 2048 tokens, 4 heads x 2 halves x 2048 sub-keys of 256, top-32, 4M x 384 bf16
-    table; scoring, selection and bag kernels timed separately with HIP events."""
+    table; scoring, selection and bag kernels timed separately with HIP events.  With cpu_tokens, the torch path
+    on the host cores over that many of the tokens (cpu_lookup_c2)."""
     import torch
     from smlm_hip import kernels as K
     N, H, kd, NK, D = 8 * 2048, 4, 512, 2048, 384
@@ -377,6 +425,9 @@ def lookup_prefill(dev, reps):
            "tok_s": N / total * 1e3, "score_TFLOPs": flops / ms_score / 1e9,
            "score_write_GBps": 2 * N * H * NK * 2 / ms_score / 1e6,
            "bag_alg_GBps": N * 128 * (2 * D + 12) / ms_bag / 1e6}
+    if cpu_tokens:
+        res["cpu_baseline"] = cpu_lookup_c2(q, keys, table, pre, idx, cpu_tokens)
+        log(f"cpu baseline config 2 lookup: {res['cpu_baseline']}")
     del q, keys, table, pre, s1, s2, sc, idx, w
     torch.cuda.empty_cache()
     return res
@@ -836,6 +887,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=GEN_TOKENS, help="most CPU-baseline decode steps")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU-baseline decode timing budget")
     ap.add_argument("--cpu-gather-tokens", type=int, default=2048, help="config-4 tokens timed on the host")
+    ap.add_argument("--cpu-lookup-tokens", type=int, default=1024, help="config-2 lookup tokens timed on the host")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--phases", default=HEADLINE_PHASES + "," + OPTIONAL_PHASES,
                     help="subset of " + HEADLINE_PHASES + "," + OPTIONAL_PHASES + ",calibrate (profiling runs); "
@@ -963,9 +1015,16 @@ def main():
         def config1():
             m1 = build_lm(lm_config(1024, 1024), dev)
             tok_s, ms_gen, ms_tok = time_generations(m1, 1, args.steps, args.warmup, dev, prompt_len=512)
+            out = {"tok_s": tok_s, "ms_per_generation": ms_gen, "ms_per_token_step": ms_tok, "batch": 1,
+                   "prompt_len": 512, "new_tokens": GEN_TOKENS, "table": "1,048,576 x 384 bf16 (B-1M)"}
+            if "cpu" in phases:
+                sd = host_state(m1)
+                out["cpu_baseline"] = dict(cpu_decode(sd, m1.cfg.to_dict(), 1, args.cpu_steps, args.cpu_seconds / 2,
+                                                      prompt_len=512), **cpu_info())
+                log(f"cpu baseline config 1: {out['cpu_baseline']}")
+                del sd
             del m1
-            return {"tok_s": tok_s, "ms_per_generation": ms_gen, "ms_per_token_step": ms_tok, "batch": 1,
-                    "prompt_len": 512, "new_tokens": GEN_TOKENS, "table": "1,048,576 x 384 bf16 (B-1M)"}
+            return out
 
         line["decode_config1_bs1"] = phase("config1", config1)
         line["layer_config0"] = phase("config0", lambda: layer_config0(dev, args.reps))
@@ -993,7 +1052,8 @@ def main():
             return out
 
         line["prefill_config2"] = phase("prefill", prefill)
-        line["pkm_lookup_config2"] = phase("lookup", lambda: lookup_prefill(dev, args.reps))
+        line["pkm_lookup_config2"] = phase("lookup", lambda: lookup_prefill(
+            dev, args.reps, cpu_tokens=args.cpu_lookup_tokens if "cpu" in phases else 0))
         if R.get("lookup"):
             lk = R["lookup"]
             line["roofline_score"] = {

@@ -30,7 +30,16 @@ namespace {
 
 constexpr int kCap = 1024;       // LDS candidates per half
 constexpr int kRegCand = 4;      // candidates per lane held in registers for the exact search (C <= 256)
-constexpr int kMaxKnn = 64;
+constexpr int kMaxKnn = 64;      // power-of-two knn up to this: the constant pair table, one result per lane
+constexpr int kMaxKnnGen = 128;  // any other knn up to this: pairs built at run time, two results per lane
+constexpr int kGenPairSlots = 11;  // pairs of knn = 128: sum_{i=1}^{128} floor(128 / i) = 645 <= 11 * 64
+
+// Bits of a sub-key index below NK (any NK >= 1) and of a table index below NK^2: the bits of a key's index field
+// above these are set in every key (the field holds 2^B - 1 - index).
+__device__ __host__ __forceinline__ int index_bits(int NK) { return NK <= 1 ? 0 : 32 - __builtin_clz((uint32_t)NK - 1); }
+__device__ __host__ __forceinline__ int pair_bits(int NK) {
+  return NK <= 1 ? 0 : 64 - __builtin_clzll((uint64_t)NK * (uint64_t)NK - 1);
+}
 
 // ---- the Cartesian pair list, built at compile time: for knn = 2^lg, pairs [off[lg], off[lg+1]) ------------
 // Pair p of knn = 2^lg is ij[off[lg] + p] = i | j << 8; entries past the list read as kNoPair.
@@ -129,7 +138,8 @@ __device__ __forceinline__ int count_ge_lanes(Key v, Key c) {
   return (int)__popcll(__builtin_amdgcn_ballot_w64(v >= c));
 }
 
-// rank of u among the n (a multiple of 4 not above kMaxKnn) keys of sel[]: how many are larger; 16-byte reads
+// rank of u among the n keys of sel[] (n a multiple of 4, zero keys past the real ones): how many are larger;
+// 16-byte reads
 template <typename Key>
 __device__ __forceinline__ int rank_in(const Key *sel, int n, Key u) {
   constexpr int PER = 16 / (int)sizeof(Key);
@@ -207,8 +217,9 @@ __device__ __forceinline__ void bitonic_sort_desc(Key (&x)[SLOTS]) {
   if constexpr (K < SLOTS * kWave) bitonic_sort_desc<Key, SLOTS, K * 2>(x);
 }
 
-// The knn keys >= t (exactly knn exist) from `src` (n entries, LDS) into out[] in descending order.
-template <typename Key, typename Fetch>
+// The knn keys >= t (exactly knn exist) from `src` (n entries, LDS) into out[] in descending order; sel[] and out[]
+// hold MAXK keys.
+template <typename Key, int MAXK, typename Fetch>
 __device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetch, Key *sel, Key *out) {
   const int lane = lane_id();
   int S = 0;
@@ -218,20 +229,30 @@ __device__ __forceinline__ void collect_sorted(int n, int knn, Key t, Fetch fetc
     const bool ge = p < n && u >= t;
     const uint64_t m = ballot(ge);
     const int pos = S + lanes_below(m);
-    if (ge && pos < kMaxKnn) sel[pos] = u;
+    if (ge && pos < MAXK) sel[pos] = u;
     S += (int)__popcll(m);
   }
-  if (lane >= knn && lane < 4) sel[lane] = 0;     // pad knn < 4 to whole 16-byte reads
-  wave_lds_sync();
-  if (lane < knn) {
-    const Key u = sel[lane];
-    out[rank_in(sel, knn < 4 ? 4 : knn, u)] = u;
+  if constexpr (MAXK <= kWave) {
+    if (lane >= knn && lane < 4) sel[lane] = 0;     // pad knn < 4 to whole 16-byte reads
+    wave_lds_sync();
+    if (lane < knn) {
+      const Key u = sel[lane];
+      out[rank_in(sel, knn < 4 ? 4 : knn, u)] = u;
+    }
+  } else {
+    const int padded = (knn + 7) & ~7;              // zero keys up to whole pairs of 16-byte reads
+    for (int q = knn + lane; q < padded; q += kWave) sel[q] = 0;
+    wave_lds_sync();
+    for (int q = lane; q < knn; q += kWave) {
+      const Key u = sel[q];
+      out[rank_in(sel, padded, u)] = u;
+    }
   }
   wave_lds_sync();
 }
 
 // Exact top-knn among C candidate keys in LDS (keys of sub-key indices < 2^IB), into out[] descending.
-template <bool F32>
+template <bool F32, int MAXK>
 __device__ __forceinline__ void topk_of_candidates(int C, int knn, int IB, typename SelKey<F32>::T *cand,
                                                    typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
@@ -267,22 +288,27 @@ __device__ __forceinline__ void topk_of_candidates(int C, int knn, int IB, typen
       return n;
     });
   }
-  collect_sorted<Key>(C, knn, t, [&](int p) { return cand[p]; }, sel, out);
+  collect_sorted<Key, MAXK>(C, knn, t, [&](int p) { return cand[p]; }, sel, out);
 }
 
-// Streaming half top-k: any NK, searching the row in global memory.
-template <bool F32, int CAP>
+// Streaming half top-k: any NK, searching the row in global memory.  Up to 64 lanes, the knn-th largest lane maximum
+// bounds the answer from below; a larger knn takes every element as a candidate (or, past the LDS, the exact search
+// over the row).
+template <bool F32, int CAP, int MAXK>
 __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
                                  typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
   constexpr int kBits = F32 ? 64 : 32;
   const int lane = lane_id();
-  Key mx = 0;
-  for (int k = lane; k < NK; k += kWave) {
-    const Key u = half_key<F32>(row, k);
-    mx = u > mx ? u : mx;
+  Key t0 = 0;
+  if (knn <= kWave) {
+    Key mx = 0;
+    for (int k = lane; k < NK; k += kWave) {
+      const Key u = half_key<F32>(row, k);
+      mx = u > mx ? u : mx;
+    }
+    t0 = threshold_search<Key>(knn, kBits, [&](Key t) { return count_ge_lanes(mx, t); });
   }
-  const Key t0 = threshold_search<Key>(knn, kBits, [&](Key t) { return count_ge_lanes(mx, t); });
   int C = 0;
   for (int k0 = 0; k0 < NK; k0 += kWave) {
     const int k = k0 + lane;
@@ -295,7 +321,7 @@ __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelK
   }
   wave_lds_sync();
   if (C <= CAP) {
-    topk_of_candidates<F32>(C, knn, 31 - __builtin_clz(NK), cand, sel, out);
+    topk_of_candidates<F32, MAXK>(C, knn, index_bits(NK), cand, sel, out);
     return;
   }
   const Key t1 = threshold_search<Key>(knn, kBits, [&](Key t) {
@@ -306,7 +332,7 @@ __device__ void half_topk_stream(const void *row, int NK, int knn, typename SelK
     }
     return cnt;
   });
-  collect_sorted<Key>(NK, knn, t1, [&](int k) { return half_key<F32>(row, k); }, sel, out);
+  collect_sorted<Key, MAXK>(NK, knn, t1, [&](int k) { return half_key<F32>(row, k); }, sel, out);
 }
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
@@ -336,14 +362,14 @@ __device__ __forceinline__ uint4 chunk_codes(uint4 v) {
 //   5. the exact top knn of the candidates, in descending order.
 // The wavefront's CAP keys of LDS hold the candidates at the front and the staging area (16 bytes + chunk index
 // per lane) at the back; a row with more candidates than fit takes the streaming path.
-template <bool F32, int CPL, int CAP>
+template <bool F32, int CPL, int CAP, int MAXK>
 __device__ __forceinline__ void half_topk_reg(const void *row, int NK, int knn, typename SelKey<F32>::T *cand,
-                              typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
+                                              typename SelKey<F32>::T *sel, typename SelKey<F32>::T *out) {
   using Key = typename SelKey<F32>::T;
   constexpr int EPC = F32 ? 4 : 8;  // elements per chunk
   constexpr int kStageBytes = kWave * (16 + 4);
   constexpr int kCandMax = (CAP * (int)sizeof(Key) - kStageBytes) / (int)sizeof(Key);
-  static_assert(kCandMax >= kMaxKnn, "candidate area too small");
+  static_assert(kCandMax >= MAXK, "candidate area too small");
   uint4 *stage = (uint4 *)((char *)cand + CAP * sizeof(Key) - kStageBytes);
   uint32_t *stage_id = (uint32_t *)(stage + kWave);
   const int lane = lane_id();
@@ -419,9 +445,9 @@ __device__ __forceinline__ void half_topk_reg(const void *row, int NK, int knn, 
     wave_lds_sync();  // the staging area is rewritten by the next round
   }
   if (C <= kCandMax) {
-    topk_of_candidates<F32>(C, knn, 31 - __builtin_clz(NK), cand, sel, out);
+    topk_of_candidates<F32, MAXK>(C, knn, index_bits(NK), cand, sel, out);
   } else {
-    half_topk_stream<F32, CAP>(row, NK, knn, cand, sel, out);
+    half_topk_stream<F32, CAP, MAXK>(row, NK, knn, cand, sel, out);
   }
 }
 
@@ -475,8 +501,8 @@ __device__ __forceinline__ uint64_t cartesian_threshold(const typename SelKey<F3
       ck[s] = ((uint64_t)code << 32) | (uint64_t)(0xFFFFFFFFu - full);
     }
   }
-  // table indices are below NK^2 = 2^(2 log2 NK): the bits above them in the low word are set in every key
-  const int IB = 2 * (31 - __builtin_clz(NK));
+  // table indices are below NK^2 <= 2^IB: the bits above them in the low word are set in every key
+  const int IB = pair_bits(NK);
   const uint64_t t = key_search<uint64_t>(knn, F32 ? 64 : 48, 32, IB, [&](uint64_t c) {
     int n = 0;
 #pragma unroll
@@ -560,37 +586,175 @@ __device__ __forceinline__ bool cartesian_topk(const typename SelKey<F32>::T *to
   return true;
 }
 
-template <bool F32, int CPL>
+
+// ---- any knn up to kMaxKnnGen: the pair list built at run time, two results per lane ----------------------------
+// Pairs (i, j) with (i + 1)(j + 1) <= knn in row order: pair p is (i, p - pre[i]) for the row i with
+// pre[i] <= p < pre[i + 1], pre[i] = sum_{r < i} floor(knn / (r + 1)) (the same list, in the same order, as the
+// constant table's).  pre: the wavefront's LDS scratch of at least kMaxKnnGen + 1 ints.  Slots past the list hold
+// kNoPair; returns the pair count.
+__device__ __forceinline__ int gen_pairs(int knn, int *pre, uint32_t (&pc)[kGenPairSlots]) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int r0 = 0; r0 < knn; r0 += kWave) {  // at most two rounds
+    const int i = r0 + lane;
+    const int c = i < knn ? knn / (i + 1) : 0;
+    int total;
+    const int ex = wave_exclusive_sum(c, &total);
+    if (i < knn) pre[i] = carry + ex;
+    carry += total;
+  }
+  wave_lds_sync();
+  const int P = carry;
+  int cur[kGenPairSlots];
+#pragma unroll
+  for (int s = 0; s < kGenPairSlots; ++s) cur[s] = 0;
+  // the last row whose start is <= p, seven bisection steps (knn <= 128) over all slots at once
+#pragma unroll
+  for (int b = 6; b >= 0; --b) {
+#pragma unroll
+    for (int s = 0; s < kGenPairSlots; ++s) {
+      const int probe = cur[s] | (1 << b);
+      const int p = s * kWave + lane;
+      if (probe < knn && pre[probe] <= p) cur[s] = probe;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < kGenPairSlots; ++s) {
+    const int p = s * kWave + lane;
+    pc[s] = p < P ? (uint32_t)cur[s] | ((uint32_t)(p - pre[cur[s]]) << 8) : kNoPair;
+  }
+  wave_lds_sync();
+  return P;
+}
+
+// Cartesian step of one head for any knn <= kMaxKnnGen (wavefront 0 of the head only): the pairs' keys, the exact
+// knn-th largest by the threshold search, the keys at or above it compacted and ranked through LDS (s_fsel, s_fin:
+// kMaxKnnGen entries each), then the fp32 softmax.  Lane l holds results j = l (r = 0) and j = l + 64 (r = 1) for
+// j < knn: score sc[r] (code[r] = its order code), table index full[r], weight wt[r].
+template <bool F32>
+__device__ __forceinline__ void cartesian_general(const typename SelKey<F32>::T *top1,
+                                                  const typename SelKey<F32>::T *top2, int NK, int knn,
+                                                  const uint32_t (&pc)[kGenPairSlots], uint64_t *s_fsel,
+                                                  uint64_t *s_fin, float (&sc)[2], uint32_t (&full)[2],
+                                                  uint32_t (&code)[2], float (&wt)[2]) {
+  using Key = typename SelKey<F32>::T;
+  const int lane = lane_id();
+  uint64_t ck[kGenPairSlots];
+#pragma unroll
+  for (int s = 0; s < kGenPairSlots; ++s) {
+    ck[s] = 0;  // no pair: key 0, never counted (every tested threshold is >= 1)
+    if (pc[s] != kNoPair) {
+      const Key k1 = top1[pc[s] & 0xFFu];
+      const Key k2 = top2[pc[s] >> 8];
+      const float sum = key_value<F32>(k1) + key_value<F32>(k2);
+      const uint32_t cd = F32 ? order32(__float_as_uint(sum)) : order16(bf16_bits_rtne(sum));
+      const uint32_t f = key_index<F32>(k1) * (uint32_t)NK + key_index<F32>(k2);
+      ck[s] = ((uint64_t)cd << 32) | (uint64_t)(0xFFFFFFFFu - f);
+    }
+  }
+  const uint64_t t = key_search<uint64_t>(knn, F32 ? 64 : 48, 32, pair_bits(NK), [&](uint64_t c) {
+    int n = 0;
+#pragma unroll
+    for (int s = 0; s < kGenPairSlots; ++s) n += count_ge_lanes(ck[s], c);
+    return n;
+  });
+  int S = 0;
+#pragma unroll
+  for (int s = 0; s < kGenPairSlots; ++s) {
+    const bool ge = ck[s] >= t;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(ge);
+    const int pos = S + lanes_below(m);
+    if (ge && pos < kMaxKnnGen) s_fsel[pos] = ck[s];
+    S += (int)__popcll(m);
+  }
+  const int padded = (knn + 3) & ~3;
+  for (int q = knn + lane; q < padded; q += kWave) s_fsel[q] = 0;
+  wave_lds_sync();
+  for (int q = lane; q < knn; q += kWave) {
+    const uint64_t mine = s_fsel[q];
+    s_fin[rank_in(s_fsel, padded, mine)] = mine;
+  }
+  wave_lds_sync();
+  float e[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int j = lane + r * kWave;
+    const uint64_t u = j < knn ? s_fin[j] : 0;
+    code[r] = (uint32_t)(u >> 32);
+    full[r] = 0xFFFFFFFFu - (uint32_t)u;
+    sc[r] = j < knn ? (F32 ? __uint_as_float(unorder32(code[r])) : bf16_bits_to_f32(unorder16(code[r]))) : 0.f;
+  }
+  // descending: lane 0's first result is the largest score
+  const float mxs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc[0]), 0));
+#pragma unroll
+  for (int r = 0; r < 2; ++r) e[r] = lane + r * kWave < knn ? expf(sc[r] - mxs) : 0.f;
+  const float sum = wave_sum_dpp(e[0] + e[1]);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) wt[r] = e[r] / sum;
+}
+
+// One workgroup (two wavefronts) per (token, head).  GEN: any knn <= kMaxKnnGen (pairs built at run time, two
+// results per lane, the half top-k from the row in memory when knn > 64); otherwise a power-of-two knn <= kMaxKnn.
+template <bool F32, int CPL, bool GEN>
 __global__ void __launch_bounds__(128) select_kernel(const void *__restrict__ s1, const void *__restrict__ s2,
                                                      int NK, int knn, void *__restrict__ scores,
                                                      int64_t *__restrict__ idx, float *__restrict__ w) {
   using Key = typename SelKey<F32>::T;
+  constexpr int MAXK = GEN ? kMaxKnnGen : kMaxKnn;
   __shared__ __align__(16) Key s_cand[2][kCap];
-  __shared__ __align__(16) Key s_sel[2][kMaxKnn];
-  __shared__ __align__(16) Key s_top[2][kMaxKnn];
-  __shared__ __align__(16) uint64_t s_fsel[kMaxKnn];
-  __shared__ __align__(16) uint64_t s_fin[kMaxKnn];
+  __shared__ __align__(16) Key s_sel[2][MAXK];
+  __shared__ __align__(16) Key s_top[2][MAXK];
+  __shared__ __align__(16) uint64_t s_fsel[MAXK];
+  __shared__ __align__(16) uint64_t s_fin[MAXK];
 
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
   const int64_t row = blockIdx.x;  // n * H + h
   const size_t esz = F32 ? 4 : 2;
   const void *src = (const char *)(wave == 0 ? s1 : s2) + row * (int64_t)NK * esz;
-  uint32_t pc[kMaxPairSlots];
-  load_pairs(knn, pc);
-  if constexpr (CPL > 0) half_topk_reg<F32, CPL, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
-  else half_topk_stream<F32, kCap>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
-  __syncthreads();
+  if constexpr (!GEN) {
+    uint32_t pc[kMaxPairSlots];
+    load_pairs(knn, pc);
+    if constexpr (CPL > 0) half_topk_reg<F32, CPL, kCap, MAXK>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+    else half_topk_stream<F32, kCap, MAXK>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+    __syncthreads();
 
-  float sc, wt;
-  uint32_t full, code;
-  if (!cartesian_topk<F32>(s_top[0], s_top[1], NK, knn, pc, wave, s_fin, s_fsel, s_fin, sc, full, code, wt)) return;
-  if (lane < knn) {
-    const int64_t o = row * knn + lane;
-    if constexpr (F32) ((float *)scores)[o] = sc;
-    else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
-    idx[o] = (int64_t)full;
-    w[o] = wt;
+    float sc, wt;
+    uint32_t full, code;
+    if (!cartesian_topk<F32>(s_top[0], s_top[1], NK, knn, pc, wave, s_fin, s_fsel, s_fin, sc, full, code, wt))
+      return;
+    if (lane < knn) {
+      const int64_t o = row * knn + lane;
+      if constexpr (F32) ((float *)scores)[o] = sc;
+      else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
+      idx[o] = (int64_t)full;
+      w[o] = wt;
+    }
+  } else {
+    if constexpr (CPL > 0) {
+      if (knn <= kWave) half_topk_reg<F32, CPL, kCap, MAXK>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+      else half_topk_stream<F32, kCap, MAXK>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+    } else {
+      half_topk_stream<F32, kCap, MAXK>(src, NK, knn, s_cand[wave], s_sel[wave], s_top[wave]);
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    uint32_t pc[kGenPairSlots];
+    gen_pairs(knn, (int *)s_cand[0], pc);
+    float sc[2], wt[2];
+    uint32_t full[2], code[2];
+    cartesian_general<F32>(s_top[0], s_top[1], NK, knn, pc, s_fsel, s_fin, sc, full, code, wt);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int j = lane + r * kWave;
+      if (j < knn) {
+        const int64_t o = row * knn + j;
+        if constexpr (F32) ((float *)scores)[o] = sc[r];
+        else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code[r]);
+        idx[o] = (int64_t)full[r];
+        w[o] = wt[r];
+      }
+    }
   }
 }
 
@@ -601,13 +765,16 @@ void launch_select(const void *s1, const void *s2, int64_t rows, int NK, int knn
   const bool aligned = (((uintptr_t)s1 | (uintptr_t)s2) % 16) == 0 && NK % epc == 0;
   const int chunks = NK / epc;
   const dim3 grid((unsigned)rows), block(2 * kWave);
-#define SMLM_SELECT(CPL) \
-  hipLaunchKernelGGL((select_kernel<F32, CPL>), grid, block, 0, stream, s1, s2, NK, knn, scores, idx, w)
-  if (!aligned || chunks > 8 * kWave) SMLM_SELECT(0);
-  else if (chunks <= kWave) SMLM_SELECT(1);
-  else if (chunks <= 2 * kWave) SMLM_SELECT(2);
-  else if (chunks <= 4 * kWave) SMLM_SELECT(4);
-  else SMLM_SELECT(8);
+#define SMLM_SELECT(CPL, GEN) \
+  hipLaunchKernelGGL((select_kernel<F32, CPL, GEN>), grid, block, 0, stream, s1, s2, NK, knn, scores, idx, w)
+  if (!is_pow2(knn) || knn > kMaxKnn) {  // the general path: register rows up to 8 chunks per lane
+    if (!aligned || chunks > 8 * kWave || knn > kWave) SMLM_SELECT(0, true);
+    else SMLM_SELECT(8, true);
+  } else if (!aligned || chunks > 8 * kWave) SMLM_SELECT(0, false);
+  else if (chunks <= kWave) SMLM_SELECT(1, false);
+  else if (chunks <= 2 * kWave) SMLM_SELECT(2, false);
+  else if (chunks <= 4 * kWave) SMLM_SELECT(4, false);
+  else SMLM_SELECT(8, false);
 #undef SMLM_SELECT
 }
 
@@ -622,7 +789,7 @@ constexpr int kFusedCapBytes = 4096;   // LDS candidate + staging bytes per half
 
 constexpr int kFusedMaxHeads = 4;       // 2H wavefronts per workgroup
 
-template <bool F32, int CPL, int TK>
+template <bool F32, int CPL, int TK, bool GEN>
 __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
     select_bag_kernel(const void *__restrict__ s1, const void *__restrict__ s2, int H, int NK, int knn,
                       const uint8_t *__restrict__ table, int64_t rows, int D, int row_bytes, int cpr,
@@ -632,14 +799,15 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   using Key = typename SelKey<F32>::T;
   constexpr int CAP = kFusedCapBytes / (int)sizeof(Key);
   constexpr int VPC = bag::vals_per_chunk<TK>();
+  constexpr int MAXK = GEN ? kMaxKnnGen : kMaxKnn;
   extern __shared__ __align__(16) unsigned char smem[];
   const int nw = 2 * H;
   Key *s_cand = (Key *)smem;                            // [nw][CAP]; then float [rpr][D] partial sums
-  Key *s_sel = (Key *)(smem + union_bytes);             // [nw][kMaxKnn]
-  Key *s_top = s_sel + nw * kMaxKnn;                    // [nw][kMaxKnn]
-  uint64_t *s_fsel = (uint64_t *)(s_top + nw * kMaxKnn);  // [H][kMaxKnn]
-  uint64_t *s_fin = s_fsel + H * kMaxKnn;               // [H][kMaxKnn]
-  int64_t *s_off = (int64_t *)(s_fin + H * kMaxKnn);    // [H * knn]
+  Key *s_sel = (Key *)(smem + union_bytes);             // [nw][MAXK]
+  Key *s_top = s_sel + nw * MAXK;                       // [nw][MAXK]
+  uint64_t *s_fsel = (uint64_t *)(s_top + nw * MAXK);   // [H][MAXK]
+  uint64_t *s_fin = s_fsel + H * MAXK;                  // [H][MAXK]
+  int64_t *s_off = (int64_t *)(s_fin + H * MAXK);       // [H * knn]
   float *s_w = (float *)(s_off + H * knn);              // [H * knn]
   __shared__ int s_bad;
 
@@ -653,35 +821,60 @@ __global__ void __launch_bounds__(2 * kFusedMaxHeads * kWave)
   // memory round trip after the gather
   const uint16_t pre_first = pre && tid < D ? pre[n * D + tid] : (uint16_t)0;
   const void *src = (const char *)(p ? s2 : s1) + row * (int64_t)NK * esz;
-  Key *sel = s_sel + wave * kMaxKnn, *top = s_top + wave * kMaxKnn;
-  uint32_t pc[kMaxPairSlots];
-  load_pairs(knn, pc);
-  if constexpr (CPL > 0) half_topk_reg<F32, CPL, CAP>(src, NK, knn, s_cand + wave * CAP, sel, top);
-  else half_topk_stream<F32, CAP>(src, NK, knn, s_cand + wave * CAP, sel, top);
-  __syncthreads();
+  Key *sel = s_sel + wave * MAXK, *top = s_top + wave * MAXK;
 
-  float sc, wt;
-  uint32_t full, code;
-  if (cartesian_topk<F32>(s_top + 2 * h * kMaxKnn, s_top + (2 * h + 1) * kMaxKnn, NK, knn, pc, p,
-                          s_fin + h * kMaxKnn, s_fsel + h * kMaxKnn, s_fin + h * kMaxKnn, sc, full, code, wt)) {
-    if (lane < knn) {
-      const int64_t o = row * knn + lane;
-      if (scores) {
-        if constexpr (F32) ((float *)scores)[o] = sc;
-        else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
-      }
-      if (idx) idx[o] = (int64_t)full;
-      if (w) w[o] = wt;
-      int64_t r = full;
-      float ww = wt;
-      if (r >= rows) {  // a table with fewer than NK^2 rows: the token's output is NaN, as in the bag
-        s_bad = 1;
-        r = 0;
-        ww = 0.f;
-      }
-      if constexpr (TK == bag::kI8 || TK == bag::kQ4) ww *= f16_bits_to_f32(scales[r]);
-      s_off[h * knn + lane] = r * row_bytes;
-      s_w[h * knn + lane] = ww;
+  // result j of head h (wavefront (h, 0)): outputs, and the lookup staged for the gather
+  auto emit = [&](int j, float sc, uint32_t full, uint32_t code, float wt) {
+    const int64_t o = row * knn + j;
+    if (scores) {
+      if constexpr (F32) ((float *)scores)[o] = sc;
+      else ((uint16_t *)scores)[o] = (uint16_t)unorder16(code);
+    }
+    if (idx) idx[o] = (int64_t)full;
+    if (w) w[o] = wt;
+    int64_t r = full;
+    float ww = wt;
+    if (r >= rows) {  // a table with fewer than NK^2 rows: the token's output is NaN, as in the bag
+      s_bad = 1;
+      r = 0;
+      ww = 0.f;
+    }
+    if constexpr (TK == bag::kI8 || TK == bag::kQ4) ww *= f16_bits_to_f32(scales[r]);
+    s_off[h * knn + j] = r * row_bytes;
+    s_w[h * knn + j] = ww;
+  };
+
+  if constexpr (!GEN) {
+    uint32_t pc[kMaxPairSlots];
+    load_pairs(knn, pc);
+    if constexpr (CPL > 0) half_topk_reg<F32, CPL, CAP, MAXK>(src, NK, knn, s_cand + wave * CAP, sel, top);
+    else half_topk_stream<F32, CAP, MAXK>(src, NK, knn, s_cand + wave * CAP, sel, top);
+    __syncthreads();
+
+    float sc, wt;
+    uint32_t full, code;
+    if (cartesian_topk<F32>(s_top + 2 * h * MAXK, s_top + (2 * h + 1) * MAXK, NK, knn, pc, p, s_fin + h * MAXK,
+                            s_fsel + h * MAXK, s_fin + h * MAXK, sc, full, code, wt)) {
+      if (lane < knn) emit(lane, sc, full, code, wt);
+    }
+  } else {
+    if constexpr (CPL > 0) {
+      if (knn <= kWave) half_topk_reg<F32, CPL, CAP, MAXK>(src, NK, knn, s_cand + wave * CAP, sel, top);
+      else half_topk_stream<F32, CAP, MAXK>(src, NK, knn, s_cand + wave * CAP, sel, top);
+    } else {
+      half_topk_stream<F32, CAP, MAXK>(src, NK, knn, s_cand + wave * CAP, sel, top);
+    }
+    __syncthreads();
+    if (p == 0) {
+      uint32_t pc[kGenPairSlots];
+      gen_pairs(knn, (int *)(s_cand + wave * CAP), pc);
+      float sc[2], wt[2];
+      uint32_t full[2], code[2];
+      cartesian_general<F32>(s_top + 2 * h * MAXK, s_top + (2 * h + 1) * MAXK, NK, knn, pc, s_fsel + h * MAXK,
+                             s_fin + h * MAXK, sc, full, code, wt);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (lane + r * kWave < knn) emit(lane + r * kWave, sc[r], full[r], code[r], wt[r]);
     }
   }
   __syncthreads();
@@ -714,27 +907,32 @@ void launch_select_bag(const void *s1, const void *s2, int64_t N, int H, int NK,
                        int64_t rows, int D, const uint16_t *scales, const uint16_t *pre, void *out, int out_bf16,
                        void *scores, int64_t *idx, float *w, hipStream_t stream) {
   using Key = typename SelKey<F32>::T;
+  const bool gen = !is_pow2(knn) || knn > kMaxKnn;
+  const int maxk = gen ? kMaxKnnGen : kMaxKnn;
   const int row_bytes = TK == bag::kF32 ? 4 * D : TK == bag::kBF16 ? 2 * D : TK == bag::kI8 ? D : D / 2;
   const int cpr = row_bytes / 16;
   const int nthr = 2 * H * kWave;
   const int rpr = bag::bag_slots(cpr);
   const size_t cand = (size_t)2 * H * kFusedCapBytes, red = (size_t)rpr * D * sizeof(float);
   const size_t union_bytes = (cand > red ? cand : red + 15) / 16 * 16;
-  const size_t shmem = union_bytes + (size_t)2 * 2 * H * kMaxKnn * sizeof(Key) + (size_t)2 * H * kMaxKnn * 8 +
+  const size_t shmem = union_bytes + (size_t)2 * 2 * H * maxk * sizeof(Key) + (size_t)2 * H * maxk * 8 +
                        (size_t)H * knn * (8 + 4);
   const int epc = F32 ? 4 : 8;
   const bool aligned = (((uintptr_t)s1 | (uintptr_t)s2) % 16) == 0 && NK % epc == 0;
   const int chunks = NK / epc;
   const dim3 grid((unsigned)N), block(nthr);
-#define SMLM_SELECT_BAG(CPL)                                                                                     \
-  hipLaunchKernelGGL((select_bag_kernel<F32, CPL, TK>), grid, block, shmem, stream, s1, s2, H, NK, knn,          \
+#define SMLM_SELECT_BAG(CPL, GEN)                                                                                \
+  hipLaunchKernelGGL((select_bag_kernel<F32, CPL, TK, GEN>), grid, block, shmem, stream, s1, s2, H, NK, knn,     \
                      (const uint8_t *)table, rows, D, row_bytes, cpr, scales, pre, out, out_bf16, union_bytes, \
                      scores, idx, w)
-  if (!aligned || chunks > 8 * kWave) SMLM_SELECT_BAG(0);
-  else if (chunks <= kWave) SMLM_SELECT_BAG(1);
-  else if (chunks <= 2 * kWave) SMLM_SELECT_BAG(2);
-  else if (chunks <= 4 * kWave) SMLM_SELECT_BAG(4);
-  else SMLM_SELECT_BAG(8);
+  if (gen) {
+    if (!aligned || chunks > 8 * kWave || knn > kWave) SMLM_SELECT_BAG(0, true);
+    else SMLM_SELECT_BAG(8, true);
+  } else if (!aligned || chunks > 8 * kWave) SMLM_SELECT_BAG(0, false);
+  else if (chunks <= kWave) SMLM_SELECT_BAG(1, false);
+  else if (chunks <= 2 * kWave) SMLM_SELECT_BAG(2, false);
+  else if (chunks <= 4 * kWave) SMLM_SELECT_BAG(4, false);
+  else SMLM_SELECT_BAG(8, false);
 #undef SMLM_SELECT_BAG
 }
 
@@ -762,10 +960,10 @@ extern "C" int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_
     return fail(SMLM_EINVAL, "smlm_pkm_select: dtype must be SMLM_BF16 or SMLM_F32, got %d", dtype);
   if (N < 0 || H < 1 || N * (int64_t)H > 0x7FFFFFFFLL)
     return fail(SMLM_EINVAL, "smlm_pkm_select: N=%lld, H=%d out of range", (long long)N, H);
-  if (!is_pow2(knn) || knn > kMaxKnn)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select: knn=%d must be a power of two <= %d", knn, kMaxKnn);
-  if (!is_pow2(NK) || NK > 65536 || NK < knn)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select: NK=%d must be a power of two in [knn, 65536]", NK);
+  if (knn < 1 || knn > kMaxKnnGen)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select: knn=%d must be in [1, %d]", knn, kMaxKnnGen);
+  if (NK < knn || NK > 65536)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select: NK=%d must be in [knn, 65536]", NK);
   if (N == 0) return SMLM_OK;
   if (dtype == SMLM_F32) launch_select<true>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
   else launch_select<false>(s1, s2, N * H, NK, knn, scores, idx, w, (hipStream_t)stream);
@@ -784,10 +982,10 @@ extern "C" int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, in
   if (N < 0 || N > 0x7FFFFFFFLL || H < 1 || H > kFusedMaxHeads)
     return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: N=%lld, H=%d (1 <= H <= %d)", (long long)N, H,
                 kFusedMaxHeads);
-  if (!is_pow2(knn) || knn > kMaxKnn)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: knn=%d must be a power of two <= %d", knn, kMaxKnn);
-  if (!is_pow2(NK) || NK > 65536 || NK < knn)
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: NK=%d must be a power of two in [knn, 65536]", NK);
+  if (knn < 1 || knn > kMaxKnnGen)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: knn=%d must be in [1, %d]", knn, kMaxKnnGen);
+  if (NK < knn || NK > 65536)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_bag: NK=%d must be in [knn, 65536]", NK);
   if (table_dtype != SMLM_F32 && table_dtype != SMLM_BF16 && table_dtype != SMLM_I8 && table_dtype != SMLM_Q4)
     return fail(SMLM_EINVAL, "smlm_pkm_select_bag: table_dtype %d is not a table format", table_dtype);
   if ((table_dtype == SMLM_I8 || table_dtype == SMLM_Q4) != (scales != nullptr))

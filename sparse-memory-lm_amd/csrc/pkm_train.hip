@@ -55,63 +55,106 @@ __global__ void __launch_bounds__(kTrainThreads)
   const int lane = lane_id();
   const int64_t row = (int64_t)blockIdx.x * kTrainWaves + threadIdx.x / kWave;  // (n, h)
   if (row >= rows) return;                                                       // wavefront-uniform
-  const bool have = lane < knn;
-  const int64_t o = row * knn + (have ? lane : 0);
-  const int64_t ix = have ? idx[o] : 0;
-  const float wk = have ? w[o] : 0.f;
-  float dl = 0.f;
+  // selected entry j = lane + 64 r (r < 2: knn <= 128)
+  bool have[2];
+  int64_t ix[2];
+  float wk[2], dl[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int j = lane + r * kWave;
+    have[r] = j < knn;
+    const int64_t o = row * knn + (have[r] ? j : 0);
+    ix[r] = have[r] ? idx[o] : 0;
+    wk[r] = have[r] ? w[o] : 0.f;
+    dl[r] = 0.f;
+  }
   if (g_w) {
-    const float gw = have ? g_w[o] : 0.f;
-    const float s = wave_sum_f32(wk * gw);
-    dl = wk * (gw - s);
+    float gw[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) gw[r] = have[r] ? g_w[row * knn + lane + r * kWave] : 0.f;
+    const float s = wave_sum_f32(wk[0] * gw[0] + wk[1] * gw[1]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) dl[r] = wk[r] * (gw[r] - s);
   }
   if (g_scores) {
-    const float gs = !have ? 0.f
-                     : F32 ? ((const float *)g_scores)[o]
-                           : bf16_bits_to_f32(((const uint16_t *)g_scores)[o]);
-    dl = dl + gs;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int64_t o = row * knn + lane + r * kWave;
+      const float gs = !have[r] ? 0.f
+                       : F32 ? ((const float *)g_scores)[o]
+                             : bf16_bits_to_f32(((const uint16_t *)g_scores)[o]);
+      dl[r] = dl[r] + gs;
+    }
   }
-  const float ds = to_dtype<F32>(dl);
-  const int i1 = (int)(ix / NK), i2 = (int)(ix % NK);
+  float ds[2];
+  int i1[2], i2[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    ds[r] = to_dtype<F32>(dl[r]);
+    i1[r] = (int)(ix[r] / NK);
+    i2[r] = (int)(ix[r] % NK);
+  }
 
-  // 1. both dense rows as zeros, 16 bytes per store
+  // 1. both dense rows as zeros: 16 bytes per store where rows are whole 16-byte chunks, else element by element
   constexpr int EPV = F32 ? 4 : 8;            // elements per 16 bytes
-  const int chunks = NK / EPV;
   char *r1 = (char *)ds1 + row * (int64_t)NK * (F32 ? 4 : 2);
   char *r2 = (char *)ds2 + row * (int64_t)NK * (F32 ? 4 : 2);
-  typedef unsigned u32x4z __attribute__((ext_vector_type(4)));
-  for (int c = lane; c < chunks; c += kWave) {  // streamed to memory (non-temporal): 2 x NK per row, written once
-    __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r1 + (int64_t)c * 16));
-    __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r2 + (int64_t)c * 16));
+  if (NK % EPV == 0) {
+    typedef unsigned u32x4z __attribute__((ext_vector_type(4)));
+    const int chunks = NK / EPV;
+    for (int c = lane; c < chunks; c += kWave) {  // streamed to memory (non-temporal): 2 x NK per row, written once
+      __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r1 + (int64_t)c * 16));
+      __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r2 + (int64_t)c * 16));
+    }
+  } else {
+    for (int k = lane; k < NK; k += kWave) {
+      if constexpr (F32) {
+        ((float *)r1)[k] = 0.f;
+        ((float *)r2)[k] = 0.f;
+      } else {
+        ((uint16_t *)r1)[k] = 0;
+        ((uint16_t *)r2)[k] = 0;
+      }
+    }
   }
   // every zero store acknowledged before the first value store: the value then lands after the zero
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_s_waitcnt(0);
 
   // 2. per sub-key: the sum of its selected pairs' gradients in selection order, by its first occurrence
-  float sum1 = 0.f, sum2 = 0.f;
-  bool first1 = have, first2 = have;
+  float sum1[2] = {0.f, 0.f}, sum2[2] = {0.f, 0.f};
+  bool first1[2] = {have[0], have[1]}, first2[2] = {have[0], have[1]};
   for (int j = 0; j < knn; ++j) {
-    const int j1 = __builtin_amdgcn_readlane(i1, j), j2 = __builtin_amdgcn_readlane(i2, j);
-    const float dj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ds), j));
-    if (j1 == i1) {
-      sum1 = sum1 + dj;
-      if (j < lane) first1 = false;
-    }
-    if (j2 == i2) {
-      sum2 = sum2 + dj;
-      if (j < lane) first2 = false;
+    const int rj = j / kWave, lj = j % kWave;  // wavefront-uniform
+    const int j1 = __builtin_amdgcn_readlane(rj ? i1[1] : i1[0], lj);
+    const int j2 = __builtin_amdgcn_readlane(rj ? i2[1] : i2[0], lj);
+    const float dj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rj ? ds[1] : ds[0]),
+                                                                         lj));
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int me = lane + r * kWave;
+      if (j1 == i1[r]) {
+        sum1[r] = sum1[r] + dj;
+        if (j < me) first1[r] = false;
+      }
+      if (j2 == i2[r]) {
+        sum2[r] = sum2[r] + dj;
+        if (j < me) first2[r] = false;
+      }
     }
   }
-  // an index outside [0, NK^2) (not a selection's output) writes nothing
-  first1 = first1 && (unsigned)i1 < (unsigned)NK && ix >= 0;
-  first2 = first2 && (unsigned)i2 < (unsigned)NK && ix >= 0;
-  if constexpr (F32) {
-    if (first1) ((float *)r1)[i1] = sum1;
-    if (first2) ((float *)r2)[i2] = sum2;
-  } else {
-    if (first1) ((uint16_t *)r1)[i1] = (uint16_t)bf16_bits_rtne(sum1);
-    if (first2) ((uint16_t *)r2)[i2] = (uint16_t)bf16_bits_rtne(sum2);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    // an index outside [0, NK^2) (not a selection's output) writes nothing
+    const bool w1 = first1[r] && (unsigned)i1[r] < (unsigned)NK && ix[r] >= 0;
+    const bool w2 = first2[r] && (unsigned)i2[r] < (unsigned)NK && ix[r] >= 0;
+    if constexpr (F32) {
+      if (w1) ((float *)r1)[i1[r]] = sum1[r];
+      if (w2) ((float *)r2)[i2[r]] = sum2[r];
+    } else {
+      if (w1) ((uint16_t *)r1)[i1[r]] = (uint16_t)bf16_bits_rtne(sum1[r]);
+      if (w2) ((uint16_t *)r2)[i2[r]] = (uint16_t)bf16_bits_rtne(sum2[r]);
+    }
   }
 }
 
@@ -551,9 +594,9 @@ extern "C" int smlm_pkm_select_backward(const int64_t *idx, const float *w, cons
   if (!idx || !w || !ds1 || !ds2) return fail(SMLM_EINVAL, "smlm_pkm_select_backward: null idx, w, ds1 or ds2");
   if (dtype != SMLM_BF16 && dtype != SMLM_F32)
     return fail(SMLM_EINVAL, "smlm_pkm_select_backward: dtype must be SMLM_BF16 or SMLM_F32, got %d", dtype);
-  if (N < 0 || H < 1 || knn < 1 || knn > kWave || !is_pow2(NK) || NK > 65536 || NK < (dtype == SMLM_F32 ? 4 : 8))
-    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_backward: N=%lld H=%d NK=%d knn=%d (NK a power of two in "
-                "[8, 65536], knn <= 64)", (long long)N, H, NK, knn);
+  if (N < 0 || H < 1 || knn < 1 || knn > 2 * kWave || NK < knn || NK > 65536)
+    return fail(SMLM_EUNSUPPORTED, "smlm_pkm_select_backward: N=%lld H=%d NK=%d knn=%d (knn in [1, 128], NK in "
+                "[knn, 65536])", (long long)N, H, NK, knn);
   if (!aligned(ds1, 16) || !aligned(ds2, 16))
     return fail(SMLM_EINVAL, "smlm_pkm_select_backward: ds1 and ds2 must be 16-byte aligned");
   const int64_t rows = N * H;

@@ -61,8 +61,8 @@ def _table_ptr(t, name):
                      + (" (pageable)" if t.device.type == "cpu" else ""))
 
 
-def _pow2(n):
-    return n > 0 and n & (n - 1) == 0
+MAX_N_KEYS = 65536    # sub-key indices fit the 16-bit index field of the selection keys
+MAX_KNN = 128         # the selection's result lists (csrc/pkm_select.hip: kMaxKnnGen)
 
 
 def pk_scores(q, keys):
@@ -98,9 +98,9 @@ def pk_select(s1, s2, knn, ch=128, num_warps=4):
         raise ValueError(f"pk_select: s1, s2 must be (N, H, n_keys) tensors of one dtype (bf16 or fp32), got "
                          f"{s1.dtype} {tuple(s1.shape)} and {s2.dtype} {tuple(s2.shape)}")
     N, H, NK = s1.shape
-    if not (_pow2(NK) and NK <= 65536 and _pow2(knn) and knn <= 64 and knn <= NK):
-        raise ValueError(f"pk_select needs n_keys and knn to be powers of two, knn <= min(n_keys, 64) and "
-                         f"n_keys <= 65536, got n_keys={NK}, knn={knn}")
+    if not (1 <= knn <= min(NK, MAX_KNN) and NK <= MAX_N_KEYS):
+        raise ValueError(f"pk_select needs 1 <= knn <= min(n_keys, {MAX_KNN}) and n_keys <= {MAX_N_KEYS}, got "
+                         f"n_keys={NK}, knn={knn}")
     s1, s2 = s1.contiguous(), s2.contiguous()
     scores = torch.empty(N, H, knn, dtype=s1.dtype, device=s1.device)
     idx = torch.empty(N, H, knn, dtype=torch.int64, device=s1.device)
@@ -186,9 +186,9 @@ def pk_select_bag(s1, s2, knn, table, scales=None, pre=None, out_bf16=False, rec
         raise ValueError(f"pk_select_bag: s1, s2 must be (N, H, n_keys) tensors of one dtype (bf16 or fp32), got "
                          f"{s1.dtype} {tuple(s1.shape)} and {s2.dtype} {tuple(s2.shape)}")
     N, H, NK = s1.shape
-    if not (_pow2(NK) and NK <= 65536 and _pow2(knn) and knn <= 64 and knn <= NK) or H > 4:
-        raise ValueError(f"pk_select_bag needs n_keys and knn to be powers of two, knn <= min(n_keys, 64), "
-                         f"n_keys <= 65536 and at most 4 heads, got n_keys={NK}, knn={knn}, heads={H}")
+    if not (1 <= knn <= min(NK, MAX_KNN) and NK <= MAX_N_KEYS) or H > 4:
+        raise ValueError(f"pk_select_bag needs 1 <= knn <= min(n_keys, {MAX_KNN}), n_keys <= {MAX_N_KEYS} and "
+                         f"at most 4 heads, got n_keys={NK}, knn={knn}, heads={H}")
     kind, D = _table_kind(table, scales, "pk_select_bag")
     if pre is not None and (pre.dtype != torch.bfloat16 or tuple(pre.shape) != (N, D)):
         raise ValueError(f"pk_select_bag: pre must be a bf16 (N, D) = ({N}, {D}) tensor")

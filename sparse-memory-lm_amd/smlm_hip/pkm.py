@@ -7,6 +7,8 @@ graph switch), whose lookup runs on the gfx950 kernels of smlm_hip.kernels:
 
 impl: "hip", or the reference's names "torch" and "triton" (smlm/pkm.py:48), which a reference config carries;
 every name runs the same kernels (there is one implementation here) and is kept in self.impl for the config.
+Shapes: any n_keys <= 65536 and knn <= min(n_keys, 128) (the reference's torch path takes any); "triton" keeps
+the reference's power-of-two rule for it.
 
 A forward that autograd records (training) takes the reference's differentiable path with the HIP kernels where the
 reference uses its Triton ones (smlm/pkm.py:186-228): torch query projection and BatchNorm, sub-key scores by
@@ -65,10 +67,14 @@ class ProductKeyMemory(nn.Module):
         if k_dim % 2 or knn > n_keys:
             raise ValueError(f"k_dim must be even and knn <= n_keys, got k_dim={k_dim}, knn={knn}, n_keys={n_keys}")
         check_impl(impl, "ProductKeyMemory")
-        if not (_pow2(n_keys) and n_keys <= 65536 and _pow2(knn) and knn <= 64):
-            # the selection kernel packs sub-key indices into 16 bits and keeps one selected entry per lane
-            raise ValueError(f"the HIP kernels need n_keys and knn to be powers of two, n_keys <= 65536 and "
-                             f"knn <= 64, got n_keys={n_keys}, knn={knn} (mem_impl={impl!r}).")
+        if impl == "triton" and not (_pow2(n_keys) and n_keys <= 65536 and _pow2(knn)):
+            # the reference's rule for its Triton kernels (smlm/pkm.py:49-53), kept for configs that name them
+            raise ValueError(f"mem_impl='triton' needs n_keys and knn to be powers of two and n_keys <= 65536, "
+                             f"got n_keys={n_keys}, knn={knn}. Use mem_impl='torch' for other sizes.")
+        if n_keys > kernels.MAX_N_KEYS or knn > kernels.MAX_KNN:
+            # the selection keys hold sub-key indices in 16 bits; the result lists hold up to 128 entries
+            raise ValueError(f"the HIP kernels take n_keys <= {kernels.MAX_N_KEYS} and knn <= {kernels.MAX_KNN}, "
+                             f"got n_keys={n_keys}, knn={knn} (mem_impl={impl!r}).")
         if value_grad not in ("dense", "row_sparse"):
             raise ValueError(value_grad)
         self.d_in, self.d_out = d_in, d_out

@@ -50,9 +50,9 @@ def test_argument_checks_return_status_codes():
     assert "scales" in _lib.last_error()
     assert lib.smlm_pkm_bag(fake, _lib.I64, fake, 1, 1, fake, _lib.Q4, 1, 5, fake, None, fake, _lib.F32,
                             None) == _lib.EINVAL                                 # odd D for q4
-    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 1024, 48, fake, fake, fake, None) == _lib.EUNSUPPORTED
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 1024, 129, fake, fake, fake, None) == _lib.EUNSUPPORTED
     assert "knn" in _lib.last_error()
-    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 1000, 32, fake, fake, fake, None) == _lib.EUNSUPPORTED
+    assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 20, 32, fake, fake, fake, None) == _lib.EUNSUPPORTED
     assert lib.smlm_pkm_select(fake, fake, _lib.BF16, 1, 4, 131072, 32, fake, fake, fake, None) == _lib.EUNSUPPORTED
     assert lib.smlm_pkm_select(fake, fake, _lib.I8, 1, 4, 1024, 32, fake, fake, fake, None) == _lib.EINVAL
     assert lib.smlm_pkm_score(fake, 512, fake, _lib.BF16, 1, 1, 64, 12, fake, fake, None) == _lib.EUNSUPPORTED
@@ -93,15 +93,22 @@ def test_status_becomes_python_exception():
                    "smlm_pkm_quantize")
 
 
-def test_rejects_unsupported_shapes():
-    """As the reference's Triton path: non-power-of-two n_keys or knn fail at construction with a clear
-    message (and, here, knn > 64, whatever impl name is given)."""
-    for n_keys, knn in ((24, 4), (16, 5), (256, 128)):
-        for impl in ("hip", "torch", "triton"):
-            with pytest.raises(ValueError, match="powers of two"):
-                ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16, impl=impl)
-    m = ProductKeyMemory(32, 32, n_keys=16, knn=4, k_dim=16)
-    assert m.keys.shape == (4, 2, 16, 8) and m.values.weight.shape == (256, 32)
+def test_shapes_of_the_reference_impls():
+    """As the reference (smlm/pkm.py:49-53, tests/test_pkm.py:130-136): impl="triton" refuses non-power-of-two
+    n_keys or knn at construction with a clear message, impl="torch" (and "hip") takes them; every impl is
+    bounded by the kernels' limits, n_keys <= 65536 and knn <= 128."""
+    for n_keys, knn in ((24, 4), (16, 5)):
+        with pytest.raises(ValueError, match="powers of two"):
+            ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16, impl="triton")
+        for impl in ("torch", "hip"):
+            m = ProductKeyMemory(32, 32, n_keys=n_keys, knn=knn, k_dim=16, impl=impl)
+            assert m.keys.shape == (4, 2, n_keys, 8) and m.values.weight.shape == (n_keys ** 2, 32)
+    for impl in ("hip", "torch", "triton"):
+        ProductKeyMemory(32, 32, n_keys=256, knn=128, k_dim=16, impl=impl)
+        with pytest.raises(ValueError, match="knn <= 128"):
+            ProductKeyMemory(32, 32, n_keys=512, knn=256, k_dim=16, impl=impl)
+    with pytest.raises(ValueError, match="k_dim must be even and knn <= n_keys"):
+        ProductKeyMemory(32, 32, n_keys=8, knn=9, k_dim=16)
 
 
 def test_impl_names_of_reference_configs():

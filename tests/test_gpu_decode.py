@@ -320,6 +320,10 @@ def _tables(kind, rows, D, seed):
     (3, 1, 512, 16, torch.bfloat16, "bf16", True, True),      # 2 thread slots run the 8 bf16 slots
     (4, 1, 256, 32, torch.bfloat16, "fp32", False, True),     # 1 thread slot runs the 4 fp32 slots
     (6, 1, 1024, 32, torch.bfloat16, "int8", True, False),    # 5 thread slots run the 8 int8 slots
+    (3, 4, 24, 4, torch.bfloat16, "bf16", True, True),        # n_keys not a power of two
+    (5, 4, 1000, 5, torch.bfloat16, "int8", True, True),      # knn not a power of two: pairs built at run time
+    (2, 4, 4096, 128, torch.bfloat16, "bf16", True, True),    # knn above 64: two results per lane
+    (4, 2, 256, 100, torch.float32, "bf16", False, False),
 ])
 def test_select_bag_bit_identical_to_select_then_bag(N, H, NK, knn, dtype, kind, with_pre, out_bf16):
     """pk_select_bag == pk_select followed by bag_infer, bit for bit (same selection, same bag additions in the

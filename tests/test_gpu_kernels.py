@@ -66,6 +66,49 @@ def test_pk_select_bf16_bit_exact(N, H, NK, knn):
     assert bool((srt[:, 1:] != srt[:, :-1]).all())
 
 
+# shapes the reference's torch path takes (smlm/pkm.py:48-53): n_keys not a power of two (the register path when
+# n_keys is a multiple of 8, else the row searched in memory; 24 and 1000 sub-keys, 3000 = 375 chunks, 4100 and
+# 65535), knn not a power of two (pairs built at run time, tests/test_pkm.py:18 uses knn 5) and knn above 64 (two
+# results per lane, the half top-k from the row in memory), knn = n_keys
+GENERAL_SHAPES = [(100, 3, 24, 4), (64, 4, 1000, 32), (9, 2, 3000, 32), (7, 2, 4100, 16), (3, 1, 65535, 32),
+                  (200, 3, 32, 5), (64, 4, 1024, 5), (40, 2, 1000, 12), (33, 3, 256, 48), (17, 2, 512, 100),
+                  (9, 4, 4096, 128), (13, 2, 128, 128), (5, 2, 24, 24), (20, 3, 96, 20), (50, 2, 8, 1),
+                  (6, 2, 4100, 77)]
+
+
+@pytest.mark.parametrize("N,H,NK,knn", GENERAL_SHAPES)
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_pk_select_general_shapes_bit_exact(N, H, NK, knn, dtype):
+    note(f"pk_select {dtype} general N={N} H={H} NK={NK} knn={knn}")
+    rng = np.random.default_rng(N * 7 + NK + knn)
+    f1 = rng.standard_normal((N, H, NK)).astype(np.float32)
+    f2 = rng.standard_normal((N, H, NK)).astype(np.float32)
+    if dtype == "bf16":
+        s1, s2 = O.bf16_bits_rtne(f1), O.bf16_bits_rtne(f2)
+        t1, t2 = bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV)
+    else:
+        s1, s2 = f1, f2
+        t1, t2 = torch.from_numpy(f1).to(DEV), torch.from_numpy(f2).to(DEV)
+    sc, idx, w = K.pk_select(t1, t2, knn)
+    torch.cuda.synchronize()
+    check_select(s1, s2, knn, sc, idx, w)
+    assert bool((idx >= 0).all()) and bool((idx < NK * NK).all())
+    assert abs(float(w.double().sum(-1).mean()) - 1.0) < 1e-5
+
+
+def test_pk_select_general_ties():
+    """The general path on tie-heavy rows (a handful of values, both signed zeros): knn 12 and 100."""
+    rng = np.random.default_rng(13)
+    vals = np.array([0x3F80, 0x3F00, 0x0000, 0x8000, 0xBF00, 0x3F40, 0x4000, 0xBF80], np.uint16)
+    for N, H, NK, knn in ((40, 3, 64, 12), (9, 2, 1000, 100)):
+        note(f"pk_select general ties N={N} NK={NK} knn={knn}")
+        s1 = vals[rng.integers(0, len(vals), (N, H, NK))]
+        s2 = vals[rng.integers(0, len(vals), (N, H, NK))]
+        sc, idx, w = K.pk_select(bf16_from_bits(s1).to(DEV), bf16_from_bits(s2).to(DEV), knn)
+        torch.cuda.synchronize()
+        check_select(s1, s2, knn, sc, idx, w)
+
+
 @pytest.mark.parametrize("N,H,NK,knn", [(512, 4, 1024, 32), (64, 4, 4096, 32), (40, 3, 64, 8), (9, 2, 16, 16)])
 def test_pk_select_bf16_ties(N, H, NK, knn):
     """Scores from a handful of values (both signed zeros): almost every comparison is a tie."""

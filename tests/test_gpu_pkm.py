@@ -284,3 +284,54 @@ def test_lm_logits_bf16_within_1e2():
     ref = TP.lm_forward(sd, cfg.to_dict(), x, selections={1: (mem.last_indices.cpu(), mem.last_weights.cpu())})
     err = (got - ref).abs().max() / ref.abs().max()
     assert float(err) < 1e-2, float(err)
+
+
+@pytest.mark.parametrize("n_keys,knn", [(16, 8), (16, 16), (32, 5), (8, 1), (24, 4), (16, 5), (128, 100)])
+@torch.no_grad()
+def test_product_key_topk_equals_bruteforce(n_keys, knn):
+    """tests/test_pkm.py:16-37 on the kernels, with the shapes the reference's torch path takes (non-power-of-two
+    n_keys and knn, knn above 64): the product-key search returns the top-k of a brute-force search over all
+    n_keys^2 full keys (fp64 on the host; the kernels score in fp32, so a row may differ at a near tie: 99% of the
+    rows must be identical sets), and every returned score belongs to its index."""
+    note(f"product-key search vs brute force n_keys={n_keys} knn={knn}")
+    torch.manual_seed(0)
+    mem = ProductKeyMemory(24, 24, n_keys=n_keys, heads=3, knn=knn, k_dim=16, impl="torch").to(DEV).eval()
+    q = torch.randn(200, 3, 16, generator=torch.Generator().manual_seed(1)).to(DEV)
+    scores, indices = mem.get_indices(q)
+    assert scores.shape == (200, 3, knn) and indices.shape == (200, 3, knn)
+    qd = q.double().cpu()
+    for h in range(3):
+        k1, k2 = mem.keys[h, 0].double().cpu(), mem.keys[h, 1].double().cpu()
+        full = torch.cat([k1.repeat_interleave(n_keys, 0), k2.repeat(n_keys, 1)], 1)
+        bf_scores, bf_idx = (qd[:, h] @ full.T).topk(knn, dim=-1)
+        got = scores[:, h].double().cpu()
+        torch.testing.assert_close(got, bf_scores, rtol=1e-5, atol=1e-5)
+        same = (indices[:, h].cpu().sort(-1).values == bf_idx.sort(-1).values).all(-1)
+        assert float(same.double().mean()) >= 0.99
+        recomputed = (qd[:, h].unsqueeze(1) * full[indices[:, h].cpu()]).sum(-1)
+        torch.testing.assert_close(got, recomputed, rtol=1e-5, atol=1e-5)
+
+
+@torch.no_grad()
+def test_generate_with_reference_torch_shapes():
+    """A bf16 LM whose memory layer has n_keys = 24 and knn = 5 (shapes only the reference's torch path takes):
+    the fused decode step selects bit-exactly against the oracle on its own sub-key scores, and the whole-step
+    graphs give the eager loop's tokens."""
+    cfg = ModelConfig(vocab_size=256, d_model=128, n_layers=2, n_heads=2, ffn_hidden=256, max_seq_len=64,
+                      mem_layers=[1], mem_n_keys=24, mem_heads=4, mem_knn=5, mem_k_dim=64, mem_impl="torch")
+    torch.manual_seed(4)
+    m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
+    m.set_memory_inference_table("bf16")
+    prompt = torch.randint(0, 256, (3, 7), generator=torch.Generator().manual_seed(2)).to(DEV)
+    note("generate n_keys=24 knn=5")
+    eager = m.generate(prompt, 20, use_graph=False)
+    graph = m.generate(prompt, 20, use_graph=True)
+    assert torch.equal(eager, graph)
+    dec = m._decoder(3, 28, DEV)
+    assert dec.fused is not None
+    rec = {}
+    dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec)
+    r = rec[1]
+    rs, ri, rw = O.pk_select(bits_of(r["s1"]), bits_of(r["s2"]), 5)
+    assert np.array_equal(r["indices"].cpu().numpy(), ri) and np.array_equal(bits_of(r["scores"]), rs)
+    np.testing.assert_allclose(r["weights"].cpu().numpy(), rw, rtol=0, atol=1e-6)
