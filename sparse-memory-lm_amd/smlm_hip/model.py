@@ -17,7 +17,7 @@ from torch import nn
 
 from . import kernels
 from .engram import EngramMemory, NgramHash
-from .pkm import ProductKeyMemory, inference_tables, state_tag
+from .pkm import ProductKeyMemory, inference_tables, state_tag, state_tensors
 
 
 @dataclass
@@ -296,6 +296,7 @@ class Transformer(nn.Module):
         self._decoders = {}
         self._fwd_graphs = {}
         self._fwd_graphs_tag = None
+        self._state = None              # state_tensors(self), kept for the graphs' state_tag
         self._init_weights()
 
     @torch.no_grad()
@@ -388,9 +389,10 @@ class Transformer(nn.Module):
         pass of ~60 launches).  The returned logits are the graph's static output, overwritten by the next call
         with the same shape; clone them to keep them.  A graph reads the tensors it was captured with, among them
         derived copies (cast sub-keys, the BatchNorm affine), so every graph is dropped and captured again when a
-        parameter or buffer has been replaced or written since (state_tag: an optimizer step, load_state_dict, new
-        BatchNorm statistics); set_memory_inference_table drops them too."""
-        tag = state_tag(self)
+        parameter or buffer has been written since (state_tag: an optimizer step, load_state_dict, new BatchNorm
+        statistics); set_memory_inference_table drops them too, and so must drop_graphs() after a parameter or
+        buffer is replaced by another object."""
+        tag = state_tag(self.state_tensors())
         if tag != self._fwd_graphs_tag:
             self._fwd_graphs.clear()
             self._fwd_graphs_tag = tag
@@ -416,10 +418,22 @@ class Transformer(nn.Module):
         graph.replay()
         return static_out
 
+    def state_tensors(self):
+        """The parameters and buffers, listed once (state_tensors) and kept until drop_graphs()."""
+        if self._state is None:
+            self._state = state_tensors(self)
+        return self._state
+
     def drop_graphs(self):
-        """Forget the captured forward graphs (and their memory)."""
+        """Forget the captured graphs (forward_graphed's, the decoders' and the memory layers') and the kept
+        parameter list: needed after a parameter or buffer is replaced by another object."""
         self._fwd_graphs.clear()
         self._fwd_graphs_tag = None
+        self._state = None
+        self._decoders.clear()
+        for m in self.memory_layers():
+            m._graph = None
+            m._graph_state = None
 
     def _ngram_rows(self, idx, kv_caches):
         """Engram rows of this chunk (smlm/model.py:270-279): the hash sees the last history tokens before the
@@ -490,6 +504,9 @@ class _FusedDecodeStep:
     0.155 -> 0.144 ms per step at batch 1).  Larger batches keep the wo launch: the summing prologue works on
     4-token groups, which re-read the weights per group, and with the wo launch on 8-token groups the fold loses
     from batch 20 up (139.4 -> 133.3 us per step at batch 16 folded, 147.3 -> 150.4 at 24, 150.1 -> 153.8 at 32).
+    Summing the heads in the attention launch itself (the last of a sequence's head workgroups adding the parts
+    after agent-scope release / acquire fences, no workgroup waiting) measured 176 -> 414 us per batch-64 step:
+    the fences' cache writebacks and invalidations cost ~40 us per launch.
 
     Derived weights (the concatenated query_proj | swilu_proj and its bias) are built at construction and rebuilt
     on an eager run after a parameter changed; a captured graph keeps what it was captured with."""
@@ -531,7 +548,7 @@ class _FusedDecodeStep:
         self._prepare()
 
     def _params_tag(self):
-        return tuple((p.data_ptr(), p._version) for p in self.model.parameters())
+        return state_tag(self.model.state_tensors())
 
     def _prepare(self):
         self.mem = {}
@@ -735,10 +752,10 @@ class _StepDecoder:
                     for _ in range(k):
                         self._step()
                 self.graph_runs[k] = run
-        self._graph_tag = state_tag(self.model)
+        self._graph_tag = state_tag(self.model.state_tensors())
 
     def _graphs_current(self):
-        return self.graph is not None and self._graph_tag == state_tag(self.model)
+        return self.graph is not None and self._graph_tag == state_tag(self.model.state_tensors())
 
     def replay(self, n):
         """n decode steps as graph replays: as many runs of the longest run length as fit, then of the next, then

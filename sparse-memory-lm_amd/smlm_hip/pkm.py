@@ -46,14 +46,19 @@ def inference_tables(values):
     return t
 
 
-def state_tag(module):
-    """(data_ptr, _version) of every parameter and buffer of `module`.  It changes whenever one of them is replaced
-    or written in place (an optimizer step, load_state_dict, new BatchNorm statistics), so a captured HIP graph,
-    which reads the tensors and the derived copies (cast sub-keys, BatchNorm affine) it was captured with, is
-    valid only while the tag it was captured under holds."""
-    out = [(t.data_ptr(), t._version) for t in module.parameters()]
-    out += [(t.data_ptr(), t._version) for t in module.buffers()]
-    return tuple(out)
+def state_tensors(module):
+    """The parameters and buffers of `module`, as a list to keep: walking the module tree costs ~0.3 ms of host time
+    per call on the configs' LM, checking a kept list ~20 us."""
+    return list(module.parameters()) + list(module.buffers())
+
+
+def state_tag(tensors):
+    """(data_ptr, _version) of every tensor of `tensors` (state_tensors).  It changes whenever one of them is
+    written in place or has its storage replaced (an optimizer step, load_state_dict, new BatchNorm statistics,
+    .to()), so a captured HIP graph, which reads the tensors and the derived copies (cast sub-keys, BatchNorm
+    affine) it was captured with, is valid only while the tag it was captured under holds.  A parameter or buffer
+    replaced by another object is not in a list kept from before: drop the graphs after such a change."""
+    return tuple((t.data_ptr(), t._version) for t in tensors)
 
 
 class ProductKeyMemory(nn.Module):
@@ -124,6 +129,7 @@ class ProductKeyMemory(nn.Module):
         self.last_lookup = None     # with record, also the no-grad lookup's input, query and sub-key scores
         self.decode_graph = False
         self._graph = None
+        self._graph_state = None    # state_tensors(self), kept for the graph's state_tag
         self._keys_cache = {}
         self._bn_cache = None
         self.reset_parameters()
@@ -192,10 +198,13 @@ class ProductKeyMemory(nn.Module):
     def _graph_forward(self, x):
         """Replay a HIP graph of _forward captured for this input shape (any token count): the same kernels as
         the eager path without the per-op launch cost.  Re-captured when the shape, dtype, autocast state or
-        inference table changes, or when a parameter or buffer was replaced or written (state_tag)."""
+        inference table changes, or when a parameter or buffer was written (state_tag); after replacing one by
+        another object, set self._graph = None."""
         ac = torch.is_autocast_enabled("cuda")
+        if self._graph_state is None:
+            self._graph_state = state_tensors(self)
         tag = (tuple(x.shape), x.dtype, ac, torch.get_autocast_dtype("cuda") if ac else None,
-               id(getattr(self.values, "infer_table", None)), state_tag(self))
+               id(getattr(self.values, "infer_table", None)), state_tag(self._graph_state))
         if self._graph is None or self._graph[0] != tag:
             static_x = x.clone()
             ctx = (torch.autocast("cuda", dtype=tag[3], cache_enabled=False) if ac
