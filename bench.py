@@ -852,12 +852,12 @@ def gather_sources_sha256():
     return h.hexdigest()
 
 
-def read_traffic():
+def read_traffic(path=None):
     """HBM bytes per launch of the config-4 gather (uniform control, Zipf) from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy kernel).  The summary names the sha256 of the
     gather's sources it was measured on; when that is absent or differs from the sources here, the counters
     belong to other code and the traffic is None (with "stale": True)."""
-    path = os.path.join(REPO, "profiles", "gather_config4_pmc.txt")
+    path = path or os.path.join(REPO, "profiles", "gather_config4_pmc.txt")
     out = {"uniform": None, "zipf": None, "stale": True}
     if not os.path.exists(path):
         return out

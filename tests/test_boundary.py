@@ -269,3 +269,19 @@ def test_bench_decode_roofline_accounting():
     assert abs(r["hbm_floor_ms"] - r["hbm_bytes_per_step"] / 8e12 * 1e3) < 1e-12
     assert _FusedDecodeStep.proj_max_batch >= 1
     assert bench.decode_roofline(m, 1, 0.15, 100.0, 1.5, 1.8)["launches_per_step"] == 4 * 5 + 6 + 1   # wo folded
+
+
+def test_bench_reads_counter_traffic_only_for_the_measured_sources(tmp_path):
+    """bench.py takes the gather's HBM traffic from the committed rocprofv3 summary only while the summary names the
+    sha256 of the gather sources it runs with; another hash, or none, leaves the traffic unmeasured."""
+    import bench
+    good = bench.read_traffic()
+    assert not good["stale"] and good["uniform"] > 3.4e9 and good["zipf"] > 1e9
+    text = open(os.path.join(os.path.dirname(HEADER), "..", "profiles", "gather_config4_pmc.txt")).read()
+    stale = tmp_path / "stale.txt"
+    stale.write_text(text.replace(bench.gather_sources_sha256(), "0" * 64))
+    r = bench.read_traffic(str(stale))
+    assert r["stale"] and r["uniform"] is None and r["zipf"] is None
+    none = tmp_path / "none.txt"
+    none.write_text("\n".join(line for line in text.splitlines() if not line.startswith("gather_sources_sha256")))
+    assert bench.read_traffic(str(none))["stale"]
