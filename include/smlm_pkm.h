@@ -76,7 +76,7 @@ int smlm_pkm_score(const void *q, int64_t q_row_stride, const void *keys, int dt
  *   scores  (N, H, knn) of `dtype`, descending
  *   idx     (N, H, knn) int64 table rows in [0, NK^2)
  *   w       (N, H, knn) fp32 softmax weights
- * NK a power of two in [knn, 65536]; knn a power of two in [1, 64].
+ * NK in [knn, 65536]; knn in [1, 128] (the shapes the reference's torch path takes, smlm/pkm.py:48-53).
  */
 int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_t N, int H, int NK, int knn, void *scores,
                     int64_t *idx, float *w, void *stream);
@@ -87,8 +87,8 @@ int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_t N, int H,
  * Replaces pk_select + bag_infer of smlm/pkm.py:197-223 (kernels.py:214-226, 364-378).
  *   s1, s2 (N, H, NK) of dtype; table / table_dtype / rows / D / scales / pre / out / out_dtype as smlm_pkm_bag;
  *   scores, idx, w: optional (NULL = not written) copies of the selection, as smlm_pkm_select writes them.
- * H <= 4; a table row must be whole 16-byte chunks, c of them, and the bag's row-slot layout for c
- * (lcm(c, 64) threads, at least 128; c * floor(256 / c) if lcm(c, 64) > 256) must fit in the 2*H*64 threads.
+ * H <= 4; NK and knn as smlm_pkm_select; a table row must be whole 16-byte chunks, at most 2*H*64 of them (the
+ * bag's additions follow the row-slot layout of smlm_pkm_bag whatever the workgroup's thread count).
  */
 int smlm_pkm_select_bag(const void *s1, const void *s2, int dtype, int64_t N, int H, int NK, int knn,
                         const void *table, int table_dtype, int64_t rows, int D, const uint16_t *scales,

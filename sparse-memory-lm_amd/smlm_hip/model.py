@@ -506,7 +506,11 @@ class _FusedDecodeStep:
     from batch 20 up (139.4 -> 133.3 us per step at batch 16 folded, 147.3 -> 150.4 at 24, 150.1 -> 153.8 at 32).
     Summing the heads in the attention launch itself (the last of a sequence's head workgroups adding the parts
     after agent-scope release / acquire fences, no workgroup waiting) measured 176 -> 414 us per batch-64 step:
-    the fences' cache writebacks and invalidations cost ~40 us per launch.
+    the fences' cache writebacks and invalidations cost ~40 us per launch.  Running value_proj in the selection + bag launch the same way
+    (one workgroup per token and 64-column slice of the bag output, each with the token's whole selection, the next
+    block's first launch summing the slices) measured no gain at batch 1: that launch went from 10.7-11.1 to 13.6
+    us (value_proj rows loaded at its start) or 14.3 us (loaded after the half top-ks), against the 4.1-4.4 us
+    value_proj launch it saves and 0.9 us more in the summing prologue (123.2-123.7 -> 123.8-124.3 us per step).
 
     Derived weights (the concatenated query_proj | swilu_proj and its bias) are built at construction and rebuilt
     on an eager run after a parameter changed; a captured graph keeps what it was captured with."""
@@ -605,14 +609,13 @@ class _FusedDecodeStep:
                                                     affine=affine, n_split=nq)
                 s1, s2 = kernels.pk_scores(q.view(B, m.heads, m.k_dim), m._keys_as(torch.bfloat16))
                 table, scales = inference_tables(m.values)
-                if record is None:
-                    out = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True)
-                else:
-                    out, sc, idx, wt = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True,
-                                                             record=True)
-                    record[i] = {"x": x, "q": q, "pre": pre, "s1": s1, "s2": s2, "scores": sc, "indices": idx,
-                                 "weights": wt}
+                res = kernels.pk_select_bag(s1, s2, m.knn, table, scales, pre=pre, out_bf16=True,
+                                            record=record is not None)
+                out, sel = (res[0], res[1:]) if record is not None else (res, None)
                 delta = kernels.decode_linear(m.value_proj.weight, out, bias=m.value_proj.bias)
+                if record is not None:
+                    record[i] = {"x": x, "q": q, "pre": pre, "s1": s1, "s2": s2, "scores": sel[0], "indices": sel[1],
+                                 "weights": sel[2]}
             else:
                 f = blk.ffn
                 x, act = kernels.decode_linear(f.w13.weight, x, delta=delta, norm=blk.ffn_norm, write_x=True,

@@ -450,14 +450,14 @@ def test_fused_generate_multi_step_graph_matches_eager(monkeypatch, proj_max):
     assert torch.equal(graph, eager) and torch.equal(graph2, eager)
 
 
-@pytest.mark.parametrize("proj_max", [0, 64])
+@pytest.mark.parametrize("proj_max,mem_layer", [(0, 2), (64, 2), (0, 1), (64, 1)])
 @torch.no_grad()
-def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
-    """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last block: its query and swilu
-    projection match the host recomputation from the step's residual row (tests/query_check.py), its sub-key
-    scores the fp64 products of that query, its selection is bit-exact against the oracle on those scores, and
-    its logits are within 1e-2 of the fp32 torch path (oracle/torch_path.py) given that selection (the prompt
-    pass does not reach the step through the last block, so the caches agree)."""
+def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max, mem_layer):
+    """The fused decode step with a B-style memory layer (BatchNorm, swilu) in the last or a middle block: its
+    query and swilu projection match the host recomputation from the step's residual row (tests/query_check.py),
+    its sub-key scores the fp64 products of that query, its selection is bit-exact against the oracle on those
+    scores, and its logits are within 1e-2 of the fp32 torch path (oracle/torch_path.py) given that selection and
+    the prompt pass's (so that the caches of the blocks after the memory layer agree)."""
     import numpy as np
     import oracle.pkm_oracle as O
     import oracle.torch_path as TP
@@ -465,11 +465,11 @@ def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
     from smlm_hip.model import ModelConfig, Transformer, _FusedDecodeStep
     monkeypatch.setattr(_FusedDecodeStep, "proj_max_batch", proj_max)
     cfg = ModelConfig(vocab_size=512, d_model=128, n_layers=3, n_heads=2, ffn_hidden=256, max_seq_len=64,
-                      mem_layers=[2], mem_n_keys=128, mem_heads=4, mem_knn=16, mem_k_dim=64)
+                      mem_layers=[mem_layer], mem_n_keys=128, mem_heads=4, mem_knn=16, mem_k_dim=64)
     torch.manual_seed(3)
     m = Transformer(cfg).to(DEV, torch.bfloat16).eval()
     with torch.no_grad():
-        bn = m.layers[2].ffn.query_norm
+        bn = m.layers[mem_layer].ffn.query_norm
         bn.running_mean.normal_(0.0, 0.1)
         bn.running_var.uniform_(0.5, 2.0)
         bn.weight.uniform_(0.5, 1.5)
@@ -477,25 +477,35 @@ def test_fused_step_with_memory_layer_matches_torch_path(monkeypatch, proj_max):
     for kind in ("bf16", "int8"):
         m.set_memory_inference_table(kind)
         B, P = 3, 10
-        note(f"fused step memory layer table={kind} proj_max_batch={proj_max}")
-        dec, prompt = _prefilled(m, B, P, 7)
+        note(f"fused step memory layer {mem_layer} table={kind} proj_max_batch={proj_max}")
+        dec = m._decoder(B, P + 8, DEV)
         assert dec.fused is not None
+        prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=torch.Generator().manual_seed(7)).to(DEV)
+        mem = m.layers[mem_layer].ffn
+        mem.record = True
+        logits = m(prompt, kv_caches=dec.caches, pos0=0)
+        mem.record = False
+        sel_prompt = (mem.last_indices.cpu(), mem.last_weights.cpu())
+        dec.hist[:, :P] = prompt
+        dec.hist[:, P] = logits[:, -1].argmax(-1)
+        dec.tok.copy_(dec.hist[:, P:P + 1])
+        dec.pos.fill_(P)
         rec = {}
         got = dec.fused.run(dec.tok, dec.pos, dec.caches, dec.hist, logits=True, record=rec).float().cpu()
-        r = rec[2]
+        r = rec[mem_layer]
         s1, s2, sc, idx, w = r["s1"], r["s2"], r["scores"], r["indices"], r["weights"]
-        QC.check_decode_step_query(m, 2, r)
+        QC.check_decode_step_query(m, mem_layer, r)
         rs, ri, rw = O.pk_select(_bits(s1), _bits(s2), cfg.mem_knn)
         assert np.array_equal(idx.cpu().numpy(), ri) and np.array_equal(_bits(sc), rs)
         np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=0, atol=1e-6)
         sd = {k: v.float().cpu() for k, v in m.state_dict().items()}
         tables = None
         if kind == "int8":
-            codes, scales = m.layers[2].ffn.values.infer_table
-            tables = {2: K.dequantize_int8(codes, scales).cpu()}
+            codes, scales = mem.values.infer_table
+            tables = {mem_layer: K.dequantize_int8(codes, scales).cpu()}
         caches = [dict() for _ in range(cfg.n_layers)]
-        TP.lm_forward(sd, cfg.to_dict(), prompt.cpu(), caches, 0, tables=tables)
+        TP.lm_forward(sd, cfg.to_dict(), prompt.cpu(), caches, 0, tables=tables, selections={mem_layer: sel_prompt})
         ref = TP.lm_forward(sd, cfg.to_dict(), dec.tok.cpu(), caches, P, tables=tables,
-                            selections={2: (idx.cpu(), w.cpu())})[:, -1]
+                            selections={mem_layer: (idx.cpu(), w.cpu())})[:, -1]
         err = float((got - ref).abs().max() / ref.abs().max())
         assert err < 1e-2, err
