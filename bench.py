@@ -26,7 +26,8 @@ order they run (the headline ones first):
   config0        config 0: the B-1M PKM layer forward alone in fp32 over 8 x 256 tokens, GPU and host CPU.
   prefill        config 2: the LM with the B-4M memory (2048^2 rows) forward over 8 x 2048 prompt tokens (no
                  cache), tokens / median forward time; the prompt-pass attention kernel alone at that shape.
-  lookup         config 2 PKM lookup (B-4M, 8 x 2048 tokens): scoring, selection and bag kernels;
+  lookup         config 2 PKM lookup (B-4M, 8 x 2048 tokens): scoring, then selection + bag as one launch (and
+                 the selection and the bag as separate launches);
                  roofline_score: the scoring against the bf16 MFMA peak.
   offload        config 3 decode with the B-16M table as q4 in HBM, q4 / bf16 in pinned host RAM (zero-copy,
                  graphs), and bs1 from a q4 file through mmap (staged, no graphs).
@@ -400,23 +401,30 @@ def cpu_lookup_c2(q, keys, table, pre, idx_gpu, tokens, reps=3):
         # the check (untimed): the bf16 model's scores are the einsums rounded to bf16, as the kernels round them
         b1 = torch.einsum("nhd,hkd->nhk", qh[..., :half], kh[:, 0]).bfloat16().float()
         b2 = torch.einsum("nhd,hkd->nhk", qh[..., half:], kh[:, 1]).bfloat16().float()
-        _, bidx = TP.pkm_select_torch(b1, b2, 32)
+        bsc, bidx = TP.pkm_select_torch(b1, b2, 32)
+        g = idx_gpu[:tokens].cpu()
+        NK = b1.shape[-1]
+        gsc = b1.gather(-1, g // NK) + b2.gather(-1, g % NK)   # the GPU selection's scores on the host's scores
     ts.sort()
     dt = ts[len(ts) // 2]
-    g = idx_gpu[:tokens].cpu()
     same = float((bidx.sort(-1).values == g.sort(-1).values).all(-1).double().mean())
+    same_scores = float((bsc.sort(-1).values == gsc.sort(-1).values).all(-1).double().mean())
     return {"value": tokens / dt, "unit": "tok/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{tokens} of the 16,384 tokens: query -> scores -> selection -> softmax -> bag "
                       f"(x silu) in fp32 on the bf16 table, median of {reps} ({dt:.3f} s each; host copies "
                       f"{copy_s:.1f} s untimed), reference torch path restated in oracle/torch_path.py",
             "rows_with_the_gpu_selection_frac": same,
-            "rows_check": "the selection of every (token, head) row on the bf16-rounded einsum scores equals the "
-                          "GPU's as a set (torch.topk orders ties arbitrarily: a row may differ at a tie)"}
+            "rows_with_the_gpu_top_scores_frac": same_scores,
+            "rows_check": "per (token, head) row, on the bf16-rounded einsum scores: rows_with_the_gpu_selection_frac "
+                          "= the host's top-32 index set equals the GPU's (bf16 sums tie often, and torch.topk breaks "
+                          "ties arbitrarily, the kernels by index); rows_with_the_gpu_top_scores_frac = the GPU's 32 "
+                          "selected rows have the same score multiset as the host's top-32 (tie-independent)"}
 
 
 def lookup_prefill(dev, reps, cpu_tokens=0):
     """Config 2 PKM lookup: 8 x 2048 tokens, 4 heads x 2 halves x 2048 sub-keys of 256, top-32, 4M x 384 bf16
-    table; scoring, selection and bag kernels timed separately with HIP events.  With cpu_tokens, the torch path
+    table; the scoring, the selection and the bag kernels timed separately with HIP events, and the fused
+    selection + bag launch the memory layer runs (pk_select_bag): tok_s = tokens / (scoring + fused launch).  With cpu_tokens, the torch path
     on the host cores over that many of the tokens (cpu_lookup_c2)."""
     import torch
     from smlm_hip import kernels as K
@@ -432,10 +440,12 @@ def lookup_prefill(dev, reps, cpu_tokens=0):
     ms_select = event_time_ms(lambda: K.pk_select(s1, s2, 32), reps)
     ms_bag = event_time_ms(lambda: K.bag_infer(idx.view(N, -1), w.view(N, -1), table, pre=pre, out_bf16=True),
                            reps)
+    ms_select_bag = event_time_ms(lambda: K.pk_select_bag(s1, s2, 32, table, None, pre=pre, out_bf16=True), reps)
     flops = 2.0 * N * H * 2 * NK * (kd // 2)
-    total = ms_score + ms_select + ms_bag
+    total = ms_score + ms_select_bag
     res = {"tokens": N, "ms_score": ms_score, "ms_select": ms_select, "ms_bag": ms_bag,
-           "tok_s": N / total * 1e3, "score_TFLOPs": flops / ms_score / 1e9,
+           "ms_select_bag": ms_select_bag, "tok_s": N / total * 1e3,
+           "tok_s_separate_launches": N / (ms_score + ms_select + ms_bag) * 1e3, "score_TFLOPs": flops / ms_score / 1e9,
            "score_write_GBps": 2 * N * H * NK * 2 / ms_score / 1e6,
            "bag_alg_GBps": N * 128 * (2 * D + 12) / ms_bag / 1e6}
     if cpu_tokens:

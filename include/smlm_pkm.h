@@ -82,7 +82,7 @@ int smlm_pkm_select(const void *s1, const void *s2, int dtype, int64_t N, int H,
                     int64_t *idx, float *w, void *stream);
 
 /*
- * Selection fused with the value bag, for decode-sized batches: the work of smlm_pkm_select followed by
+ * Selection fused with the value bag, for any batch (decode steps and prompts): the work of smlm_pkm_select followed by
  * smlm_pkm_bag on its (idx, w) viewed as (N, H*knn), in one launch (one workgroup per token), with identical results.
  * Replaces pk_select + bag_infer of smlm/pkm.py:197-223 (kernels.py:214-226, 364-378).
  *   s1, s2 (N, H, NK) of dtype; table / table_dtype / rows / D / scales / pre / out / out_dtype as smlm_pkm_bag;

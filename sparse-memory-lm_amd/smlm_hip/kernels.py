@@ -176,8 +176,8 @@ def select_bag_supported(heads, table, scales=None):
 
 
 def pk_select_bag(s1, s2, knn, table, scales=None, pre=None, out_bf16=False, record=False):
-    """pk_select followed by bag_infer on its (indices, weights), in one launch per call (smlm_pkm_select_bag): for
-    decode-sized batches.  Same arguments and results as
+    """pk_select followed by bag_infer on its (indices, weights), in one launch per call (smlm_pkm_select_bag): the
+    memory layer's no-grad bf16 lookup at every batch size (decode steps and prompts).  Same arguments and results as
         scores, idx, w = pk_select(s1, s2, knn)
         out = bag_infer(idx.view(N, -1), w.view(N, -1), table, scales, pre, out_bf16)
     Returns out, or (out, scores, idx, w) with record=True.  H (= s1.shape[1]) <= 4."""

@@ -4,6 +4,8 @@ graph switch), whose lookup runs on the gfx950 kernels of smlm_hip.kernels:
 
     query_proj -> BatchNorm (fp32, eval statistics) -> pk_scores (MFMA) -> pk_select -> softmax
     -> bag_infer (value gather, swilu epilogue, bf16 out) -> value_proj
+(with bf16 activations, swilu, at most 4 heads and a table in device or pinned memory, pk_select and bag_infer are
+one launch, pk_select_bag, with the same results)
 
 impl: "hip", or the reference's names "torch" and "triton" (smlm/pkm.py:48), which a reference config carries;
 every name runs the same kernels (there is one implementation here) and is kept in self.impl for the config.
@@ -294,6 +296,19 @@ class ProductKeyMemory(nn.Module):
         sdt = torch.bfloat16 if (bf16 or self.keys.dtype == torch.bfloat16) else torch.float32
         q = self._query(x).to(sdt).view(N, self.heads, self.k_dim)
         s1, s2 = kernels.pk_scores(q, self._keys_as(sdt))
+        tables = inference_tables(self.values) if self.swilu and bf16 else None
+        if (tables is not None and self.log_score_scale is None
+                and kernels.select_bag_supported(self.heads, tables[0], tables[1])):
+            # selection, value bag and swilu epilogue in one launch (the same results as pk_select then bag_infer;
+            # different workgroups overlap the selection's vector work with the gather's memory traffic)
+            pre = self.swilu_proj(x).to(torch.bfloat16)
+            res = kernels.pk_select_bag(s1, s2, self.knn, tables[0], tables[1], pre=pre, out_bf16=True,
+                                        record=self.record)
+            out = res[0] if self.record else res
+            if self.record:
+                self.last_scores, self.last_indices, self.last_weights = res[1], res[2], res[3]
+                self.last_lookup = {"x": x, "q": q, "s1": s1, "s2": s2}
+            return self.value_proj(out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
         scores, indices, weights = kernels.pk_select(s1, s2, self.knn)
         if self.log_score_scale is not None:
             # a positive per-head scale keeps the selection; only the softmax sharpness changes
