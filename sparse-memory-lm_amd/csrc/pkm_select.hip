@@ -174,19 +174,71 @@ __device__ __forceinline__ Key xor_lane_key(Key v) {
   else return xor_lane<J>(v);
 }
 
+// (v[lane & ~J], v[lane | J]) on every lane for J = 16, 32: the gfx950 permlane swaps of a register with itself
+// return the lower lane's value in their first result and the upper lane's in their second
+template <int J>
+__device__ __forceinline__ void lane_pair(uint32_t v, uint32_t &lo, uint32_t &hi) {
+  const auto p = J == 16 ? __builtin_amdgcn_permlane16_swap(v, v, false, false)
+                         : __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  lo = (uint32_t)p[0];
+  hi = (uint32_t)p[1];
+}
+template <int J>
+__device__ __forceinline__ void lane_pair(uint64_t v, uint64_t &lo, uint64_t &hi) {
+  uint32_t l0, h0, l1, h1;
+  lane_pair<J>((uint32_t)v, l0, h0);
+  lane_pair<J>((uint32_t)(v >> 32), l1, h1);
+  lo = ((uint64_t)l1 << 32) | l0;
+  hi = ((uint64_t)h1 << 32) | h0;
+}
+
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// The lanes of slot s that keep the larger key of their pair at stage (K, J) of a descending bitonic sort: element
+// e = s * 64 + lane takes the maximum when it is the lower element of a descending block or the upper element of an
+// ascending one.  A constant per slot and stage.
+constexpr uint64_t take_max_lanes(int K, int J, int s) {
+  uint64_t m = 0;
+  for (int l = 0; l < kWave; ++l) {
+    const int e = s * kWave + l;
+    if (((e & J) == 0) == ((e & K) == 0)) m |= (uint64_t)1 << l;
+  }
+  return m;
+}
+
 // One compare-exchange stage (block size K, distance J < 64) of a descending bitonic sort of the wavefront's
-// SLOTS * 64 keys, element e = s * 64 + lane.
+// SLOTS * 64 keys, element e = s * 64 + lane.  Each lane holds a pair (a, b) of its key and its partner's and keeps
+// a where (a > b) equals its take-max bit: the compare writes a lane mask, one scalar xnor with the stage's constant
+// mask turns it into the select's, so a stage costs the lane exchange, one compare and one select per 32-bit word
+// (the lane-dependent direction computed per lane cost three more vector instructions per stage: the config-2
+// selection measured 146 -> 129 us with this form, the selection being bound by vector-instruction issue).  J = 16,
+// 32: the pair comes from the permlane swap as (lower lane's key, upper lane's key), which needs no select to recover
+// the partner.
 template <typename Key, int SLOTS, int K, int J>
 __device__ __forceinline__ void bitonic_stage(Key (&x)[SLOTS]) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int s = 0; s < SLOTS; ++s) {
-    const int e = s * kWave + lane;
-    const Key y = xor_lane_key<J>(x[s]);
-    const bool take_max = ((e & J) == 0) == ((e & K) == 0);  // the lower element of a descending block: max
-    const bool gt = x[s] > y;
-    x[s] = (gt == take_max) ? x[s] : y;
-  }
+  static_for<SLOTS>([&](auto sc) {
+    constexpr int s = decltype(sc)::value;
+    constexpr uint64_t tm = take_max_lanes(K, J, s);
+    Key a, b;
+    if constexpr (J == 16 || J == 32) {
+      lane_pair<J>(x[s], a, b);
+    } else {
+      a = x[s];
+      b = xor_lane_key<J>(x[s]);
+    }
+    const uint64_t keep = ~(__builtin_amdgcn_ballot_w64(a > b) ^ tm);
+    x[s] = __builtin_amdgcn_inverse_ballot_w64(keep) ? a : b;
+  });
 }
 
 template <typename Key, int SLOTS, int K, int J>
