@@ -424,6 +424,7 @@ __global__ void __launch_bounds__(WAVES * 64)
 // as whole 128-byte score rows.  A wavefront that stalls on a store is then never one that has MFMAs to issue: the
 // stores (537 MB at config 2) and the products overlap.  One barrier per block.  The score rows are written with
 // non-temporal stores: they stream to memory instead of displacing the caches (0.217 -> 0.148 ms at config 2).
+// The key rows in LDS are padded by 32 bytes (the compute wavefronts' fragment reads conflict less than with 16).
 constexpr int kWsTok = 256;             // tokens per workgroup
 constexpr int kWsOutStride = kStreamKeys + 8;  // LDS output tile row stride (bf16)
 
@@ -432,7 +433,9 @@ __global__ void __launch_bounds__(512)
     score_ws_kernel(const uint16_t *__restrict__ q, int64_t q_stride, const uint16_t *__restrict__ keys, int N,
                     int H, int NK, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
   constexpr int HALF = KSTEPS * 32;
-  constexpr int RS = HALF + 8;               // LDS key row stride (bf16)
+  // LDS key row stride (bf16): rows padded by 32 bytes.  Measured with SQ_LDS_BANK_CONFLICT at config 2: 14.7 M
+  // conflict cycles per launch with 16 bytes of padding (and with 48), 6.3 M with 32; 139-140 -> 135.5-136 us
+  constexpr int RS = HALF + 16;
   constexpr int PPR = HALF / 8;              // 16-byte pieces per sub-key row
   constexpr int PPT = kStreamKeys * PPR / 256;   // key pieces per memory thread per block
   constexpr int RPP = 256 / PPR;             // key rows per memory pass
