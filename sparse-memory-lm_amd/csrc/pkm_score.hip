@@ -434,7 +434,9 @@ __global__ void __launch_bounds__(512)
                     int H, int NK, uint16_t *__restrict__ s1, uint16_t *__restrict__ s2) {
   constexpr int HALF = KSTEPS * 32;
   // LDS key row stride (bf16): rows padded by 32 bytes.  Measured with SQ_LDS_BANK_CONFLICT at config 2: 14.7 M
-  // conflict cycles per launch with 16 bytes of padding (and with 48), 6.3 M with 32; 139-140 -> 135.5-136 us
+  // conflict cycles per launch with 16 bytes of padding (and with 48), 6.3 M with 32; 139-140 -> 135.5-136 us.  The
+  // output tile's share: unpadded rows with the 16-byte pieces XOR-swizzled by row took the count to 4.2 M and the
+  // time nowhere (135-137 us); wider padding raised it (16.8-25.2 M), no padding at all 62.9 M (234 us)
   constexpr int RS = HALF + 16;
   constexpr int PPR = HALF / 8;              // 16-byte pieces per sub-key row
   constexpr int PPT = kStreamKeys * PPR / 256;   // key pieces per memory thread per block
