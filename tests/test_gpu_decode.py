@@ -324,6 +324,8 @@ def _tables(kind, rows, D, seed):
     (5, 4, 1000, 5, torch.bfloat16, "int8", True, True),      # knn not a power of two: pairs built at run time
     (2, 4, 4096, 128, torch.bfloat16, "bf16", True, True),    # knn above 64: two results per lane
     (4, 2, 256, 100, torch.float32, "bf16", False, False),
+    (3, 4, 2048, 128, torch.float32, "fp32", True, False),    # the most LDS: fp32 keys, 4 heads, knn 128
+    (2048, 4, 2048, 32, torch.bfloat16, "bf16", True, True),  # a prompt-sized batch (the memory layer's prefill)
 ])
 def test_select_bag_bit_identical_to_select_then_bag(N, H, NK, knn, dtype, kind, with_pre, out_bf16):
     """pk_select_bag == pk_select followed by bag_infer, bit for bit (same selection, same bag additions in the
