@@ -404,7 +404,14 @@ def cpu_lookup_c2(q, keys, table, pre, idx_gpu, tokens, reps=3):
         bsc, bidx = TP.pkm_select_torch(b1, b2, 32)
         g = idx_gpu[:tokens].cpu()
         NK = b1.shape[-1]
-        gsc = b1.gather(-1, g // NK) + b2.gather(-1, g % NK)   # the GPU selection's scores on the host's scores
+        # the bf16 model's candidate rule (smlm/kernels.py:200-211, the kernels' rule): the (i+1)(j+1) <= knn pairs of
+        # the two halves' top 32, each scored bf16(v1 + v2); the top-32 VALUES of that are tie-independent
+        a1, a2 = b1.topk(32, -1).values, b2.topk(32, -1).values
+        r = torch.arange(32)
+        keep = ((r[:, None] + 1) * (r[None, :] + 1) <= 32).reshape(-1)
+        cand = (a1.unsqueeze(-1) + a2.unsqueeze(-2)).bfloat16().float().flatten(-2)[..., keep]
+        bsc = cand.topk(32, -1).values
+        gsc = (b1.gather(-1, g // NK) + b2.gather(-1, g % NK)).bfloat16().float()   # the GPU selection, same rule
     ts.sort()
     dt = ts[len(ts) // 2]
     same = float((bidx.sort(-1).values == g.sort(-1).values).all(-1).double().mean())
@@ -416,9 +423,11 @@ def cpu_lookup_c2(q, keys, table, pre, idx_gpu, tokens, reps=3):
             "rows_with_the_gpu_selection_frac": same,
             "rows_with_the_gpu_top_scores_frac": same_scores,
             "rows_check": "per (token, head) row, on the bf16-rounded einsum scores: rows_with_the_gpu_selection_frac "
-                          "= the host's top-32 index set equals the GPU's (bf16 sums tie often, and torch.topk breaks "
-                          "ties arbitrarily, the kernels by index); rows_with_the_gpu_top_scores_frac = the GPU's 32 "
-                          "selected rows have the same score multiset as the host's top-32 (tie-independent)"}
+                          "= the torch path's top-32 index set (fp32 candidate sums) equals the GPU's; "
+                          "rows_with_the_gpu_top_scores_frac = the GPU's 32 rows have the same multiset of bf16(v1 + "
+                          "v2) scores as the top 32 of the pruned candidates by that rule (the bf16 model's; "
+                          "independent of how ties are broken, which torch.topk does arbitrarily and the kernels by "
+                          "index)"}
 
 
 def lookup_prefill(dev, reps, cpu_tokens=0):
