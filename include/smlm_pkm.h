@@ -185,6 +185,17 @@ int smlm_decode_attention_proj(const void *qkv, int64_t qkv_row_stride, const vo
 int smlm_swiglu(const void *in, int64_t in_row_stride, void *out, int64_t M, int hidden, void *stream);
 
 /*
+ * The FFN up-projection of a prompt pass with the SwiGLU activation in its epilogue: replaces self.w13(x) followed
+ * by F.silu(a) * b of smlm/model.py:110-118 (SwiGLU.forward) for bf16 activations and weights.
+ *   x (M, K) bf16 rows, w13 (2*hidden, K) bf16 (nn.Linear weight: a rows then b rows), out (M, hidden) bf16:
+ *   out[m, j] = bf16(bf16(silu(a)) * b), a = bf16(x[m] . w13[j]), b = bf16(x[m] . w13[hidden + j]) with fp32
+ *   accumulation (the bf16 projection's roundings followed by smlm_swiglu's).
+ * K a multiple of 128, hidden a multiple of 64; 16-byte aligned rows, strides in elements.
+ */
+int smlm_linear_swiglu(const void *x, int64_t x_row_stride, const void *w13, int64_t w_row_stride, int64_t M, int K,
+                       int hidden, void *out, int64_t out_row_stride, void *stream);
+
+/*
  * Greedy token choice of the decode loop (smlm/train.py:297-299, `nxt = logits[:, -1:].argmax(-1)`): per row
  * the first index of the largest bf16 logit, written to tok[b]; if hist is given, also to
  * hist[b, *pos + 1] (skipped when that slot is outside [0, hist_len)).

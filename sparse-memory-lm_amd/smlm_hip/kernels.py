@@ -433,6 +433,34 @@ def swiglu(h13):
     return out.view(*h13.shape[:-1], hidden)
 
 
+def linear_swiglu_supported(x, w13):
+    """Whether linear_swiglu takes these operands (bf16 CUDA tensors, K a multiple of 128, hidden of 64)."""
+    return (x.is_cuda and w13.is_cuda and x.dtype == torch.bfloat16 and w13.dtype == torch.bfloat16
+            and w13.dim() == 2 and x.shape[-1] == w13.shape[1] and w13.shape[0] % 128 == 0
+            and w13.shape[1] % 128 == 0)
+
+
+def linear_swiglu(x, w13):
+    """bf16(bf16(silu(a)) * b) with a | b = the halves of bf16(x @ w13.T): the w13 projection and the SwiGLU
+    activation of smlm/model.py:110-118 in one launch (smlm_linear_swiglu), for prompt passes.  x (..., K) bf16,
+    w13 (2 * hidden, K) bf16 with K a multiple of 128 and hidden of 64.  Returns (..., hidden) bf16."""
+    _need_cuda("linear_swiglu", x, w13)
+    if not linear_swiglu_supported(x, w13):
+        raise ValueError(f"linear_swiglu: x (..., K) and w13 (2*hidden, K) must be bf16 with K a multiple of 128 "
+                         f"and hidden of 64, got {x.dtype} {tuple(x.shape)} and {w13.dtype} {tuple(w13.shape)}")
+    K, hidden = w13.shape[1], w13.shape[0] // 2
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    if w13.stride(1) != 1 or w13.stride(0) % 8 or w13.data_ptr() % 16:
+        w13 = w13.contiguous()
+    out = torch.empty(x2.shape[0], hidden, dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().smlm_linear_swiglu(x2.data_ptr(), x2.stride(0), w13.data_ptr(), w13.stride(0), x2.shape[0], K,
+                                       hidden, out.data_ptr(), hidden, _stream(x))
+    _lib.check(rc, "smlm_linear_swiglu")
+    return out.view(*x.shape[:-1], hidden)
+
+
 def greedy_argmax(logits, pos=None, tok=None, hist=None):
     """logits (B, V) bf16 -> tok (B,) int64, the first index of each row's largest logit (torch.argmax's rule),
     written into `tok` if given; with `hist` (B, L) int64 and a device int64 `pos`, also hist[b, pos + 1] = tok[b]

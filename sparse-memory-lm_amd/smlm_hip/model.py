@@ -226,9 +226,19 @@ class SwiGLU(nn.Module):
         self.w13 = nn.Linear(d, 2 * hidden, bias=False)
         self.w2 = nn.Linear(hidden, d, bias=False)
 
+    fused_min_rows = 128   # prompt passes: rows from which the projection and activation are one launch
+
     def forward(self, x):
         """w2(silu(a) * b) with a | b = w13(x).  On bf16 GPU tensors the activation is one kernel
-        (smlm_hip.kernels.swiglu) with the same roundings."""
+        (smlm_hip.kernels.swiglu) with the same roundings; without autograd, from fused_min_rows rows on, the w13
+        projection and the activation are one launch (kernels.linear_swiglu: the same roundings, and the
+        projection's products on the matrix cores in fp32)."""
+        w = self.w13.weight
+        if (x.is_cuda and x.dtype == torch.bfloat16 and x.numel() >= self.fused_min_rows * x.shape[-1]
+                and self.w13.bias is None and kernels.linear_swiglu_supported(x, w)
+                and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))
+                and not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != torch.bfloat16)):
+            return self.w2(kernels.linear_swiglu(x, w))
         h = self.w13(x)
         if h.is_cuda and h.dtype == torch.bfloat16 and h.shape[-1] % 16 == 0:
             act = kernels.swiglu(h)

@@ -207,3 +207,82 @@ def test_model_prefill_kernels_match_torch_path():
     for what, t in (("one pass", got), ("two chunks", torch.cat([a, b], dim=1))):
         err = float((t.float() - ref).abs().max())
         assert err <= 2e-2 * scale, f"{what}: logits off by {err:.3e} (scale {scale:.3e})"
+
+
+# ----------------------------------------------------------------------------- FFN up-projection + SwiGLU (fused)
+def _swiglu_rule(x, w):
+    """The bf16 model's arithmetic from fp64 products: a, b = bf16 of the projection's halves, then
+    bf16(bf16(silu(a)) * b) (smlm/model.py:110-118 with the bf16 roundings of the projection and the activation).
+    Returns (out, a, b) as fp32 tensors of bf16 values."""
+    h = (x.double() @ w.double().T).float().bfloat16().float()
+    H = w.shape[0] // 2
+    a, b = h[:, :H], h[:, H:]
+    return _act(a, b), a, b
+
+
+def _act(a, b):
+    s = (a / (1.0 + torch.exp(-a))).bfloat16().float()
+    return (s * b).bfloat16().float()
+
+
+def _ulp_bf16(t):
+    return torch.pow(2.0, torch.floor(torch.log2(t.abs().clamp_min(2.0 ** -126))) - 7)
+
+
+def _check_swiglu(got, x, w, what):
+    """At least 99.9% of the outputs are the rule on the exact roundings (_swiglu_rule), and every other one lies
+    within the error the kernel's arithmetic allows: a and b each off by their fp32 accumulation (2^-20 of the sum
+    of |x w| over the dot product, a generous bound on K = 1024 additions) plus one bf16 ulp, carried through silu
+    (|silu'| <= 1.1) and the product, plus one bf16 rounding of s and of the output.  A wrong operand (a and b
+    exchanged, a feature or token shifted) misses by orders of magnitude."""
+    ref, a, b = _swiglu_rule(x, w)
+    miss = got != ref
+    assert float(miss.double().mean()) <= 1e-3, f"{what}: {int(miss.sum())} outputs differ from the rule"
+    if bool(miss.any()):
+        H = w.shape[0] // 2
+        mag = x.double().abs() @ w.double().abs().T
+        ma, mb = mag[:, :H][miss], mag[:, H:][miss]
+        am, bm, gm, rm = a[miss].double(), b[miss].double(), got[miss].double(), ref[miss].double()
+        da = _ulp_bf16(am) + 2.0 ** -20 * ma
+        db = _ulp_bf16(bm) + 2.0 ** -20 * mb
+        sm = am / (1.0 + torch.exp(-am))
+        ds = 1.1 * da + _ulp_bf16(sm)
+        bound = sm.abs() * db + bm.abs() * ds + ds * db + _ulp_bf16(rm) + _ulp_bf16(gm)
+        bad = (gm - rm).abs() > bound
+        assert not bool(bad.any()), f"{what}: {int(bad.sum())} outputs beyond the arithmetic's error bound"
+
+
+@pytest.mark.parametrize("M,Kd,H", [(16384, 384, 1024), (1000, 384, 1024), (129, 512, 64), (1, 128, 128),
+                                    (300, 256, 192), (128, 1024, 512), (257, 384, 2048)])
+def test_linear_swiglu_matches_the_bf16_rule(M, Kd, H):
+    """kernels.linear_swiglu against the fp64-product restatement of the w13 projection + SwiGLU roundings
+    (_check_swiglu), with partial token tiles (M not a multiple of 128) and one row; the unfused pair (the library
+    GEMM + smlm_swiglu) meets the same check."""
+    note(f"linear_swiglu M={M} K={Kd} H={H}")
+    g = torch.Generator(device=DEV).manual_seed(M + Kd + H)
+    x = torch.randn(M, Kd, generator=g, device=DEV).bfloat16()
+    w = (torch.randn(2 * H, Kd, generator=g, device=DEV) * 0.05).bfloat16()
+    _check_swiglu(K.linear_swiglu(x, w).float(), x, w, "fused")
+    if M == 1000:   # a planted mistake fails the check: the a and b halves of the weight exchanged
+        wx = torch.cat([w[H:], w[:H]])
+        with pytest.raises(AssertionError):
+            _check_swiglu(K.linear_swiglu(x, wx).float(), x, w, "exchanged halves")
+    if M > 1:
+        _check_swiglu(K.swiglu(F.linear(x, w)).float(), x, w, "library GEMM + swiglu")
+
+
+def test_linear_swiglu_strided_input_and_rejects():
+    """A (rows, K) view with a row stride larger than K gives the contiguous call's bits; shapes outside the
+    kernel (K not a multiple of 128, hidden not of 64, fp32) are refused with ValueError."""
+    note("linear_swiglu strided / rejects")
+    g = torch.Generator(device=DEV).manual_seed(5)
+    big = torch.randn(300, 512, generator=g, device=DEV).bfloat16()
+    w = (torch.randn(256, 384, generator=g, device=DEV) * 0.05).bfloat16()
+    view = big[:, :384]
+    assert torch.equal(K.linear_swiglu(view, w), K.linear_swiglu(view.contiguous(), w))
+    with pytest.raises(ValueError):
+        K.linear_swiglu(big[:, :320], (torch.randn(256, 320, device=DEV)).bfloat16())
+    with pytest.raises(ValueError):
+        K.linear_swiglu(view, w[:192])
+    with pytest.raises(ValueError):
+        K.linear_swiglu(view.float(), w.float())
