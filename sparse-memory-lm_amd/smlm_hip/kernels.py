@@ -461,6 +461,51 @@ def linear_swiglu(x, w13):
     return out.view(*x.shape[:-1], hidden)
 
 
+def prompt_linear_supported(x, w, bias=None):
+    """Whether prompt_linear takes these operands (bf16 CUDA tensors, K and N multiples of 128, bias bf16 or None)."""
+    return (x.is_cuda and w.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2
+            and x.shape[-1] == w.shape[1] and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0
+            and (bias is None or (bias.is_cuda and bias.dtype == torch.bfloat16 and bias.shape == (w.shape[0],))))
+
+
+def prompt_linear(x, w, bias=None):
+    """bf16(x @ w.T + bias) with fp32 accumulation (smlm_prompt_linear): an nn.Linear of a prompt pass on the
+    matrix cores.  x (..., K) bf16, w (N, K) bf16 with K and N multiples of 128, bias (N,) bf16 or None.  Returns
+    (..., N) bf16."""
+    _need_cuda("prompt_linear", x, w, bias)
+    if not prompt_linear_supported(x, w, bias):
+        raise ValueError(f"prompt_linear: x (..., K), w (N, K) and bias (N,) must be bf16 with K and N multiples of "
+                         f"128, got {x.dtype} {tuple(x.shape)}, {w.dtype} {tuple(w.shape)}")
+    N, K = w.shape
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    if w.stride(1) != 1 or w.stride(0) % 8 or w.data_ptr() % 16:
+        w = w.contiguous()
+    bias = bias.contiguous() if bias is not None else None
+    out = torch.empty(x2.shape[0], N, dtype=torch.bfloat16, device=x.device)
+    rc = _lib.lib().smlm_prompt_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
+                                       bias.data_ptr() if bias is not None else None, x2.shape[0], K, N,
+                                       out.data_ptr(), N, _stream(x))
+    _lib.check(rc, "smlm_prompt_linear")
+    return out.view(*x.shape[:-1], N)
+
+
+def linear(mod, x, min_rows=128, max_n=1152):
+    """mod(x) for an nn.Linear, through prompt_linear when that applies (bf16 weights and activations, no autograd
+    recording, at least min_rows rows, at most max_n outputs, K and N multiples of 128, bf16 or no autocast): the
+    same roundings (bf16 out of the fp32 accumulation, the bias added in fp32).  max_n: wider projections keep the
+    library GEMM, faster there on MI355X (2048 outputs: 34 against 43 us for 16,384 x 384 rows)."""
+    w, b = mod.weight, mod.bias
+    if (x.is_cuda and x.dtype == torch.bfloat16 and w.shape[0] <= max_n and x.numel() >= min_rows * x.shape[-1]
+            and prompt_linear_supported(x, w, b)
+            and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad
+                                                  or (b is not None and b.requires_grad)))
+            and not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != torch.bfloat16)):
+        return prompt_linear(x, w, b)
+    return mod(x)
+
+
 def greedy_argmax(logits, pos=None, tok=None, hist=None):
     """logits (B, V) bf16 -> tok (B,) int64, the first index of each row's largest logit (torch.argmax's rule),
     written into `tok` if given; with `hist` (B, L) int64 and a device int64 `pos`, also hist[b, pos + 1] = tok[b]

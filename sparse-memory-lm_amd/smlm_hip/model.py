@@ -124,9 +124,10 @@ class Attention(nn.Module):
             qkv = self.wqkv(x).view(B, 3 * C).to(torch.bfloat16)
             y = kernels.decode_attention(qkv, self.rope.cos, self.rope.sin, pos0, kv_cache.k, kv_cache.v)
             return self.wo(y.view(B, 1, C).to(x.dtype))
-        qkv = self.wqkv(x)
+        # prompt passes: the projections through kernels.linear (smlm_prompt_linear from 128 rows on, no autograd)
+        qkv = kernels.linear(self.wqkv, x)
         if not torch.is_tensor(pos0) and _use_attention_kernels(qkv, self.head_dim):
-            return self.wo(self._prefill_kernels(qkv, kv_cache, pos0).reshape(B, T, C))
+            return kernels.linear(self.wo, self._prefill_kernels(qkv, kv_cache, pos0).reshape(B, T, C))
         q, k, v = qkv.view(B, T, 3, self.n_heads, self.head_dim).permute(2, 0, 3, 1, 4)
         q, k = self.rope(q, pos0), self.rope(k, pos0)
         if isinstance(kv_cache, StaticKVCache):
@@ -138,7 +139,7 @@ class Attention(nn.Module):
                     v = torch.cat([kv_cache["v"], v], dim=2)
                 kv_cache["k"], kv_cache["v"] = k, v
             y = _causal_attention(q, k, v)
-        return self.wo(y.reshape(B, T, C))
+        return kernels.linear(self.wo, y.reshape(B, T, C))
 
     def _prefill_kernels(self, qkv, kv_cache, pos0):
         """RoPE (smlm_rope_qkv, written straight into the static cache's slots when there is one) and causal
@@ -232,20 +233,20 @@ class SwiGLU(nn.Module):
         """w2(silu(a) * b) with a | b = w13(x).  On bf16 GPU tensors the activation is one kernel
         (smlm_hip.kernels.swiglu) with the same roundings; without autograd, from fused_min_rows rows on, the w13
         projection and the activation are one launch (kernels.linear_swiglu: the same roundings, and the
-        projection's products on the matrix cores in fp32)."""
+        projection's products on the matrix cores in fp32), and w2 runs through kernels.linear."""
         w = self.w13.weight
         if (x.is_cuda and x.dtype == torch.bfloat16 and x.numel() >= self.fused_min_rows * x.shape[-1]
                 and self.w13.bias is None and kernels.linear_swiglu_supported(x, w)
                 and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))
                 and not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != torch.bfloat16)):
-            return self.w2(kernels.linear_swiglu(x, w))
+            return kernels.linear(self.w2, kernels.linear_swiglu(x, w))
         h = self.w13(x)
         if h.is_cuda and h.dtype == torch.bfloat16 and h.shape[-1] % 16 == 0:
             act = kernels.swiglu(h)
         else:
             a, b = h.chunk(2, dim=-1)
             act = F.silu(a) * b
-        return self.w2(act)
+        return kernels.linear(self.w2, act)
 
 
 def _memory(cfg, shared):

@@ -301,14 +301,15 @@ class ProductKeyMemory(nn.Module):
                 and kernels.select_bag_supported(self.heads, tables[0], tables[1])):
             # selection, value bag and swilu epilogue in one launch (the same results as pk_select then bag_infer;
             # different workgroups overlap the selection's vector work with the gather's memory traffic)
-            pre = self.swilu_proj(x).to(torch.bfloat16)
+            pre = kernels.linear(self.swilu_proj, x).to(torch.bfloat16)
             res = kernels.pk_select_bag(s1, s2, self.knn, tables[0], tables[1], pre=pre, out_bf16=True,
                                         record=self.record)
             out = res[0] if self.record else res
             if self.record:
                 self.last_scores, self.last_indices, self.last_weights = res[1], res[2], res[3]
                 self.last_lookup = {"x": x, "q": q, "s1": s1, "s2": s2}
-            return self.value_proj(out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
+            return kernels.linear(self.value_proj,
+                                  out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
         scores, indices, weights = kernels.pk_select(s1, s2, self.knn)
         if self.log_score_scale is not None:
             # a positive per-head scale keeps the selection; only the softmax sharpness changes
@@ -320,13 +321,14 @@ class ProductKeyMemory(nn.Module):
         idx, w = indices.view(N, -1), weights.view(N, -1)
         if self.swilu and bf16:
             # fused inference bag: value rows (bf16 / fp32 / int8 / q4 table) * bf16(silu(pre)), bf16 out
-            pre = self.swilu_proj(x).to(torch.bfloat16)
+            pre = kernels.linear(self.swilu_proj, x).to(torch.bfloat16)
             tables = inference_tables(self.values)
             if tables is None:                  # a table tier that stages every call (smlm_hip.offload)
                 out = self.values.infer_table.bag(idx, w, pre)
             else:
                 out = kernels.bag_infer(idx, w, tables[0], tables[1], pre=pre, out_bf16=True)
-            return self.value_proj(out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
+            return kernels.linear(self.value_proj,
+                                  out.to(self.value_proj.weight.dtype) if not _autocast_bf16(x) else out)
         out = self.read_values(idx, w)
         if self.swilu:
             out = self.value_proj(out * F.silu(self.swilu_proj(x)).to(out.dtype))

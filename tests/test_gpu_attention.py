@@ -286,3 +286,69 @@ def test_linear_swiglu_strided_input_and_rejects():
         K.linear_swiglu(view, w[:192])
     with pytest.raises(ValueError):
         K.linear_swiglu(view.float(), w.float())
+
+
+def _check_linear(got, x, w, bias, what):
+    """At least 99.9% of the outputs are bf16 of the fp64 product plus the bias, and every other one lies within
+    the fp32 accumulation's error (2^-20 of the sum of |x w| and |bias|, generous for K <= 1024 additions) plus
+    one bf16 ulp of either value.  A wrong operand (a shifted weight row or bias entry) misses by far more."""
+    exact = x.double() @ w.double().T + (bias.double() if bias is not None else 0.0)
+    ref = exact.float().bfloat16().float()
+    miss = got != ref
+    assert float(miss.double().mean()) <= 1e-3, f"{what}: {int(miss.sum())} outputs differ from the rule"
+    if bool(miss.any()):
+        mag = x.double().abs() @ w.double().abs().T + (bias.double().abs() if bias is not None else 0.0)
+        gm, rm = got[miss].double(), ref[miss].double()
+        bound = 2.0 ** -20 * mag[miss] + _ulp_bf16(rm) + _ulp_bf16(gm)
+        bad = (gm - rm).abs() > bound
+        assert not bool(bad.any()), f"{what}: {int(bad.sum())} outputs beyond the arithmetic's error bound"
+
+
+@pytest.mark.parametrize("M,Kd,N,with_bias", [(16384, 384, 1152, False), (16384, 384, 384, True),
+                                              (16384, 1024, 384, False), (1000, 384, 384, True),
+                                              (129, 512, 128, True), (1, 128, 256, False), (300, 256, 640, True)])
+def test_prompt_linear_matches_the_fp64_rule(M, Kd, N, with_bias):
+    """kernels.prompt_linear against bf16 of the fp64 product (+ bias) (_check_linear), at the model's prompt-pass
+    shapes (wqkv, wo / value_proj with its bias, w2) and partial token tiles; the library's F.linear meets the same
+    check, and a bias shifted by one feature fails it."""
+    note(f"prompt_linear M={M} K={Kd} N={N} bias={with_bias}")
+    g = torch.Generator(device=DEV).manual_seed(M + Kd + N)
+    x = torch.randn(M, Kd, generator=g, device=DEV).bfloat16()
+    w = (torch.randn(N, Kd, generator=g, device=DEV) * 0.05).bfloat16()
+    b = torch.randn(N, generator=g, device=DEV).bfloat16() if with_bias else None
+    got = K.prompt_linear(x, w, b).float()
+    _check_linear(got, x, w, b, "prompt_linear")
+    if M > 1:
+        _check_linear(F.linear(x, w, b).float(), x, w, b, "F.linear")
+    if with_bias and M == 1000:
+        with pytest.raises(AssertionError):
+            _check_linear(K.prompt_linear(x, w, b.roll(1)).float(), x, w, b, "shifted bias")
+
+
+def test_prompt_linear_strided_input_rejects_and_dispatch():
+    """A strided (rows, K) view gives the contiguous call's bits; shapes outside the kernel are refused with
+    ValueError; kernels.linear takes the kernel for a no-grad bf16 prompt (its bits) and the module itself for few
+    rows or when autograd records (gradients then flow as through nn.Linear)."""
+    note("prompt_linear strided / rejects / dispatch")
+    g = torch.Generator(device=DEV).manual_seed(6)
+    big = torch.randn(300, 512, generator=g, device=DEV).bfloat16()
+    w = (torch.randn(256, 384, generator=g, device=DEV) * 0.05).bfloat16()
+    view = big[:, :384]
+    assert torch.equal(K.prompt_linear(view, w), K.prompt_linear(view.contiguous(), w))
+    with pytest.raises(ValueError):
+        K.prompt_linear(big[:, :320], torch.randn(256, 320, device=DEV).bfloat16())
+    with pytest.raises(ValueError):
+        K.prompt_linear(view, w[:192])
+    with pytest.raises(ValueError):
+        K.prompt_linear(view.float(), w.float())
+    with pytest.raises(ValueError):
+        K.prompt_linear(view, w, torch.zeros(256, device=DEV))
+    lin = torch.nn.Linear(384, 256, device=DEV).bfloat16()
+    x3 = torch.randn(2, 150, 384, generator=g, device=DEV).bfloat16()
+    with torch.no_grad():
+        assert torch.equal(K.linear(lin, x3), K.prompt_linear(x3, lin.weight, lin.bias))
+        assert torch.equal(K.linear(lin, x3[:, :60]), lin(x3[:, :60]))
+    y = K.linear(lin, x3)
+    assert y.requires_grad
+    y.float().sum().backward()
+    assert lin.weight.grad is not None and lin.bias.grad is not None
