@@ -190,7 +190,7 @@ int smlm_swiglu(const void *in, int64_t in_row_stride, void *out, int64_t M, int
  *   x (M, K) bf16 rows, w13 (2*hidden, K) bf16 (nn.Linear weight: a rows then b rows), out (M, hidden) bf16:
  *   out[m, j] = bf16(bf16(silu(a)) * b), a = bf16(x[m] . w13[j]), b = bf16(x[m] . w13[hidden + j]) with fp32
  *   accumulation (the bf16 projection's roundings followed by smlm_swiglu's).
- * K a multiple of 128, hidden a multiple of 64; 16-byte aligned rows, strides in elements.
+ * K a multiple of 64, hidden a multiple of 64; 16-byte aligned rows, strides in elements.
  */
 int smlm_linear_swiglu(const void *x, int64_t x_row_stride, const void *w13, int64_t w_row_stride, int64_t M, int K,
                        int hidden, void *out, int64_t out_row_stride, void *stream);
@@ -199,8 +199,8 @@ int smlm_linear_swiglu(const void *x, int64_t x_row_stride, const void *w13, int
  * A projection of a prompt pass, out = bf16(x W^T + bias) with fp32 accumulation (the bias, if any, added in
  * fp32): replaces the nn.Linear calls self.wqkv(x), self.wo(y) and self.w2(h) of smlm/model.py:92, 107, 118 and
  * swilu_proj / value_proj of smlm/pkm.py:213-224 for bf16 activations and weights.
- *   x (M, K) bf16 rows, w (N, K) bf16 (nn.Linear weight), bias (N,) bf16 or NULL, out (M, N) bf16; K and N
- *   multiples of 128; 16-byte aligned rows, strides in elements.
+ *   x (M, K) bf16 rows, w (N, K) bf16 (nn.Linear weight), bias (N,) bf16 or NULL, out (M, N) bf16; K a
+ *   multiple of 64, N of 128; 16-byte aligned rows, strides in elements.
  */
 int smlm_prompt_linear(const void *x, int64_t x_row_stride, const void *w, int64_t w_row_stride, const void *bias,
                        int64_t M, int K, int N, void *out, int64_t out_row_stride, void *stream);

@@ -434,19 +434,19 @@ def swiglu(h13):
 
 
 def linear_swiglu_supported(x, w13):
-    """Whether linear_swiglu takes these operands (bf16 CUDA tensors, K a multiple of 128, hidden of 64)."""
+    """Whether linear_swiglu takes these operands (bf16 CUDA tensors, K a multiple of 64, hidden of 64)."""
     return (x.is_cuda and w13.is_cuda and x.dtype == torch.bfloat16 and w13.dtype == torch.bfloat16
             and w13.dim() == 2 and x.shape[-1] == w13.shape[1] and w13.shape[0] % 128 == 0
-            and w13.shape[1] % 128 == 0)
+            and w13.shape[1] % 64 == 0)
 
 
 def linear_swiglu(x, w13):
     """bf16(bf16(silu(a)) * b) with a | b = the halves of bf16(x @ w13.T): the w13 projection and the SwiGLU
     activation of smlm/model.py:110-118 in one launch (smlm_linear_swiglu), for prompt passes.  x (..., K) bf16,
-    w13 (2 * hidden, K) bf16 with K a multiple of 128 and hidden of 64.  Returns (..., hidden) bf16."""
+    w13 (2 * hidden, K) bf16 with K a multiple of 64 and hidden of 64.  Returns (..., hidden) bf16."""
     _need_cuda("linear_swiglu", x, w13)
     if not linear_swiglu_supported(x, w13):
-        raise ValueError(f"linear_swiglu: x (..., K) and w13 (2*hidden, K) must be bf16 with K a multiple of 128 "
+        raise ValueError(f"linear_swiglu: x (..., K) and w13 (2*hidden, K) must be bf16 with K a multiple of 64 "
                          f"and hidden of 64, got {x.dtype} {tuple(x.shape)} and {w13.dtype} {tuple(w13.shape)}")
     K, hidden = w13.shape[1], w13.shape[0] // 2
     x2 = x.reshape(-1, K)
@@ -462,20 +462,21 @@ def linear_swiglu(x, w13):
 
 
 def prompt_linear_supported(x, w, bias=None):
-    """Whether prompt_linear takes these operands (bf16 CUDA tensors, K and N multiples of 128, bias bf16 or None)."""
+    """Whether prompt_linear takes these operands (bf16 CUDA tensors, K a multiple of 64 and N of 128, bias bf16 or
+    None)."""
     return (x.is_cuda and w.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2
-            and x.shape[-1] == w.shape[1] and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0
+            and x.shape[-1] == w.shape[1] and w.shape[0] % 128 == 0 and w.shape[1] % 64 == 0
             and (bias is None or (bias.is_cuda and bias.dtype == torch.bfloat16 and bias.shape == (w.shape[0],))))
 
 
 def prompt_linear(x, w, bias=None):
     """bf16(x @ w.T + bias) with fp32 accumulation (smlm_prompt_linear): an nn.Linear of a prompt pass on the
-    matrix cores.  x (..., K) bf16, w (N, K) bf16 with K and N multiples of 128, bias (N,) bf16 or None.  Returns
-    (..., N) bf16."""
+    matrix cores.  x (..., K) bf16, w (N, K) bf16 with K a multiple of 64 and N of 128, bias (N,) bf16 or None.
+    Returns (..., N) bf16."""
     _need_cuda("prompt_linear", x, w, bias)
     if not prompt_linear_supported(x, w, bias):
-        raise ValueError(f"prompt_linear: x (..., K), w (N, K) and bias (N,) must be bf16 with K and N multiples of "
-                         f"128, got {x.dtype} {tuple(x.shape)}, {w.dtype} {tuple(w.shape)}")
+        raise ValueError(f"prompt_linear: x (..., K), w (N, K) and bias (N,) must be bf16 with K a multiple of 64 "
+                         f"and N of 128, got {x.dtype} {tuple(x.shape)}, {w.dtype} {tuple(w.shape)}")
     N, K = w.shape
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
@@ -493,7 +494,7 @@ def prompt_linear(x, w, bias=None):
 
 def linear(mod, x, min_rows=128, max_n=1152):
     """mod(x) for an nn.Linear, through prompt_linear when that applies (bf16 weights and activations, no autograd
-    recording, at least min_rows rows, at most max_n outputs, K and N multiples of 128, bf16 or no autocast): the
+    recording, at least min_rows rows, at most max_n outputs, K a multiple of 64 and N of 128, bf16 or no autocast): the
     same roundings (bf16 out of the fp32 accumulation, the bias added in fp32).  max_n: wider projections keep the
     library GEMM, faster there on MI355X (2048 outputs: 34 against 43 us for 16,384 x 384 rows)."""
     w, b = mod.weight, mod.bias

@@ -253,7 +253,8 @@ def _check_swiglu(got, x, w, what):
 
 
 @pytest.mark.parametrize("M,Kd,H", [(16384, 384, 1024), (1000, 384, 1024), (129, 512, 64), (1, 128, 128),
-                                    (300, 256, 192), (128, 1024, 512), (257, 384, 2048)])
+                                    (300, 256, 192), (128, 1024, 512), (257, 384, 2048), (140, 64, 64),
+                                    (100, 192, 320)])
 def test_linear_swiglu_matches_the_bf16_rule(M, Kd, H):
     """kernels.linear_swiglu against the fp64-product restatement of the w13 projection + SwiGLU roundings
     (_check_swiglu), with partial token tiles (M not a multiple of 128) and one row; the unfused pair (the library
@@ -273,7 +274,7 @@ def test_linear_swiglu_matches_the_bf16_rule(M, Kd, H):
 
 def test_linear_swiglu_strided_input_and_rejects():
     """A (rows, K) view with a row stride larger than K gives the contiguous call's bits; shapes outside the
-    kernel (K not a multiple of 128, hidden not of 64, fp32) are refused with ValueError."""
+    kernel (K not a multiple of 64, hidden not of 64, fp32) are refused with ValueError."""
     note("linear_swiglu strided / rejects")
     g = torch.Generator(device=DEV).manual_seed(5)
     big = torch.randn(300, 512, generator=g, device=DEV).bfloat16()
@@ -281,7 +282,7 @@ def test_linear_swiglu_strided_input_and_rejects():
     view = big[:, :384]
     assert torch.equal(K.linear_swiglu(view, w), K.linear_swiglu(view.contiguous(), w))
     with pytest.raises(ValueError):
-        K.linear_swiglu(big[:, :320], (torch.randn(256, 320, device=DEV)).bfloat16())
+        K.linear_swiglu(big[:, :288], (torch.randn(256, 288, device=DEV)).bfloat16())
     with pytest.raises(ValueError):
         K.linear_swiglu(view, w[:192])
     with pytest.raises(ValueError):
@@ -306,7 +307,8 @@ def _check_linear(got, x, w, bias, what):
 
 @pytest.mark.parametrize("M,Kd,N,with_bias", [(16384, 384, 1152, False), (16384, 384, 384, True),
                                               (16384, 1024, 384, False), (1000, 384, 384, True),
-                                              (129, 512, 128, True), (1, 128, 256, False), (300, 256, 640, True)])
+                                              (129, 512, 128, True), (1, 128, 256, False), (300, 256, 640, True),
+                                              (200, 64, 128, True), (130, 192, 2048, False)])
 def test_prompt_linear_matches_the_fp64_rule(M, Kd, N, with_bias):
     """kernels.prompt_linear against bf16 of the fp64 product (+ bias) (_check_linear), at the model's prompt-pass
     shapes (wqkv, wo / value_proj with its bias, w2) and partial token tiles; the library's F.linear meets the same
@@ -336,7 +338,7 @@ def test_prompt_linear_strided_input_rejects_and_dispatch():
     view = big[:, :384]
     assert torch.equal(K.prompt_linear(view, w), K.prompt_linear(view.contiguous(), w))
     with pytest.raises(ValueError):
-        K.prompt_linear(big[:, :320], torch.randn(256, 320, device=DEV).bfloat16())
+        K.prompt_linear(big[:, :288], torch.randn(256, 288, device=DEV).bfloat16())
     with pytest.raises(ValueError):
         K.prompt_linear(view, w[:192])
     with pytest.raises(ValueError):
