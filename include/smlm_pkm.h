@@ -198,12 +198,16 @@ int smlm_linear_swiglu(const void *x, int64_t x_row_stride, const void *w13, int
 /*
  * A projection of a prompt pass, out = bf16(x W^T + bias) with fp32 accumulation (the bias, if any, added in
  * fp32): replaces the nn.Linear calls self.wqkv(x), self.wo(y) and self.w2(h) of smlm/model.py:92, 107, 118 and
- * swilu_proj / value_proj of smlm/pkm.py:213-224 for bf16 activations and weights.
- *   x (M, K) bf16 rows, w (N, K) bf16 (nn.Linear weight), bias (N,) bf16 or NULL, out (M, N) bf16; K a
- *   multiple of 64, N of 128; 16-byte aligned rows, strides in elements.
+ * swilu_proj / value_proj of smlm/pkm.py:213-224 for bf16 activations and weights.  With scale and shift (fp32,
+ * N each) every output becomes bf16(bf16(x W^T + bias) * scale + shift): query_proj followed by the eval-mode
+ * query BatchNorm of smlm/pkm.py:188-191 (the arithmetic of smlm_affine_bf16) in one launch.
+ *   x (M, K) bf16 rows, w (N, K) bf16 (nn.Linear weight), bias (N,) bf16 or NULL, scale / shift both NULL or both
+ *   given (16-byte aligned), out (M, N) bf16; K a multiple of 64, N of 128; 16-byte aligned rows, strides in
+ *   elements.
  */
 int smlm_prompt_linear(const void *x, int64_t x_row_stride, const void *w, int64_t w_row_stride, const void *bias,
-                       int64_t M, int K, int N, void *out, int64_t out_row_stride, void *stream);
+                       const float *scale, const float *shift, int64_t M, int K, int N, void *out,
+                       int64_t out_row_stride, void *stream);
 
 /*
  * Greedy token choice of the decode loop (smlm/train.py:297-299, `nxt = logits[:, -1:].argmax(-1)`): per row

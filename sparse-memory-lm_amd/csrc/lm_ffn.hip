@@ -5,7 +5,8 @@
 //     of the w13 projection (bf16 output) followed by smlm_swiglu, in one launch that writes the (M, hidden)
 //     activation only (the unfused pair writes and re-reads the (M, 2 hidden) projection);
 //   smlm_prompt_linear: out = bf16(x W^T + bias) for the other projections of a prompt pass (wqkv, wo, w2, the
-//     memory layer's swilu_proj and value_proj), where the library GEMMs' large tiles leave CUs idle.
+//     memory layer's swilu_proj and value_proj), where the library GEMMs' large tiles leave CUs idle, and with an
+//     fp32 per-column scale / shift on the bf16 result the memory query with its eval BatchNorm (smlm/pkm.py:188-191).
 //
 // Workgroup = 4 wavefronts, a tile of 128 tokens x 128 weight rows.  SwiGLU: the 64 weight rows of a and the 64
 // of b, so each lane's a and b accumulators hold the same (token, feature) pairs; wavefront w: tokens 64 (w & 1)
@@ -65,8 +66,9 @@ __device__ __forceinline__ void wait_loads() {
 template <bool SWIGLU>
 __global__ void __launch_bounds__(256)
     prompt_linear_kernel(const uint16_t *__restrict__ x, int64_t x_stride, const uint16_t *__restrict__ w,
-                         int64_t w_stride, const uint16_t *__restrict__ bias, int64_t M, int K, int hidden,
-                         uint16_t *__restrict__ out, int64_t out_stride) {
+                         int64_t w_stride, const uint16_t *__restrict__ bias, const float *__restrict__ scale,
+                         const float *__restrict__ shift, int64_t M, int K, int hidden, uint16_t *__restrict__ out,
+                         int64_t out_stride) {
   constexpr int FEAT = SWIGLU ? kFfnFeat : kFfnRows;   // output features per workgroup
   __shared__ __align__(16) unsigned char stages[2 * kStage];
 
@@ -161,7 +163,8 @@ __global__ void __launch_bounds__(256)
 
   // epilogue through LDS (the stages), stored as whole 128-byte row pieces.  SWIGLU: a, b rounded to bf16 as the
   // projection's output, bf16(silu(a)) as smlm_swiglu, then bf16(s * b), into the workgroup's 128 x 64 tile;
-  // otherwise the projection plus its bias (fp32) rounded to bf16, each wavefront its own 64 x 64 tile.  The
+  // otherwise the projection plus its bias (fp32) rounded to bf16 (with scale / shift: that bf16 value times scale
+  // plus shift, in fp32, rounded again), each wavefront its own 64 x 64 tile.  The
   // roundings use v_cvt_pk_bf16_f32 (round to nearest even: the integer rounding's bits for finite values).
   if constexpr (SWIGLU) {
     constexpr int OROW = kFfnFeat + 8;
@@ -198,16 +201,29 @@ __global__ void __launch_bounds__(256)
     uint16_t *sO = (uint16_t *)stages + wave * 64 * OROW;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const int col = f0 + fh * 64 + i * 16 + 4 * g;
       float bv[4] = {0.f, 0.f, 0.f, 0.f};
       if (bias) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bv[e] = bf16_bits_to_f32(bias[f0 + fh * 64 + i * 16 + 4 * g + e]);
+        for (int e = 0; e < 4; ++e) bv[e] = bf16_bits_to_f32(bias[col + e]);
+      }
+      float4 sc = {1.f, 1.f, 1.f, 1.f}, sh = {0.f, 0.f, 0.f, 0.f};
+      if (scale) {
+        sc = *(const float4 *)(scale + col);
+        sh = *(const float4 *)(shift + col);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = pack_bf16x2(acc[i][j][0] + bv[0], acc[i][j][1] + bv[1]);
-        const uint32_t hi = pack_bf16x2(acc[i][j][2] + bv[2], acc[i][j][3] + bv[3]);
-        *(uint2 *)&sO[(j * 16 + r) * OROW + i * 16 + 4 * g] = uint2{lo, hi};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][e] + bv[e];
+        if (scale) {   // the eval BatchNorm on the bf16 projection: bf16(bf16(v) * scale + shift)
+          v[0] = fmaf(round_bf16_hw(v[0]), sc.x, sh.x);
+          v[1] = fmaf(round_bf16_hw(v[1]), sc.y, sh.y);
+          v[2] = fmaf(round_bf16_hw(v[2]), sc.z, sh.z);
+          v[3] = fmaf(round_bf16_hw(v[3]), sc.w, sh.w);
+        }
+        *(uint2 *)&sO[(j * 16 + r) * OROW + i * 16 + 4 * g] = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
       }
     }
     // each wavefront reads back only what it wrote: no barrier
@@ -229,10 +245,12 @@ namespace {
 // shared checks and launch: N = the kernel's `hidden` (SWIGLU: the activation's width; otherwise the output width)
 template <bool SWIGLU>
 int launch_prompt_linear(const char *what, const void *x, int64_t x_row_stride, const void *w, int64_t w_row_stride,
-                         const void *bias, int64_t M, int K, int N, void *out, int64_t out_row_stride,
-                         void *stream) {
+                         const void *bias, const float *scale, const float *shift, int64_t M, int K, int N, void *out,
+                         int64_t out_row_stride, void *stream) {
   const int feat = SWIGLU ? kFfnFeat : kFfnRows;
   if (!x || !w || !out) return fail(SMLM_EINVAL, "%s: null x, weight or out pointer", what);
+  if ((scale == nullptr) != (shift == nullptr) || ((uintptr_t)scale | (uintptr_t)shift) % 16)
+    return fail(SMLM_EINVAL, "%s: scale and shift must both be given (16-byte aligned fp32) or both be null", what);
   if (M < 0 || K < 1 || N < 1)
     return fail(SMLM_EINVAL, "%s: bad shape M=%lld K=%d N=%d", what, (long long)M, K, N);
   if (K % kFfnKc || N % feat)
@@ -251,8 +269,8 @@ int launch_prompt_linear(const char *what, const void *x, int64_t x_row_stride, 
   const int64_t grid = (ntt + kXcds - 1) / kXcds * kXcds * (N / feat);
   if (grid > 0x7FFFFFFFLL) return fail(SMLM_EUNSUPPORTED, "%s: M=%lld too large", what, (long long)M);
   hipLaunchKernelGGL((prompt_linear_kernel<SWIGLU>), dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t *)x, x_row_stride, (const uint16_t *)w, w_row_stride, (const uint16_t *)bias, M,
-                     K, N, (uint16_t *)out, out_row_stride);
+                     (const uint16_t *)x, x_row_stride, (const uint16_t *)w, w_row_stride, (const uint16_t *)bias, scale,
+                     shift, M, K, N, (uint16_t *)out, out_row_stride);
   return launch_status(what);
 }
 
@@ -261,13 +279,13 @@ int launch_prompt_linear(const char *what, const void *x, int64_t x_row_stride, 
 
 extern "C" int smlm_linear_swiglu(const void *x, int64_t x_row_stride, const void *w13, int64_t w_row_stride,
                                   int64_t M, int K, int hidden, void *out, int64_t out_row_stride, void *stream) {
-  return smlm::launch_prompt_linear<true>("smlm_linear_swiglu", x, x_row_stride, w13, w_row_stride, nullptr, M, K,
-                                          hidden, out, out_row_stride, stream);
+  return smlm::launch_prompt_linear<true>("smlm_linear_swiglu", x, x_row_stride, w13, w_row_stride, nullptr, nullptr,
+                                          nullptr, M, K, hidden, out, out_row_stride, stream);
 }
 
 extern "C" int smlm_prompt_linear(const void *x, int64_t x_row_stride, const void *w, int64_t w_row_stride,
-                                  const void *bias, int64_t M, int K, int N, void *out, int64_t out_row_stride,
-                                  void *stream) {
-  return smlm::launch_prompt_linear<false>("smlm_prompt_linear", x, x_row_stride, w, w_row_stride, bias, M, K, N,
-                                           out, out_row_stride, stream);
+                                  const void *bias, const float *scale, const float *shift, int64_t M, int K, int N,
+                                  void *out, int64_t out_row_stride, void *stream) {
+  return smlm::launch_prompt_linear<false>("smlm_prompt_linear", x, x_row_stride, w, w_row_stride, bias, scale, shift,
+                                           M, K, N, out, out_row_stride, stream);
 }

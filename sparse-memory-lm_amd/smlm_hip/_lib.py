@@ -52,7 +52,7 @@ EXPORTS = {
                                         _p]),
     "smlm_swiglu": (_i, [_p, _i64, _p, _i64, _i, _p]),
     "smlm_linear_swiglu": (_i, [_p, _i64, _p, _i64, _i64, _i, _i, _p, _i64, _p]),
-    "smlm_prompt_linear": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _p, _i64, _p]),
+    "smlm_prompt_linear": (_i, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i, _i, _p, _i64, _p]),
     "smlm_greedy_argmax": (_i, [_p, _i64, _i64, _i, _p, _p, _p, _i64, _i64, _p]),
     "smlm_add_rmsnorm": (_i, [_p, _p, _p, ctypes.c_float, _i64, _i, _p, _p, _p]),
     "smlm_affine_bf16": (_i, [_p, _i64, _p, _p, _i64, _i, _p, _i64, _p]),

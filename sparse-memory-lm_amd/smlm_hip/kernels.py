@@ -469,15 +469,23 @@ def prompt_linear_supported(x, w, bias=None):
             and (bias is None or (bias.is_cuda and bias.dtype == torch.bfloat16 and bias.shape == (w.shape[0],))))
 
 
-def prompt_linear(x, w, bias=None):
+def prompt_linear(x, w, bias=None, scale=None, shift=None):
     """bf16(x @ w.T + bias) with fp32 accumulation (smlm_prompt_linear): an nn.Linear of a prompt pass on the
     matrix cores.  x (..., K) bf16, w (N, K) bf16 with K a multiple of 64 and N of 128, bias (N,) bf16 or None.
-    Returns (..., N) bf16."""
-    _need_cuda("prompt_linear", x, w, bias)
+    scale, shift (N,) fp32 (both or neither): the result is bf16(bf16(x @ w.T + bias) * scale + shift), the eval
+    BatchNorm of the memory query (affine_bf16's arithmetic) in the same launch.  Returns (..., N) bf16."""
+    _need_cuda("prompt_linear", x, w, bias, scale, shift)
     if not prompt_linear_supported(x, w, bias):
         raise ValueError(f"prompt_linear: x (..., K), w (N, K) and bias (N,) must be bf16 with K a multiple of 64 "
                          f"and N of 128, got {x.dtype} {tuple(x.shape)}, {w.dtype} {tuple(w.shape)}")
     N, K = w.shape
+    if (scale is None) != (shift is None):
+        raise ValueError("prompt_linear: give scale and shift together")
+    if scale is not None:
+        if scale.shape != (N,) or shift.shape != (N,) or scale.device != x.device or shift.device != x.device:
+            raise ValueError(f"prompt_linear: scale and shift must be ({N},) tensors on {x.device}")
+        scale = scale.float().contiguous()
+        shift = shift.float().contiguous()
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
         x2 = x2.contiguous()
@@ -486,7 +494,9 @@ def prompt_linear(x, w, bias=None):
     bias = bias.contiguous() if bias is not None else None
     out = torch.empty(x2.shape[0], N, dtype=torch.bfloat16, device=x.device)
     rc = _lib.lib().smlm_prompt_linear(x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0),
-                                       bias.data_ptr() if bias is not None else None, x2.shape[0], K, N,
+                                       bias.data_ptr() if bias is not None else None,
+                                       scale.data_ptr() if scale is not None else None,
+                                       shift.data_ptr() if shift is not None else None, x2.shape[0], K, N,
                                        out.data_ptr(), N, _stream(x))
     _lib.check(rc, "smlm_prompt_linear")
     return out.view(*x.shape[:-1], N)

@@ -227,11 +227,19 @@ class ProductKeyMemory(nn.Module):
         return static_out.clone()
 
     def _query(self, x):
-        q = self.query_proj(x)
         bn = self.query_norm
+        if bn is not None and bn.training:
+            raise NotImplementedError("smlm_hip is inference-only: put the model in eval() mode")
+        w, b = self.query_proj.weight, self.query_proj.bias
+        if (bn is not None and x.is_cuda and x.dtype == torch.bfloat16 and x.numel() >= 128 * x.shape[-1]
+                and kernels.prompt_linear_supported(x, w, b)
+                and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))
+                and not (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != torch.bfloat16)):
+            # prompt passes: the projection and the BatchNorm below in one launch (the same roundings)
+            scale, shift = self._bn_affine()
+            return kernels.prompt_linear(x, w, b, scale, shift)
+        q = self.query_proj(x)
         if bn is not None:
-            if bn.training:
-                raise NotImplementedError("smlm_hip is inference-only: put the model in eval() mode")
             # BatchNorm with the running statistics, in fp32 whatever the parameter dtype: q * scale + shift
             scale, shift = self._bn_affine()
             if q.is_cuda and q.dtype == torch.bfloat16 and q.shape[-1] % 8 == 0 and not (

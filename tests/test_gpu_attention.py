@@ -354,3 +354,24 @@ def test_prompt_linear_strided_input_rejects_and_dispatch():
     assert y.requires_grad
     y.float().sum().backward()
     assert lin.weight.grad is not None and lin.bias.grad is not None
+
+
+@pytest.mark.parametrize("M", [16384, 300])
+def test_prompt_linear_affine_equals_the_two_launches(M):
+    """prompt_linear with scale / shift (the memory query's projection + eval BatchNorm in one launch) gives the
+    bits of the projection followed by affine_bf16 (the BatchNorm kernel of the unfused path), at the config-2
+    query shape (384 -> 4 x 512) and a partial token tile; a scale without a shift is refused."""
+    note(f"prompt_linear affine M={M}")
+    g = torch.Generator(device=DEV).manual_seed(M)
+    x = torch.randn(M, 384, generator=g, device=DEV).bfloat16()
+    w = (torch.randn(2048, 384, generator=g, device=DEV) * 0.05).bfloat16()
+    b = (torch.randn(2048, generator=g, device=DEV) * 0.1).bfloat16()
+    scale = torch.rand(2048, generator=g, device=DEV) + 0.5
+    shift = torch.randn(2048, generator=g, device=DEV) * 0.1
+    fused = K.prompt_linear(x, w, b, scale, shift)
+    assert torch.equal(fused, K.affine_bf16(K.prompt_linear(x, w, b), scale, shift))
+    ref = ((x.double() @ w.double().T + b.double()).float().bfloat16().double() * scale.double()
+           + shift.double()).float().bfloat16().float()
+    assert float((fused.float() != ref).double().mean()) <= 1e-3
+    with pytest.raises(ValueError):
+        K.prompt_linear(x, w, b, scale, None)
