@@ -164,8 +164,8 @@ __global__ void __launch_bounds__(256)
   // epilogue through LDS (the stages), stored as whole 128-byte row pieces.  SWIGLU: a, b rounded to bf16 as the
   // projection's output, bf16(silu(a)) as smlm_swiglu, then bf16(s * b), into the workgroup's 128 x 64 tile;
   // otherwise the projection plus its bias (fp32) rounded to bf16 (with scale / shift: that bf16 value times scale
-  // plus shift, in fp32, rounded again), each wavefront its own 64 x 64 tile.  The
-  // roundings use v_cvt_pk_bf16_f32 (round to nearest even: the integer rounding's bits for finite values).
+  // plus shift, in fp32, rounded again), each wavefront its own 64 x 64 tile.  The roundings use v_cvt_pk_bf16_f32
+  // (round to nearest even: the integer rounding's bits for finite values).
   if constexpr (SWIGLU) {
     constexpr int OROW = kFfnFeat + 8;
     uint16_t *sO = (uint16_t *)stages;
