@@ -27,8 +27,10 @@
 // one column block share an XCD (workgroup id % 8), so its weight rows come from one L2.
 //
 // Latency is what matters at decode sizes, so every global load a lane needs is issued before the first one is
-// used: the weight fragments of the lane's K slice first (they do not depend on the prologue), then the prologue's
-// input rows (addresses clamped into range, no per-row branches), then the arithmetic.  The prologue works on rows
+// used: the prologue's input rows first (addresses clamped into range, no per-row branches; a wavefront's loads
+// retire in issue order, so the prologue can start once they are in), then the weight fragments of the lane's K
+// slice, then the prologue arithmetic, which overlaps the weights' arrival.  EMBED_ARGMAX issues the argmax keys,
+// then the weights, then the embedding rows (whose address needs the keys' reduction).  The prologue works on rows
 // of 16 lanes (DPP reductions inside a row) and writes the normalised bf16 rows to LDS ([tokens][K + 8]), from which
 // the B fragments are read; a PLAIN input is read into registers directly.
 //
