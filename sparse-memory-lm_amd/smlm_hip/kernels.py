@@ -434,8 +434,9 @@ def swiglu(h13):
 
 
 def linear_swiglu_supported(x, w13):
-    """Whether linear_swiglu takes these operands (bf16 CUDA tensors, K a multiple of 64, hidden of 64)."""
-    return (x.is_cuda and w13.is_cuda and x.dtype == torch.bfloat16 and w13.dtype == torch.bfloat16
+    """Whether linear_swiglu takes these operands (bf16 tensors on one CUDA device, K a multiple of 64, hidden of
+    64)."""
+    return (x.is_cuda and w13.device == x.device and x.dtype == torch.bfloat16 and w13.dtype == torch.bfloat16
             and w13.dim() == 2 and x.shape[-1] == w13.shape[1] and w13.shape[0] % 128 == 0
             and w13.shape[1] % 64 == 0)
 
@@ -462,11 +463,12 @@ def linear_swiglu(x, w13):
 
 
 def prompt_linear_supported(x, w, bias=None):
-    """Whether prompt_linear takes these operands (bf16 CUDA tensors, K a multiple of 64 and N of 128, bias bf16 or
-    None)."""
-    return (x.is_cuda and w.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2
-            and x.shape[-1] == w.shape[1] and w.shape[0] % 128 == 0 and w.shape[1] % 64 == 0
-            and (bias is None or (bias.is_cuda and bias.dtype == torch.bfloat16 and bias.shape == (w.shape[0],))))
+    """Whether prompt_linear takes these operands (bf16 tensors on one CUDA device, K a multiple of 64 and N of 128,
+    bias bf16 or None)."""
+    return (x.is_cuda and w.device == x.device and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and w.dim() == 2 and x.shape[-1] == w.shape[1] and w.shape[0] % 128 == 0 and w.shape[1] % 64 == 0
+            and (bias is None or (bias.device == x.device and bias.dtype == torch.bfloat16
+                                  and bias.shape == (w.shape[0],))))
 
 
 def prompt_linear(x, w, bias=None, scale=None, shift=None):
