@@ -330,7 +330,8 @@ def test_prompt_linear_matches_the_fp64_rule(M, Kd, N, with_bias):
 def test_prompt_linear_strided_input_rejects_and_dispatch():
     """A strided (rows, K) view gives the contiguous call's bits; shapes outside the kernel are refused with
     ValueError; kernels.linear takes the kernel for a no-grad bf16 prompt (its bits) and the module itself for few
-    rows or when autograd records (gradients then flow as through nn.Linear)."""
+    rows, when autograd records (gradients then flow as through nn.Linear) and under an autocast that is not bf16 or
+    with fp32 weights."""
     note("prompt_linear strided / rejects / dispatch")
     g = torch.Generator(device=DEV).manual_seed(6)
     big = torch.randn(300, 512, generator=g, device=DEV).bfloat16()
@@ -354,6 +355,14 @@ def test_prompt_linear_strided_input_rejects_and_dispatch():
     assert y.requires_grad
     y.float().sum().backward()
     assert lin.weight.grad is not None and lin.bias.grad is not None
+    # autocast: fp32 weights under bf16 autocast, and fp16 autocast, take the module (autocast's own casts)
+    lin32 = torch.nn.Linear(384, 256, device=DEV)
+    x32 = torch.randn(300, 384, generator=g, device=DEV)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        assert torch.equal(K.linear(lin32, x32), lin32(x32))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        got = K.linear(lin, x3)
+        assert got.dtype == lin(x3).dtype and torch.equal(got, lin(x3))
 
 
 @pytest.mark.parametrize("M", [16384, 300])
