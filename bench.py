@@ -653,7 +653,7 @@ def event_time_each_ms(prep, fn, reps):
 def train_kernels(dev, reps):
     """The training side of the lookup at the reference's training shape (one micro-batch = 4 x 1024 tokens, 4
     heads x top-32 = 128 lookups per token, B-1M fp32 value table 1,048,576 x 384): the row-sparse bag backward on
-    uniform and Zipf(1.1) indices, the lazy row Adam (fp32 / bf16 / int8 moments) on the rows a 32,768-token step
+    uniform and Zipf(1.1) indices (the ordered form, and the atomic form as ms_atomic), the lazy row Adam (fp32 / bf16 / int8 moments) on the rows a 32,768-token step
     (8 micro-batches) reads, and the selection backward at config 2 (8 x 2048 tokens, NK 2048, bf16 scores).
     Algorithmic bytes are the least any implementation moves: every distinct row read or written once."""
     import torch
@@ -671,8 +671,10 @@ def train_kernels(dev, reps):
         distinct = int(torch.unique(idx).numel())
         alg = N * Kl * (8 + 4 + 4) + N * D * 4 + distinct * (3 * D * 4 + 1)
         ms = event_time_ms(lambda: K.bag_backward_rows(gout, idx, w, table, acc, touched), reps)
+        ms_atomic = event_time_ms(lambda: K.bag_backward_rows(gout, idx, w, table, acc, touched, ordered=False),
+                                  reps)
         res[f"bag_backward_{name}"] = {"ms": ms, "distinct_rows": distinct, "alg_bytes": alg,
-                                       "alg_GBps": alg / ms / 1e6}
+                                       "alg_GBps": alg / ms / 1e6, "ms_atomic": ms_atomic}
     del acc, gout, w
     # rows read by a 32,768-token step: 8 micro-batches of uniform lookups
     mask = torch.zeros(rows, dtype=torch.bool, device=dev)

@@ -396,6 +396,20 @@ int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx, const floa
                            const void *table, int table_dtype, int64_t rows, int D, float *acc, uint8_t *touched,
                            float *gw, void *stream);
 
+/*
+ * The same row-sparse bag backward in a fixed order (replaces bag_backward_rows, smlm/kernels.py:34-88, with the
+ * reference's grouping: the lookups sorted by table row, each row's run added in lookup order):
+ *   acc[idx[n,k], :] += w[n,k] * grad_out[n, :], touched[idx[n,k]] = 1, gw[n,k] = grad_out[n, :] . table[idx[n,k], :]
+ * Every accumulator row is written by one wavefront (runs that span several 64-lookup chunks add their per-chunk
+ * partial sums in chunk order), so the result is the same on every call.  The workspace (caller-owned, 256-byte
+ * aligned) holds the sort keys and values, the partial sums and the sort's storage; its size comes from
+ * smlm_bag_backward_sorted_workspace.  Shapes as smlm_bag_backward_rows, with rows < 2^32 - 1 and N*K < 2^31 - 1.
+ */
+int smlm_bag_backward_sorted_workspace(int64_t N, int K, int64_t rows, int D, size_t *bytes);
+int smlm_bag_backward_sorted(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
+                             const void *table, int table_dtype, int64_t rows, int D, float *acc, uint8_t *touched,
+                             float *gw, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Moment storage of smlm_lazy_adam. */
 typedef enum smlm_adam_state {
   SMLM_ADAM_F32 = 0,   /* exp_avg, exp_avg_sq (rows, D) fp32 (smlm/kernels.py:380-433) */

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 F32, BF16, F16, I8, Q4, I32, I64 = range(7)
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, -1, -2, -3
 
-_p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+_p, _i, _i64, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
 # smlm_linear_prologue / smlm_linear_epilogue
 LIN_PLAIN, LIN_RMSNORM, LIN_EMBED_RMSNORM, LIN_RMSNORM_PARTS, LIN_EMBED_ARGMAX = range(5)
@@ -63,6 +63,8 @@ EXPORTS = {
     "smlm_argmax_finish": (_i, [_p, _i64, _i, _i64, _p, _p, _p, _i64, _i64, _i, _p]),
     "smlm_pkm_select_backward": (_i, [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _p]),
     "smlm_bag_backward_rows": (_i, [_p, _p, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _p]),
+    "smlm_bag_backward_sorted_workspace": (_i, [_i64, _i, _i64, _i, _p]),
+    "smlm_bag_backward_sorted": (_i, [_p, _p, _p, _i64, _i, _p, _i, _i64, _i, _p, _p, _p, _p, _sz, _p]),
     "smlm_lazy_adam": (_i, [_p, _p, _p, _p, _p, _i, _p, _p, _p, _i64, _i, _f, _f, _f, _f, _f, _f, _f, _p]),
     "smlm_engram_hash": (_i, [_p, _i64, _i64, _i64, _p, _p, _i, _i, _i, _i64, _p, _p]),
     "smlm_row_gather": (_i, [_p, _i64, _p, _i, _i64, _i, _p, _p]),

@@ -785,10 +785,12 @@ class PKSelect(torch.autograd.Function):
         return ds1, ds2, None
 
 
-def bag_backward_rows(grad_out, indices, weights, table, acc, touched):
+def bag_backward_rows(grad_out, indices, weights, table, acc, touched, ordered=True):
     """Row-sparse bag backward (smlm/kernels.py:90-104): acc[indices[n, k]] += weights[n, k] * grad_out[n] and
     touched[indices] = True, in place; returns the per-sample-weight gradient (N, K) fp32.  table fp32 / bf16
-    (rows, D), acc (rows, D) fp32, touched (rows,) bool; the accumulation uses fp32 atomic adds."""
+    (rows, D), acc (rows, D) fp32, touched (rows,) bool.  ordered (default): the lookups sorted by row and each row
+    written by one wavefront in a fixed order (smlm_bag_backward_sorted: the same result on every call, no
+    atomics); ordered=False: fp32 atomic adds in no fixed order (smlm_bag_backward_rows)."""
     _need_cuda("bag_backward_rows", grad_out, indices, weights, table, acc, touched)
     N, K = indices.shape
     rows, D = table.shape
@@ -803,9 +805,20 @@ def bag_backward_rows(grad_out, indices, weights, table, acc, touched):
     w = weights.float().contiguous()
     table = table.contiguous()
     gw = torch.empty(N, K, dtype=torch.float32, device=g.device)
-    rc = _lib.lib().smlm_bag_backward_rows(g.data_ptr(), idx.data_ptr(), w.data_ptr(), N, K, table.data_ptr(),
-                                           _DT[table.dtype], rows, D, acc.data_ptr(), touched.data_ptr(),
-                                           gw.data_ptr(), _stream(g))
+    L = _lib.lib()
+    if ordered and rows < 0xFFFFFFFF and N * K < 0x7FFFFFFF:
+        size = ctypes.c_size_t(0)
+        _lib.check(L.smlm_bag_backward_sorted_workspace(N, K, rows, D, ctypes.byref(size)),
+                   "smlm_bag_backward_sorted_workspace")
+        ws = torch.empty(max(size.value, 1), dtype=torch.uint8, device=g.device)
+        rc = L.smlm_bag_backward_sorted(g.data_ptr(), idx.data_ptr(), w.data_ptr(), N, K, table.data_ptr(),
+                                        _DT[table.dtype], rows, D, acc.data_ptr(), touched.data_ptr(), gw.data_ptr(),
+                                        ws.data_ptr(), size.value, _stream(g))
+        _lib.check(rc, "smlm_bag_backward_sorted")
+        return gw
+    rc = L.smlm_bag_backward_rows(g.data_ptr(), idx.data_ptr(), w.data_ptr(), N, K, table.data_ptr(),
+                                  _DT[table.dtype], rows, D, acc.data_ptr(), touched.data_ptr(), gw.data_ptr(),
+                                  _stream(g))
     _lib.check(rc, "smlm_bag_backward_rows")
     return gw
 

@@ -5,8 +5,9 @@ Adam (smlm_lazy_adam) with fp32, bf16 and int8 moments.
 Bars: the lazy Adam is bit-exact (same operation order, IEEE division and square root, no fused multiply-add).
 The selection backward is bit-exact up to the softmax backward's wavefront sum (the oracle sums w * g_w in
 numpy's order): bf16 outputs within one bf16 ulp and fp32 outputs within 1e-5 relative, and every element whose
-sub-key is not selected is exactly zero.  The bag backward's accumulator takes fp32 atomic adds in no fixed order:
-within 1e-5 of the summed magnitudes; the per-sample-weight gradient within 1e-5; the flags exact."""
+sub-key is not selected is exactly zero.  The bag backward's accumulator (a fixed order in the default, sorted form;
+fp32 atomic adds in no fixed order in the other): within 1e-5 of the summed magnitudes; the per-sample-weight
+gradient within 1e-5; the flags exact; the sorted form gives the same bits on every call."""
 import numpy as np
 import pytest
 import torch
@@ -89,8 +90,9 @@ def test_pkselect_autograd_matches_oracle():
                                                (64, 128, 384, 3, torch.float32),
                                                # K = 1: 64 tokens per workgroup; K > 512: one token per workgroup
                                                (700, 1, 64, 50, torch.float32), (3, 600, 64, 500, torch.bfloat16)])
-def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype):
-    note(f"bag backward N={N} K={K} D={D} rows={rows} {tdtype}")
+@pytest.mark.parametrize("ordered", [True, False])
+def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype, ordered):
+    note(f"bag backward N={N} K={K} D={D} rows={rows} {tdtype} ordered={ordered}")
     g = torch.Generator().manual_seed(N + K + D)
     idx = torch.randint(0, rows, (N, K), generator=g)
     idx[0, : min(K, 5)] = 1                                # a row read several times in a bag and across bags
@@ -102,7 +104,7 @@ def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype):
     t0 = torch.zeros(rows, dtype=torch.bool)
     t0[rows - 1] = True
     acc, touched = acc0.to(DEV), t0.to(DEV)
-    gw = KR.bag_backward_rows(G.to(DEV), idx.to(DEV), w.to(DEV), table.to(DEV), acc, touched)
+    gw = KR.bag_backward_rows(G.to(DEV), idx.to(DEV), w.to(DEV), table.to(DEV), acc, touched, ordered=ordered)
     torch.cuda.synchronize()
     rgw, racc, rt = T.bag_backward_rows(G.numpy(), idx.numpy(), w.numpy(), table.float().numpy(), acc0.numpy(),
                                         t0.numpy())
@@ -116,18 +118,80 @@ def test_bag_backward_rows_matches_oracle(N, K, D, rows, tdtype):
     np.testing.assert_array_equal(touched.cpu().numpy(), rt)
 
 
-def test_bag_backward_rows_index_outside_table():
-    note("bag backward: index outside the table")
+@pytest.mark.parametrize("ordered", [True, False])
+def test_bag_backward_rows_index_outside_table(ordered):
+    note(f"bag backward: index outside the table, ordered={ordered}")
     N, K, D, rows = 2, 3, 64, 10
     idx = torch.tensor([[0, 10, 2], [3, -1, 3]])
     acc = torch.zeros(rows, D, device=DEV)
     touched = torch.zeros(rows, dtype=torch.bool, device=DEV)
     gw = KR.bag_backward_rows(torch.ones(N, D, device=DEV), idx.to(DEV), torch.ones(N, K, device=DEV),
-                             torch.ones(rows, D, device=DEV), acc, touched)
+                             torch.ones(rows, D, device=DEV), acc, touched, ordered=ordered)
     gw = gw.cpu()
     assert torch.isnan(gw[0, 1]) and torch.isnan(gw[1, 1]) and not torch.isnan(gw[:, [0, 2]]).any()
     assert touched.cpu().nonzero().view(-1).tolist() == [0, 2, 3]
     np.testing.assert_array_equal(acc.cpu().sum(1).numpy(), [64, 0, 64, 128, 0, 0, 0, 0, 0, 0])
+
+
+@pytest.mark.parametrize("N,K,rows,hot", [(256, 128, 1000, 0.5), (1, 5, 10, 0.0), (1, 64, 3, 0.0), (5, 13, 7, 0.9),
+                                          (1, 65, 2, 0.0), (300, 1, 40, 0.0)])
+def test_bag_backward_ordered_is_repeatable_and_matches_oracle(N, K, rows, hot):
+    """The ordered bag backward gives the same bits on every call (each accumulator row has one writer, runs across
+    64-lookup chunks add their partial sums in chunk order), matches the oracle, and covers a row read by half of
+    all lookups (its run spans hundreds of chunks), lookups fewer than a chunk, exactly one chunk and one more."""
+    note(f"ordered bag backward N={N} K={K} rows={rows} hot={hot}")
+    D = 384
+    g = torch.Generator().manual_seed(N * K + rows)
+    idx = torch.randint(0, rows, (N, K), generator=g)
+    idx[torch.rand(N, K, generator=g) < hot] = 7 % rows
+    w = torch.rand(N, K, generator=g)
+    table = torch.randn(rows, D, generator=g)
+    G = torch.randn(N, D, generator=g)
+    acc0 = torch.randn(rows, D, generator=g) * 0.1
+    outs = []
+    for _ in range(2):
+        acc, touched = acc0.to(DEV), torch.zeros(rows, dtype=torch.bool, device=DEV)
+        gw = KR.bag_backward_rows(G.to(DEV), idx.to(DEV), w.to(DEV), table.to(DEV), acc, touched)
+        outs.append((gw.cpu(), acc.cpu(), touched.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][2], outs[1][2])
+    rgw, racc, rt = T.bag_backward_rows(G.numpy(), idx.numpy(), w.numpy(), table.numpy(), acc0.numpy(),
+                                        np.zeros(rows, dtype=bool))
+    gw, acc, touched = (t.numpy() for t in outs[0])
+    mag_gw = np.abs(G.numpy()) @ np.abs(table.numpy()).T
+    np.testing.assert_array_less(np.abs(gw - rgw), 1e-5 * np.take_along_axis(mag_gw, idx.numpy(), 1) + 1e-6)
+    mag = np.zeros((rows, D))
+    np.add.at(mag, idx.reshape(-1).numpy(), (np.abs(w.numpy())[..., None] * np.abs(G.numpy())[:, None]).reshape(
+        N * K, D))
+    np.testing.assert_array_less(np.abs(acc - racc), 1e-5 * (mag + np.abs(acc0.numpy())) + 1e-7)
+    np.testing.assert_array_equal(touched, rt)
+
+
+def test_bag_backward_sorted_workspace_checks():
+    """The workspace query and its use: a too-small or unaligned workspace is refused before any launch."""
+    note("ordered bag backward workspace checks")
+    import ctypes
+    from smlm_hip import _lib
+    L = _lib.lib()
+    size = ctypes.c_size_t(0)
+    assert L.smlm_bag_backward_sorted_workspace(4, 8, 100, 64, ctypes.byref(size)) == _lib.OK and size.value > 0
+    assert L.smlm_bag_backward_sorted_workspace(4, 8, 100, 600, ctypes.byref(size)) == _lib.EUNSUPPORTED
+    g = torch.zeros(4, 64, device=DEV)
+    idx = torch.zeros(4, 8, dtype=torch.int64, device=DEV)
+    w = torch.zeros(4, 8, device=DEV)
+    table = torch.zeros(100, 64, device=DEV)
+    acc = torch.zeros(100, 64, device=DEV)
+    touched = torch.zeros(100, dtype=torch.uint8, device=DEV)
+    gw = torch.empty(4, 8, device=DEV)
+    L.smlm_bag_backward_sorted_workspace(4, 8, 100, 64, ctypes.byref(size))
+    ws = torch.empty(size.value + 256, dtype=torch.uint8, device=DEV)
+    args = (g.data_ptr(), idx.data_ptr(), w.data_ptr(), 4, 8, table.data_ptr(), _lib.F32, 100, 64, acc.data_ptr(),
+            touched.data_ptr(), gw.data_ptr())
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.smlm_bag_backward_sorted(*args, ws.data_ptr(), size.value - 1, s) == _lib.EINVAL
+    assert L.smlm_bag_backward_sorted(*args, ws.data_ptr() + 16, size.value, s) == _lib.EINVAL
+    assert L.smlm_bag_backward_sorted(*args, ws.data_ptr(), size.value, s) == _lib.OK
+    torch.cuda.synchronize()
 
 
 def _adam_case(rows, D, seed):
