@@ -28,6 +28,10 @@ constexpr int kChunksPerBlock = kRunThreads / kWave;
 constexpr int kSegsInFlight = 4;                    // segments whose rows are loaded together
 constexpr int kLookAhead = 8;                       // lookups of a segment whose gradient rows are loaded together
 constexpr int kMaxDSorted = 512;
+// the stable radix sort in onesweep passes (one per 8 key bits) at every size: rocPRIM's default sorts fewer than
+// 2^20 items by block sort + merge passes (18 launches at 524,288 lookups, ~125 us against ~3 radix passes)
+using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                              rocprim::default_config, 0>;
 
 template <bool F32>
 __device__ __forceinline__ float table_value(const void *table, int64_t i) {
@@ -273,7 +277,7 @@ int sorted_layout(int64_t L, int64_t rows, int D, SortedLayout &lay) {
   lay.cross = lay.partial + align256(nchunks * 2 * (size_t)D * 4);
   lay.sort_tmp = lay.cross + align256(nchunks);
   size_t bytes = 0;
-  const hipError_t e = rocprim::radix_sort_pairs(nullptr, bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
+  const hipError_t e = rocprim::radix_sort_pairs<SortConfig>(nullptr, bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
                                                  (const uint32_t *)nullptr, (uint32_t *)nullptr, (unsigned)L, 0,
                                                  end_bit_for((uint32_t)rows), (hipStream_t)0);
   if (e != hipSuccess) return fail(SMLM_EHIP, "smlm_bag_backward_sorted: sort storage query: %s", hipGetErrorString(e));
@@ -357,7 +361,7 @@ extern "C" int smlm_bag_backward_sorted(const float *grad_out, const int64_t *id
   hipLaunchKernelGGL(keys_kernel, dim3((unsigned)((L + 255) / 256)), dim3(256), 0, s, idx, L, (uint32_t)rows,
                      keys_in, vals_in);
   size_t sort_bytes = lay.sort_bytes;
-  const hipError_t e = rocprim::radix_sort_pairs(ws + lay.sort_tmp, sort_bytes, keys_in, keys, vals_in, vals,
+  const hipError_t e = rocprim::radix_sort_pairs<SortConfig>(ws + lay.sort_tmp, sort_bytes, keys_in, keys, vals_in, vals,
                                                  (unsigned)L, 0, end_bit_for((uint32_t)rows), s);
   if (e != hipSuccess) return fail(SMLM_EHIP, "smlm_bag_backward_sorted: sort: %s", hipGetErrorString(e));
   const bool f32 = table_dtype == SMLM_F32;
