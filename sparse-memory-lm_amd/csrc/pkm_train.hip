@@ -14,6 +14,8 @@
 //                            take hardware fp32 atomic adds (lane l owns columns l, l + 64, ...: each atomic
 //                            instruction covers 256 contiguous bytes), so rows read by several lookups need no
 //                            sort (the reference sorts the lookups and adds runs, with atomics at the borders).
+//                            This is the atomic form; the ordered form, sorted by row with one writer per row
+//                            and a fixed order of additions, is smlm_bag_backward_sorted (pkm_train_sorted.hip).
 //   lazy_adam_kernel         the lazy Adam step of LazyRowAdam on the rows flagged in `touched` (smlm/kernels.py:
 //                            380-515): fp32 moments, or bf16 moments, or int8 companded moments with fp32 row
 //                            scales; afterwards the rows' accumulator is zero and their flag cleared.  One
