@@ -576,7 +576,8 @@ def engram_lookup(dev, reps):
             touched = torch.zeros(table.shape[0], dtype=torch.bool, device=dev)
             grad = torch.randn(M, 24, generator=g, device=dev)
             flat, ones = rows.reshape(-1, 1), torch.ones(M, 1, device=dev)
-            ms_b = event_time_ms(lambda: K.bag_backward_rows(grad, flat, ones, table, acc, touched), reps)
+            ms_b = event_time_ms(lambda: K.bag_backward_rows(grad, flat, ones, table, acc, touched, ordered=False),
+                                 reps)   # the form EngramMemory's backward uses
             distinct = int(torch.unique(flat).numel())
             alg_b = M * 16 + M * 24 * 4 + distinct * (3 * 24 * 4 + 1)
             res["backward_fp32"] = {"ms": ms_b, "distinct_rows": distinct, "alg_GBps": alg_b / ms_b / 1e6}
