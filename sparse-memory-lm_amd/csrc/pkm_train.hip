@@ -4,9 +4,9 @@
 //   select_backward_kernel   PKSelect.backward (smlm/kernels.py:253-266): the softmax backward of each head's knn
 //                            weights plus the scores' own gradient, rounded to the scores' dtype, scattered into
 //                            dense (N, H, NK) gradients of both halves (sums per sub-key in fp32, in selection
-//                            order, rounded once).  One wavefront per (token, head): the two dense rows are first
-//                            written as zeros with 16-byte stores, the wavefront waits until they are acknowledged,
-//                            then the lanes holding the first occurrence of a sub-key write its merged sum.
+//                            order, rounded once).  One wavefront per (token, head): the two dense rows are
+//                            composed in the wavefront's LDS, 64 sixteen-byte chunks at a time (zeros, then the
+//                            merged sum of each selected sub-key), and each chunk is written to memory once.
 //   bag_backward_kernel      the row-sparse bag backward (smlm/kernels.py:1-104, smlm/sparse_values.py:94-113):
 //                            acc[idx[n,k]] += w[n,k] * g[n], touched[idx[n,k]] = 1, and the per-sample-weight
 //                            gradient gw[n,k] = g[n] . table[idx[n,k]].  One workgroup per token, a wavefront per
@@ -97,33 +97,8 @@ __global__ void __launch_bounds__(kTrainThreads)
     i2[r] = (int)(ix[r] % NK);
   }
 
-  // 1. both dense rows as zeros: 16 bytes per store where rows are whole 16-byte chunks, else element by element
-  constexpr int EPV = F32 ? 4 : 8;            // elements per 16 bytes
-  char *r1 = (char *)ds1 + row * (int64_t)NK * (F32 ? 4 : 2);
-  char *r2 = (char *)ds2 + row * (int64_t)NK * (F32 ? 4 : 2);
-  if (NK % EPV == 0) {
-    typedef unsigned u32x4z __attribute__((ext_vector_type(4)));
-    const int chunks = NK / EPV;
-    for (int c = lane; c < chunks; c += kWave) {  // streamed to memory (non-temporal): 2 x NK per row, written once
-      __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r1 + (int64_t)c * 16));
-      __builtin_nontemporal_store(u32x4z{0u, 0u, 0u, 0u}, (u32x4z *)(r2 + (int64_t)c * 16));
-    }
-  } else {
-    for (int k = lane; k < NK; k += kWave) {
-      if constexpr (F32) {
-        ((float *)r1)[k] = 0.f;
-        ((float *)r2)[k] = 0.f;
-      } else {
-        ((uint16_t *)r1)[k] = 0;
-        ((uint16_t *)r2)[k] = 0;
-      }
-    }
-  }
-  // every zero store acknowledged before the first value store: the value then lands after the zero
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __builtin_amdgcn_s_waitcnt(0);
-
-  // 2. per sub-key: the sum of its selected pairs' gradients in selection order, by its first occurrence
+  // per sub-key: the sum of its selected pairs' gradients in selection order (every occurrence holds the full sum;
+  // the first occurrence of each sub-key is the one that writes it)
   float sum1[2] = {0.f, 0.f}, sum2[2] = {0.f, 0.f};
   bool first1[2] = {have[0], have[1]}, first2[2] = {have[0], have[1]};
   for (int j = 0; j < knn; ++j) {
@@ -145,17 +120,69 @@ __global__ void __launch_bounds__(kTrainThreads)
       }
     }
   }
+  // an index outside [0, NK^2) (not a selection's output) writes nothing
+  bool w1[2], w2[2];
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    // an index outside [0, NK^2) (not a selection's output) writes nothing
-    const bool w1 = first1[r] && (unsigned)i1[r] < (unsigned)NK && ix[r] >= 0;
-    const bool w2 = first2[r] && (unsigned)i2[r] < (unsigned)NK && ix[r] >= 0;
+    w1[r] = first1[r] && (unsigned)i1[r] < (unsigned)NK && ix[r] >= 0;
+    w2[r] = first2[r] && (unsigned)i2[r] < (unsigned)NK && ix[r] >= 0;
+  }
+  constexpr int EPV = F32 ? 4 : 8;            // elements per 16 bytes
+  char *r1 = (char *)ds1 + row * (int64_t)NK * (F32 ? 4 : 2);
+  char *r2 = (char *)ds2 + row * (int64_t)NK * (F32 ? 4 : 2);
+  if (NK % EPV == 0) {
+    // each 16-byte chunk of both rows written once, with the merged sums of its selected sub-keys in place: the rows
+    // are composed in this wavefront's LDS, 64 chunks of each at a time (zeros, then the sums), and streamed to
+    // memory (non-temporal, 2 x NK per row, written once)
+    typedef unsigned u32x4z __attribute__((ext_vector_type(4)));
+    __shared__ u32x4z stage[kTrainWaves][2][kWave];
+    u32x4z *st1 = stage[threadIdx.x / kWave][0], *st2 = stage[threadIdx.x / kWave][1];
+    const int chunks = NK / EPV;
+    for (int cb = 0; cb < chunks; cb += kWave) {
+      st1[lane] = u32x4z{0u, 0u, 0u, 0u};
+      st2[lane] = u32x4z{0u, 0u, 0u, 0u};
+      wave_lds_sync();
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e1 = i1[r] - cb * EPV, e2 = i2[r] - cb * EPV;  // element within this pass's 64 chunks
+        if (w1[r] && (unsigned)e1 < (unsigned)(kWave * EPV)) {
+          if constexpr (F32) ((float *)st1)[e1] = sum1[r];
+          else ((uint16_t *)st1)[e1] = (uint16_t)bf16_bits_rtne(sum1[r]);
+        }
+        if (w2[r] && (unsigned)e2 < (unsigned)(kWave * EPV)) {
+          if constexpr (F32) ((float *)st2)[e2] = sum2[r];
+          else ((uint16_t *)st2)[e2] = (uint16_t)bf16_bits_rtne(sum2[r]);
+        }
+      }
+      wave_lds_sync();
+      if (cb + lane < chunks) {
+        __builtin_nontemporal_store(st1[lane], (u32x4z *)(r1 + (int64_t)(cb + lane) * 16));
+        __builtin_nontemporal_store(st2[lane], (u32x4z *)(r2 + (int64_t)(cb + lane) * 16));
+      }
+      wave_lds_sync();
+    }
+    return;
+  }
+  // rows that are not whole 16-byte chunks: zeros element by element, every zero store acknowledged, then the sums
+  for (int k = lane; k < NK; k += kWave) {
     if constexpr (F32) {
-      if (w1) ((float *)r1)[i1[r]] = sum1[r];
-      if (w2) ((float *)r2)[i2[r]] = sum2[r];
+      ((float *)r1)[k] = 0.f;
+      ((float *)r2)[k] = 0.f;
     } else {
-      if (w1) ((uint16_t *)r1)[i1[r]] = (uint16_t)bf16_bits_rtne(sum1[r]);
-      if (w2) ((uint16_t *)r2)[i2[r]] = (uint16_t)bf16_bits_rtne(sum2[r]);
+      ((uint16_t *)r1)[k] = 0;
+      ((uint16_t *)r2)[k] = 0;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if constexpr (F32) {
+      if (w1[r]) ((float *)r1)[i1[r]] = sum1[r];
+      if (w2[r]) ((float *)r2)[i2[r]] = sum2[r];
+    } else {
+      if (w1[r]) ((uint16_t *)r1)[i1[r]] = (uint16_t)bf16_bits_rtne(sum1[r]);
+      if (w2[r]) ((uint16_t *)r2)[i2[r]] = (uint16_t)bf16_bits_rtne(sum2[r]);
     }
   }
 }

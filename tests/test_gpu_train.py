@@ -33,8 +33,11 @@ def _ulp_bf16(x):
     (3, 2, 64, 64, torch.float32, True, True),
     (7, 3, 8, 8, torch.bfloat16, True, False),
     (4, 4, 1024, 16, torch.float32, False, True),
-    # shapes of the reference's torch path: non-power-of-two n_keys (element-wise zero rows) and knn, knn > 64
+    # shapes of the reference's torch path: non-power-of-two n_keys and knn, knn > 64
     (6, 3, 24, 4, torch.bfloat16, True, True),
+    # rows that are not whole 16-byte chunks (zeros element by element, then the sums)
+    (5, 2, 30, 6, torch.bfloat16, True, True),
+    (4, 3, 50, 10, torch.float32, True, True),
     (5, 2, 1000, 5, torch.float32, True, True),
     (3, 4, 4096, 128, torch.bfloat16, True, True),
     (4, 2, 100, 100, torch.float32, False, True),
