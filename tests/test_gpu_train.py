@@ -225,7 +225,7 @@ def test_lazy_adam_fp32_bit_exact(rows, D):
 
 
 @pytest.mark.parametrize("state,rows,D", [("bf16", 200, 384), ("int8", 200, 384), ("int8", 33, 100),
-                                          ("bf16", 30, 130), ("int8", 30, 98), ("int8", 40, 512)])
+                                          ("bf16", 30, 130), ("int8", 30, 98), ("int8", 40, 512), ("int8", 50, 300)])
 def test_lazy_adam_lowmem_bit_exact(state, rows, D):
     note(f"lazy adam {state} rows={rows} D={D}")
     rng, p = _adam_case(rows, D, 7 * rows + D)

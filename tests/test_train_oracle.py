@@ -161,3 +161,34 @@ def test_lazy_adam_int8_first_step_codes():
         assert np.all(np.abs(np.sqrt(np.sqrt(v_dec)) - np.sqrt(np.sqrt(vr[r]))) <= 1.0 / 255 * vs[r])
     np.testing.assert_array_equal(p1[~touched], p[~touched])
     assert not mq[~touched].any() and not acc1[touched].any() and not t1.any()
+
+
+def _rn32(x):
+    """The float32 nearest to the rational x, ties to even (x zero or in the normal range)."""
+    from fractions import Fraction
+    if x == 0:
+        return np.float32(0)
+    c = np.float32(float(x))
+    cands = [np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))]
+    return min(cands, key=lambda t: (abs(Fraction(float(t)) - x), int(np.float32(t).view(np.uint32)) & 1))
+
+
+def test_code_division_by_corrected_reciprocal_is_the_ieee_quotient():
+    """The int8 lazy Adam decodes its codes with q = c * RN(1/DEN), e = fma(-q, DEN, c), q' = fma(e, RN(1/DEN), q)
+    instead of an IEEE division (csrc/pkm_train.hip: div_code).  Every code of both moments, in exact rational
+    arithmetic with one rounding per operation, against the correctly rounded c / DEN."""
+    from fractions import Fraction
+    for den, lo, hi in ((127, -127, 127), (255, 0, 255)):
+        r = _rn32(Fraction(1, den))
+        assert r == np.float32(1) / np.float32(den)
+        for ci in range(lo, hi + 1):
+            c = Fraction(ci)
+            q = _rn32(c * Fraction(float(r)))
+            e = _rn32(c - Fraction(float(q)) * den)
+            q2 = _rn32(Fraction(float(e)) * Fraction(float(r)) + Fraction(float(q)))
+            assert q2 == _rn32(Fraction(ci, den)) == np.float32(ci) / np.float32(den), (den, ci)
+    # a plain product with the reciprocal is not enough: it differs for some codes of each moment
+    c = np.arange(-127, 128, dtype=np.float32)
+    assert np.any(c * (np.float32(1) / np.float32(127)) != c / np.float32(127))
+    c = np.arange(0, 256, dtype=np.float32)
+    assert np.any(c * (np.float32(1) / np.float32(255)) != c / np.float32(255))
