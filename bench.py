@@ -576,11 +576,16 @@ def engram_lookup(dev, reps):
             touched = torch.zeros(table.shape[0], dtype=torch.bool, device=dev)
             grad = torch.randn(M, 24, generator=g, device=dev)
             flat, ones = rows.reshape(-1, 1), torch.ones(M, 1, device=dev)
-            ms_b = event_time_ms(lambda: K.bag_backward_rows(grad, flat, ones, table, acc, touched, ordered=False),
-                                 reps)   # the form EngramMemory's backward uses
+            # the form EngramMemory's backward uses: unit weights, no weight gradient, no table read
+            ms_b = event_time_ms(lambda: K.bag_backward_rows(grad, flat, None, table, acc, touched, ordered=False,
+                                                             weight_grad=False), reps)
+            # the general atomic bag backward on the same lookups (weights of 1 read, weight gradient computed)
+            ms_w = event_time_ms(lambda: K.bag_backward_rows(grad, flat, ones, table, acc, touched, ordered=False),
+                                 reps)
             distinct = int(torch.unique(flat).numel())
-            alg_b = M * 16 + M * 24 * 4 + distinct * (3 * 24 * 4 + 1)
-            res["backward_fp32"] = {"ms": ms_b, "distinct_rows": distinct, "alg_GBps": alg_b / ms_b / 1e6}
+            alg_b = M * 8 + M * 24 * 4 + distinct * (2 * 24 * 4 + 1)
+            res["backward_fp32"] = {"ms": ms_b, "distinct_rows": distinct, "alg_bytes": alg_b,
+                                    "alg_GBps": alg_b / ms_b / 1e6, "ms_with_weight_grad": ms_w}
             del acc, touched, grad
         del table
     torch.cuda.empty_cache()

@@ -391,6 +391,10 @@ int smlm_pkm_select_backward(const int64_t *idx, const float *w, const void *g_s
  *   grad_out (N, D) fp32; idx (N, K) int64; w (N, K) fp32; table (rows, D) SMLM_F32 or SMLM_BF16; acc (rows, D)
  *   fp32; touched (rows,) uint8; gw (N, K) fp32.  D <= 512.  An index outside [0, rows) adds nothing and gives a
  *   NaN gw.
+ * gw NULL: the per-sample-weight gradient is not wanted (the reference computes it and its caller discards it when
+ *   the weights do not train: the unit weights of the Engram lookups, smlm/engram.py:118); then w may be NULL (unit
+ *   weights), table and table_dtype are not read, and the lookups are scattered with one thread per element and no
+ *   sort.  With gw given, w and table are required.
  */
 int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
                            const void *table, int table_dtype, int64_t rows, int D, float *acc, uint8_t *touched,

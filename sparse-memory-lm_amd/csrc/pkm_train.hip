@@ -22,6 +22,8 @@
 //                            wavefront per row; untouched rows cost one byte read.  No multiply-add contraction in
 //                            this file: the update is evaluated in the reference's operation order (its compact
 //                            kernel is compiled with fp fusion off), with IEEE division and square root.
+#include <type_traits>
+
 #include "pkm_common.h"
 
 #pragma clang fp contract(off)
@@ -592,6 +594,42 @@ __global__ void __launch_bounds__(kTrainThreads)
   }
 }
 
+// The bag backward without the per-sample-weight gradient (its caller discards it when the weights do not train: the
+// unit weights of the Engram lookups, smlm/engram.py:118): acc[idx[i]] += w[i] * g[i / K] (w[i] = 1 when w is null)
+// and touched[idx[i]] = 1 for the L = N * K lookups i, in no fixed order (fp32 atomic adds), with no table read and
+// no sort.  One thread per element, so the lanes of an atomic instruction cover contiguous columns of 64 / D rows
+// (Engram: 24-column rows, 2.7 rows per instruction).  Timing probe at the Engram shape (262,144 lookups of 24 into
+// 8.4M rows): 31 us this way, 109 us with 16 bytes per lane (each instruction then spreads its lanes over 10 rows at
+// a 16-byte stride, and four instructions revisit each row).  WIDE: 64-bit element indices.  An index outside
+// [0, rows) adds nothing.
+template <bool WIDE>
+__global__ void __launch_bounds__(kTrainThreads)
+    row_scatter_kernel(const float *__restrict__ g, const int64_t *__restrict__ idx, const float *__restrict__ w,
+                       int64_t L, int K, int D, int64_t rows, float *__restrict__ acc, uint8_t *__restrict__ touched) {
+  typedef typename std::conditional<WIDE, uint64_t, uint32_t>::type index_t;
+  const index_t total = (index_t)(L * D), stride = (index_t)gridDim.x * kTrainThreads;
+  for (index_t t = (index_t)blockIdx.x * kTrainThreads + threadIdx.x; t < total; t += stride) {
+    const index_t i = t / (index_t)D;
+    const int d = (int)(t - i * (index_t)D);
+    const int64_t r = idx[i];
+    if (r < 0 || r >= rows) continue;
+    const float v = g[(int64_t)(K == 1 ? i : i / (index_t)K) * D + d];
+    unsafeAtomicAdd(acc + r * D + d, w ? w[i] * v : v);
+    if (d == 0) touched[r] = 1;
+  }
+}
+
+void launch_row_scatter(const float *g, const int64_t *idx, const float *w, int64_t L, int K, int D, int64_t rows,
+                        float *acc, uint8_t *touched, hipStream_t stream) {
+  const int64_t total = L * D;
+  const dim3 grid((unsigned)std::min<int64_t>((total + kTrainThreads - 1) / kTrainThreads, 1 << 20)),
+      block(kTrainThreads);
+  if (total + (int64_t)grid.x * kTrainThreads <= (int64_t)UINT32_MAX)  // t + stride stays within 32 bits
+    hipLaunchKernelGGL((row_scatter_kernel<false>), grid, block, 0, stream, g, idx, w, L, K, D, rows, acc, touched);
+  else
+    hipLaunchKernelGGL((row_scatter_kernel<true>), grid, block, 0, stream, g, idx, w, L, K, D, rows, acc, touched);
+}
+
 template <int CPL>
 void launch_bag_backward(const float *grad_out, const int64_t *idx, const float *w, int64_t N, int K,
                          const void *table, bool f32, int64_t rows, int D, float *acc, uint8_t *touched, float *gw,
@@ -674,8 +712,16 @@ extern "C" int smlm_bag_backward_rows(const float *grad_out, const int64_t *idx,
                                       const void *table, int table_dtype, int64_t rows, int D, float *acc,
                                       uint8_t *touched, float *gw, void *stream) {
   using namespace smlm;
-  if (!grad_out || !idx || !w || !table || !acc || !touched || !gw)
-    return fail(SMLM_EINVAL, "smlm_bag_backward_rows: null pointer argument");
+  if (!grad_out || !idx || !acc || !touched || (gw && (!w || !table)))
+    return fail(SMLM_EINVAL, "smlm_bag_backward_rows: null pointer argument (w and table are needed with gw)");
+  if (!gw) {  // no per-sample-weight gradient: scatter the lookups, no table read
+    if (N < 0 || K < 1 || rows < 1 || D < 1 || D > kMaxD || (N > 0 && K > INT64_MAX / D / N))
+      return fail(SMLM_EUNSUPPORTED, "smlm_bag_backward_rows: N=%lld K=%d rows=%lld D=%d (1 <= D <= %d)",
+                  (long long)N, K, (long long)rows, D, kMaxD);
+    if (N == 0) return SMLM_OK;
+    launch_row_scatter(grad_out, idx, w, N * K, K, D, rows, acc, touched, (hipStream_t)stream);
+    return launch_status("smlm_bag_backward_rows");
+  }
   if (table_dtype != SMLM_F32 && table_dtype != SMLM_BF16)
     return fail(SMLM_EINVAL, "smlm_bag_backward_rows: the table must be SMLM_F32 or SMLM_BF16, got %d", table_dtype);
   if (N < 0 || N > 0x7FFFFFFFLL || K < 1 || rows < 1 || rows >= (1LL << (63 - kSortShift)) || D < 1 || D > kMaxD)

@@ -785,27 +785,38 @@ class PKSelect(torch.autograd.Function):
         return ds1, ds2, None
 
 
-def bag_backward_rows(grad_out, indices, weights, table, acc, touched, ordered=True):
+def bag_backward_rows(grad_out, indices, weights, table, acc, touched, ordered=True, weight_grad=True):
     """Row-sparse bag backward (smlm/kernels.py:90-104): acc[indices[n, k]] += weights[n, k] * grad_out[n] and
     touched[indices] = True, in place; returns the per-sample-weight gradient (N, K) fp32.  table fp32 / bf16
     (rows, D), acc (rows, D) fp32, touched (rows,) bool.  ordered (default): the lookups sorted by row and each row
     written by one wavefront in a fixed order (smlm_bag_backward_sorted: the same result on every call, no
-    atomics); ordered=False: fp32 atomic adds in no fixed order (smlm_bag_backward_rows)."""
-    _need_cuda("bag_backward_rows", grad_out, indices, weights, table, acc, touched)
+    atomics); ordered=False: fp32 atomic adds in no fixed order (smlm_bag_backward_rows).
+    weight_grad=False with ordered=False: the per-sample-weight gradient is not computed (returns None) and the
+    table is not read; weights may then be None (unit weights, the Engram lookups of smlm/engram.py:118).  The
+    lookups are scattered with fp32 atomic adds and no sort (smlm_bag_backward_rows with gw NULL)."""
+    scatter = not weight_grad and not ordered
+    if weights is None and not scatter:
+        raise ValueError("bag_backward_rows: weights=None needs weight_grad=False and ordered=False")
+    _need_cuda("bag_backward_rows", grad_out, indices, table, acc, touched, *(() if weights is None else (weights,)))
     N, K = indices.shape
     rows, D = table.shape
     if table.dtype not in _DT or acc.dtype != torch.float32 or tuple(acc.shape) != (rows, D) \
             or not acc.is_contiguous() or touched.dtype != torch.bool or touched.numel() != rows:
         raise ValueError("bag_backward_rows: table fp32/bf16 (rows, D), acc contiguous fp32 (rows, D), touched "
                          "(rows,) bool")
-    if tuple(grad_out.shape) != (N, D) or tuple(weights.shape) != (N, K):
+    if tuple(grad_out.shape) != (N, D) or (weights is not None and tuple(weights.shape) != (N, K)):
         raise ValueError("bag_backward_rows: grad_out must be (N, D) and weights (N, K)")
     g = grad_out.float().contiguous()
     idx = indices.to(torch.int64).contiguous()
-    w = weights.float().contiguous()
+    w = None if weights is None else weights.float().contiguous()
+    L = _lib.lib()
+    if scatter:
+        rc = L.smlm_bag_backward_rows(g.data_ptr(), idx.data_ptr(), None if w is None else w.data_ptr(), N, K, None,
+                                      _DT[table.dtype], rows, D, acc.data_ptr(), touched.data_ptr(), None, _stream(g))
+        _lib.check(rc, "smlm_bag_backward_rows")
+        return None
     table = table.contiguous()
     gw = torch.empty(N, K, dtype=torch.float32, device=g.device)
-    L = _lib.lib()
     if ordered and rows < 0xFFFFFFFF and N * K < 0x7FFFFFFF:
         size = ctypes.c_size_t(0)
         _lib.check(L.smlm_bag_backward_sorted_workspace(N, K, rows, D, ctypes.byref(size)),

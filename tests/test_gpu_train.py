@@ -170,6 +170,70 @@ def test_bag_backward_ordered_is_repeatable_and_matches_oracle(N, K, rows, hot):
     np.testing.assert_array_equal(touched, rt)
 
 
+@pytest.mark.parametrize("N,K,D,rows,weighted,offset", [
+    (700, 1, 24, 50, False, 0),        # the Engram width: 2.7 rows per wavefront, many repeated rows
+    (300, 3, 24, 100000, True, 0),     # K > 1 (lookup i reads gradient row i / K), weights
+    (50, 2, 100, 30, True, 0),
+    (40, 1, 256, 20, False, 0),
+    (33, 2, 98, 40, True, 0),
+    (20, 1, 384, 10, False, 0),
+    (64, 1, 24, 30, False, 1),         # gradient rows not 16-byte aligned
+])
+def test_bag_backward_without_weight_grad_matches_oracle(N, K, D, rows, weighted, offset):
+    """weight_grad=False (smlm_bag_backward_rows with gw NULL, the Engram backward): the lookups' w * g scattered
+    with fp32 atomic adds and no table read; the accumulator within 1e-5 of the summed magnitudes, the flags exact,
+    an index outside the table adding nothing."""
+    note(f"bag backward without weight grad N={N} K={K} D={D} rows={rows} weighted={weighted} offset={offset}")
+    g = torch.Generator().manual_seed(N * D + K)
+    idx = torch.randint(0, rows, (N, K), generator=g)
+    idx[0, 0] = -1
+    idx[-1, -1] = rows                                      # outside the table: no update
+    w = torch.rand(N, K, generator=g) if weighted else torch.ones(N, K)
+    G = torch.randn(N, D, generator=g)
+    acc0 = torch.randn(rows, D, generator=g) * 0.1
+    t0 = torch.zeros(rows, dtype=torch.bool)
+    acc, touched = acc0.to(DEV), t0.to(DEV)
+    store = torch.zeros(N * D + offset, device=DEV)
+    gd = store[offset:].view(N, D)
+    gd.copy_(G.to(DEV))
+    out = KR.bag_backward_rows(gd, idx.to(DEV), w.to(DEV) if weighted else None, torch.empty(rows, D, device=DEV),
+                               acc, touched, ordered=False, weight_grad=False)
+    torch.cuda.synchronize()
+    assert out is None
+    ok = (idx >= 0) & (idx < rows)
+    _, racc, rt = T.bag_backward_rows(G.numpy(), torch.where(ok, idx, 0).numpy(), (w * ok).numpy(),
+                                      np.zeros((rows, D), np.float32), acc0.numpy(), t0.numpy())
+    rt[:] = False
+    rt[idx[ok].numpy()] = True
+    mag = np.zeros((rows, D))
+    np.add.at(mag, idx[ok].numpy(), (np.abs(w.numpy())[..., None] * np.abs(G.numpy())[:, None])[ok.numpy()])
+    np.testing.assert_array_less(np.abs(acc.cpu().numpy() - racc), 1e-5 * (mag + np.abs(acc0.numpy())) + 1e-7)
+    np.testing.assert_array_equal(touched.cpu().numpy(), rt)
+
+
+def test_bag_backward_without_weight_grad_arguments():
+    """The C-ABI's null-pointer rules for the weight-gradient-free form, and the wrapper's refusal of weights=None
+    where a weight gradient or the ordered form is asked for."""
+    note("bag backward without weight grad: arguments")
+    from smlm_hip import _lib
+    L = _lib.lib()
+    g = torch.ones(4, 24, device=DEV)
+    idx = torch.zeros(4, 1, dtype=torch.int64, device=DEV)
+    acc = torch.zeros(10, 24, device=DEV)
+    touched = torch.zeros(10, dtype=torch.uint8, device=DEV)
+    gw = torch.empty(4, 1, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    assert L.smlm_bag_backward_rows(g.data_ptr(), idx.data_ptr(), None, 4, 1, None, _lib.F32, 10, 24,
+                                    acc.data_ptr(), touched.data_ptr(), None, s) == _lib.OK
+    assert L.smlm_bag_backward_rows(g.data_ptr(), idx.data_ptr(), None, 4, 1, acc.data_ptr(), _lib.F32, 10, 24,
+                                    acc.data_ptr(), touched.data_ptr(), gw.data_ptr(), s) == _lib.EINVAL
+    torch.cuda.synchronize()
+    assert acc[0].sum().item() == 4 * 24 and touched.cpu().tolist() == [1] + [0] * 9
+    for kw in ({"ordered": True, "weight_grad": False}, {"ordered": False, "weight_grad": True}):
+        with pytest.raises(ValueError):
+            KR.bag_backward_rows(g, idx, None, acc, acc, touched.bool(), **kw)
+
+
 def test_bag_backward_sorted_workspace_checks():
     """The workspace query and its use: a too-small or unaligned workspace is refused before any launch."""
     note("ordered bag backward workspace checks")
