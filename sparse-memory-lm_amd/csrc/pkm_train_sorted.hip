@@ -29,9 +29,16 @@ constexpr int kSegsInFlight = 4;                    // segments whose rows are l
 constexpr int kLookAhead = 8;                       // lookups of a segment whose gradient rows are loaded together
 constexpr int kMaxDSorted = 512;
 // the stable radix sort in onesweep passes (one per 8 key bits) at every size: rocPRIM's default sorts fewer than
-// 2^20 items by block sort + merge passes (18 launches at 524,288 lookups, ~125 us against ~3 radix passes)
-using SortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
-                                              rocprim::default_config, 0>;
+// 2^20 items by block sort + merge passes (18 launches at 524,288 lookups, ~125 us against ~3 radix passes).  The
+// passes: 1024 threads x 4 keys per block, ranks by the match algorithm (timing probe of 524,288 21-bit keys, sorted
+// and stable each time: 59 us, against 96 us for rocPRIM's onesweep defaults; 65-70 us at 2-3 or 8 keys per thread,
+// 512 threads 68 us, 7-bit digits 60 us, 11-bit digits 67-85 us; 8-bit digits above 4 keys per thread at 512 or 1024
+// threads need more than the 160 KB of LDS without the match ranks)
+using SortConfig = rocprim::radix_sort_config<
+    rocprim::default_config, rocprim::default_config,
+    rocprim::radix_sort_onesweep_config<rocprim::kernel_config<1024, 4>, rocprim::kernel_config<1024, 4>, 8,
+                                        rocprim::block_radix_rank_algorithm::match>,
+    0>;
 
 template <bool F32>
 __device__ __forceinline__ float table_value(const void *table, int64_t i) {
