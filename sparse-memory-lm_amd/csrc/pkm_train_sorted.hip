@@ -25,7 +25,7 @@ namespace {
 constexpr int kRunThreads = 256;                    // 4 wavefronts, one sorted chunk each
 constexpr int kChunk = kWave;                       // sorted lookups per wavefront
 constexpr int kChunksPerBlock = kRunThreads / kWave;
-constexpr int kSegsInFlight = 4;                    // segments whose rows are loaded together
+constexpr int kSegsInFlight = 3;                    // segments whose rows are loaded together
 constexpr int kLookAhead = 8;                       // lookups of a segment whose gradient rows are loaded together
 constexpr int kMaxDSorted = 512;
 // the stable radix sort in onesweep passes (one per 8 key bits) at every size: rocPRIM's default sorts fewer than
