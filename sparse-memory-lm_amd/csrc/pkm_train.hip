@@ -660,7 +660,9 @@ void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, u
                  const float *grad_scale, int64_t rows, int D, float step_size, float bc2_sqrt, float b1, float b2,
                  float omb1, float omb2, float eps, hipStream_t stream) {
   int64_t blocks = (rows + kTrainWaves - 1) / kTrainWaves;
-  if (blocks > 65536) blocks = 65536;   // grid-stride beyond 262,144 rows at a time
+  // one row per wavefront up to 1,048,576 rows, grid-stride beyond (B-1M, all rows touched: fp32 2.53 -> 2.43 ms,
+  // bf16 1.91 -> 1.78, int8 1.62 -> 1.52 against 4 rows per wavefront; 16 rows per wavefront 2.59 / 1.95 / 1.62)
+  if (blocks > (1 << 18)) blocks = 1 << 18;
   const dim3 grid((unsigned)blocks), block(kTrainThreads);
   constexpr int kMomentBytes = STATE == 0 ? 4 : STATE == 1 ? 2 : 1;
   const bool vec = D % 4 == 0 && aligned(p, 16) && aligned(acc, 16) && aligned(m, 4 * kMomentBytes) &&
