@@ -25,6 +25,7 @@ namespace {
 constexpr int kRunThreads = 256;                    // 4 wavefronts, one sorted chunk each
 constexpr int kChunk = kWave;                       // sorted lookups per wavefront
 constexpr int kChunksPerBlock = kRunThreads / kWave;
+constexpr int kCrossWaves = 4;                      // wavefronts of a crossing-run workgroup
 constexpr int kSegsInFlight = 3;                    // segments whose rows are loaded together
 constexpr int kLookAhead = 8;                       // lookups of a segment whose gradient rows are loaded together
 constexpr int kMaxDSorted = 512;
@@ -220,10 +221,10 @@ __device__ __forceinline__ int64_t run_last(const uint32_t *__restrict__ keys, i
 // adds the run's partial sums: its own (slot 1), then the continuation chunks' (slot 0), wavefront i taking chunks
 // c + 1 + i, c + 5 + i, .. (8 loads in flight), the four sums added in wavefront order through LDS.
 template <int CPL>
-__global__ void __launch_bounds__(kRunThreads)
+__global__ void __launch_bounds__(kCrossWaves * kWave)
     cross_runs_kernel(const uint32_t *__restrict__ keys, int64_t L, int D, const float *__restrict__ partial,
                       const uint8_t *__restrict__ cross, float *__restrict__ acc, uint8_t *__restrict__ touched) {
-  __shared__ float sSum[kChunksPerBlock][CPL * kWave];
+  __shared__ float sSum[kCrossWaves][CPL * kWave];
   const int64_t c = blockIdx.x;
   if (!cross[c]) return;                            // workgroup-uniform, before the barrier
   const int lane = lane_id(), wave = threadIdx.x / kWave;
@@ -233,11 +234,11 @@ __global__ void __launch_bounds__(kRunThreads)
   float s[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) s[e] = 0.f;
-  for (int64_t c0 = c + 1 + wave; c0 <= c_last; c0 += kChunksPerBlock * 8) {
+  for (int64_t c0 = c + 1 + wave; c0 <= c_last; c0 += kCrossWaves * 8) {
     float pv[8][CPL];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const int64_t cq = c0 + (int64_t)q * kChunksPerBlock;
+      const int64_t cq = c0 + (int64_t)q * kCrossWaves;
 #pragma unroll
       for (int e = 0; e < CPL; ++e) {
         const int d = lane + kWave * e;
@@ -259,7 +260,7 @@ __global__ void __launch_bounds__(kRunThreads)
     const int d = lane + kWave * e;
     float t = d < D ? partial[(2 * c + 1) * (int64_t)D + d] : 0.f;   // the run's first chunk, then the rest
 #pragma unroll
-    for (int i = 0; i < kChunksPerBlock; ++i) t += sSum[i][e * kWave + lane];
+    for (int i = 0; i < kCrossWaves; ++i) t += sSum[i][e * kWave + lane];
     if (d < D) acc[ro + d] += t;
   }
   if (lane == 0) touched[r] = 1;
@@ -315,7 +316,7 @@ void launch_runs(const float *grad_out, const float *w, int K, const void *table
   else
     hipLaunchKernelGGL((runs_kernel<false, CPL>), grid, block, 0, s, grad_out, w, K, table, rows, D, keys, vals, L,
                        acc, touched, gw, partial, cross);
-  hipLaunchKernelGGL((cross_runs_kernel<CPL>), dim3((unsigned)nchunks), block, 0, s, keys, L, D,
+  hipLaunchKernelGGL((cross_runs_kernel<CPL>), dim3((unsigned)nchunks), dim3(kCrossWaves * kWave), 0, s, keys, L, D,
                      (const float *)partial, (const uint8_t *)cross, acc, touched);
 }
 
