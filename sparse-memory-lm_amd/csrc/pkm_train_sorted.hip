@@ -10,8 +10,10 @@
 //      of w x g in registers, added in lookup order.  A run that starts and ends in the chunk updates its
 //      accumulator row with a plain read-add-write (the row has no other writer); a segment at a chunk edge that
 //      continues into the neighbouring chunk leaves its sum in a per-chunk partial;
-//   4. cross_runs_kernel: for each run that crosses chunk edges, a workgroup finds the run's end in the sorted keys
-//      (a 64-lane search), adds the partials of its chunks in a fixed order and updates the row once.
+//   4. group_sums_kernel: the partials of each group of 32 chunks that lies inside one run, summed in a fixed order;
+//   5. cross_runs_kernel: for each run that crosses chunk edges, a workgroup finds the run's end in the sorted keys
+//      (a 64-lane search), adds the partials of its chunks (whole groups by their sums) in a fixed order and updates
+//      the row once.
 // Every accumulator row has one writer and every sum a fixed order, so the result does not depend on scheduling
 // (the atomic form in pkm_train.hip is faster to start but pays contention on rows read by many tokens).
 #include <cstring>
@@ -26,6 +28,7 @@ constexpr int kRunThreads = 256;                    // 4 wavefronts, one sorted 
 constexpr int kChunk = kWave;                       // sorted lookups per wavefront
 constexpr int kChunksPerBlock = kRunThreads / kWave;
 constexpr int kCrossWaves = 4;                      // wavefronts of a crossing-run workgroup
+constexpr int kGroup = 32;                          // chunks per group sum (runs spanning whole groups)
 constexpr int kSegsInFlight = 3;                    // segments whose rows are loaded together
 constexpr int kLookAhead = 8;                       // lookups of a segment whose gradient rows are loaded together
 constexpr int kMaxDSorted = 512;
@@ -217,13 +220,71 @@ __device__ __forceinline__ int64_t run_last(const uint32_t *__restrict__ keys, i
   return a;
 }
 
+// Rows first .. last of base (row i at i * stride), wavefront `wave` of kCrossWaves taking rows first + wave,
+// first + wave + kCrossWaves, .. with 8 loads in flight, added to s in that order.
+template <int CPL>
+__device__ __forceinline__ void add_rows(const float *__restrict__ base, int64_t stride, int64_t first, int64_t last,
+                                         int D, int wave, int lane, float (&s)[CPL]) {
+  for (int64_t i0 = first + wave; i0 <= last; i0 += kCrossWaves * 8) {
+    float pv[8][CPL];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t i = i0 + (int64_t)q * kCrossWaves;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) {
+        const int d = lane + kWave * e;
+        pv[q][e] = i <= last && d < D ? base[i * stride + d] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) s[e] += pv[q][e];
+  }
+}
+
+// One workgroup per group of kGroup chunks that lies inside one run with the run going on at both sides (its key
+// at the positions just before and just after the group): the group's chunks each hold one segment of that run,
+// whose sum is their slot-0 partial; their sum, in the order of add_rows and then wavefront order, is the group's.
+// A hot row's run of hundreds of chunks then costs its crossing workgroup a few dozen loads instead of one per chunk.
+template <int CPL>
+__global__ void __launch_bounds__(kCrossWaves * kWave)
+    group_sums_kernel(const uint32_t *__restrict__ keys, int64_t L, uint32_t rows, int D,
+                      const float *__restrict__ partial, float *__restrict__ gsum) {
+  __shared__ float sSum[kCrossWaves][CPL * kWave];
+  const int64_t g = blockIdx.x;
+  const int64_t p0 = g * kGroup * kChunk, p1 = p0 + kGroup * kChunk;   // the group's positions [p0, p1)
+  if (p0 == 0 || p1 >= L) return;                   // workgroup-uniform, before the barrier
+  const uint32_t r = keys[p0];
+  if (r >= rows || keys[p0 - 1] != r || keys[p1 - 1] != r || keys[p1] != r) return;
+  const int lane = lane_id(), wave = threadIdx.x / kWave;
+  float s[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) s[e] = 0.f;
+  add_rows<CPL>(partial, 2 * (int64_t)D, g * kGroup, g * kGroup + kGroup - 1, D, wave, lane, s);
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) sSum[wave][e * kWave + lane] = s[e];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    const int d = lane + kWave * e;
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kCrossWaves; ++i) t += sSum[i][e * kWave + lane];
+    if (d < D) gsum[g * D + d] = t;
+  }
+}
+
 // One workgroup per chunk; a chunk whose last segment starts a run that continues into the next chunk (cross[c])
-// adds the run's partial sums: its own (slot 1), then the continuation chunks' (slot 0), wavefront i taking chunks
-// c + 1 + i, c + 5 + i, .. (8 loads in flight), the four sums added in wavefront order through LDS.
+// adds the run's partial sums: its own (slot 1), then the continuation chunks' (slot 0) and whole groups' sums
+// (add_rows: wavefront i taking every fourth row, 8 loads in flight), the four sums added in wavefront order
+// through LDS.
 template <int CPL>
 __global__ void __launch_bounds__(kCrossWaves * kWave)
     cross_runs_kernel(const uint32_t *__restrict__ keys, int64_t L, int D, const float *__restrict__ partial,
-                      const uint8_t *__restrict__ cross, float *__restrict__ acc, uint8_t *__restrict__ touched) {
+                      const float *__restrict__ gsum, const uint8_t *__restrict__ cross, float *__restrict__ acc,
+                      uint8_t *__restrict__ touched) {
   __shared__ float sSum[kCrossWaves][CPL * kWave];
   const int64_t c = blockIdx.x;
   if (!cross[c]) return;                            // workgroup-uniform, before the barrier
@@ -234,21 +295,16 @@ __global__ void __launch_bounds__(kCrossWaves * kWave)
   float s[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) s[e] = 0.f;
-  for (int64_t c0 = c + 1 + wave; c0 <= c_last; c0 += kCrossWaves * 8) {
-    float pv[8][CPL];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t cq = c0 + (int64_t)q * kCrossWaves;
-#pragma unroll
-      for (int e = 0; e < CPL; ++e) {
-        const int d = lane + kWave * e;
-        pv[q][e] = cq <= c_last && d < D ? partial[2 * cq * (int64_t)D + d] : 0.f;
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-#pragma unroll
-      for (int e = 0; e < CPL; ++e) s[e] += pv[q][e];
+  // the continuation chunks c + 1 .. c_last: whole groups of kGroup chunks strictly before c_last by their group
+  // sums (group_sums_kernel wrote every such group: the run covers it and the positions on both sides of it), the
+  // chunks before and after them one by one
+  const int64_t g_lo = (c + 1 + kGroup - 1) / kGroup, g_hi = c_last / kGroup - 1;
+  if (g_lo <= g_hi) {
+    add_rows<CPL>(partial, 2 * (int64_t)D, c + 1, g_lo * kGroup - 1, D, wave, lane, s);
+    add_rows<CPL>(gsum, D, g_lo, g_hi, D, wave, lane, s);
+    add_rows<CPL>(partial, 2 * (int64_t)D, (g_hi + 1) * kGroup, c_last, D, wave, lane, s);
+  } else {
+    add_rows<CPL>(partial, 2 * (int64_t)D, c + 1, c_last, D, wave, lane, s);
   }
 #pragma unroll
   for (int e = 0; e < CPL; ++e) sSum[wave][e * kWave + lane] = s[e];
@@ -266,9 +322,10 @@ __global__ void __launch_bounds__(kCrossWaves * kWave)
   if (lane == 0) touched[r] = 1;
 }
 
-// workspace: keys and values in / out, partials, cross flags, the sort's own storage (each 256-byte aligned)
+// workspace: keys and values in / out, partials, group sums, cross flags, the sort's own storage (each 256-byte
+// aligned)
 struct SortedLayout {
-  size_t keys_in, vals_in, keys_out, vals_out, partial, cross, sort_tmp, sort_bytes, total;
+  size_t keys_in, vals_in, keys_out, vals_out, partial, gsum, cross, sort_tmp, sort_bytes, total;
 };
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
@@ -282,7 +339,8 @@ int sorted_layout(int64_t L, int64_t rows, int D, SortedLayout &lay) {
   lay.keys_out = lay.vals_in + l4;
   lay.vals_out = lay.keys_out + l4;
   lay.partial = lay.vals_out + l4;
-  lay.cross = lay.partial + align256(nchunks * 2 * (size_t)D * 4);
+  lay.gsum = lay.partial + align256(nchunks * 2 * (size_t)D * 4);
+  lay.cross = lay.gsum + align256((nchunks + kGroup - 1) / kGroup * (size_t)D * 4);
   lay.sort_tmp = lay.cross + align256(nchunks);
   size_t bytes = 0;
   const hipError_t e = rocprim::radix_sort_pairs<SortConfig>(nullptr, bytes, (const uint32_t *)nullptr, (uint32_t *)nullptr,
@@ -307,7 +365,7 @@ int check_sorted_shape(const char *what, int64_t N, int K, int64_t rows, int D) 
 template <int CPL>
 void launch_runs(const float *grad_out, const float *w, int K, const void *table, bool f32, uint32_t rows, int D,
                  const uint32_t *keys, const uint32_t *vals, int64_t L, float *acc, uint8_t *touched, float *gw,
-                 float *partial, uint8_t *cross, hipStream_t s) {
+                 float *partial, float *gsum, uint8_t *cross, hipStream_t s) {
   const int64_t nchunks = (L + kChunk - 1) / kChunk;
   const dim3 grid((unsigned)((nchunks + kChunksPerBlock - 1) / kChunksPerBlock)), block(kRunThreads);
   if (f32)
@@ -316,8 +374,10 @@ void launch_runs(const float *grad_out, const float *w, int K, const void *table
   else
     hipLaunchKernelGGL((runs_kernel<false, CPL>), grid, block, 0, s, grad_out, w, K, table, rows, D, keys, vals, L,
                        acc, touched, gw, partial, cross);
+  hipLaunchKernelGGL((group_sums_kernel<CPL>), dim3((unsigned)((nchunks + kGroup - 1) / kGroup)),
+                     dim3(kCrossWaves * kWave), 0, s, keys, L, rows, D, (const float *)partial, gsum);
   hipLaunchKernelGGL((cross_runs_kernel<CPL>), dim3((unsigned)nchunks), dim3(kCrossWaves * kWave), 0, s, keys, L, D,
-                     (const float *)partial, (const uint8_t *)cross, acc, touched);
+                     (const float *)partial, (const float *)gsum, (const uint8_t *)cross, acc, touched);
 }
 
 }  // namespace
@@ -364,7 +424,7 @@ extern "C" int smlm_bag_backward_sorted(const float *grad_out, const int64_t *id
   unsigned char *ws = (unsigned char *)workspace;
   uint32_t *keys_in = (uint32_t *)(ws + lay.keys_in), *vals_in = (uint32_t *)(ws + lay.vals_in);
   uint32_t *keys = (uint32_t *)(ws + lay.keys_out), *vals = (uint32_t *)(ws + lay.vals_out);
-  float *partial = (float *)(ws + lay.partial);
+  float *partial = (float *)(ws + lay.partial), *gsum = (float *)(ws + lay.gsum);
   uint8_t *cross = ws + lay.cross;
   hipLaunchKernelGGL(keys_kernel, dim3((unsigned)((L + 255) / 256)), dim3(256), 0, s, idx, L, (uint32_t)rows,
                      keys_in, vals_in);
@@ -374,9 +434,12 @@ extern "C" int smlm_bag_backward_sorted(const float *grad_out, const int64_t *id
   if (e != hipSuccess) return fail(SMLM_EHIP, "smlm_bag_backward_sorted: sort: %s", hipGetErrorString(e));
   const bool f32 = table_dtype == SMLM_F32;
   const uint32_t r32 = (uint32_t)rows;
-  if (D <= 128) launch_runs<2>(grad_out, w, K, table, f32, r32, D, keys, vals, L, acc, touched, gw, partial, cross, s);
-  else if (D <= 256) launch_runs<4>(grad_out, w, K, table, f32, r32, D, keys, vals, L, acc, touched, gw, partial, cross, s);
-  else if (D <= 384) launch_runs<6>(grad_out, w, K, table, f32, r32, D, keys, vals, L, acc, touched, gw, partial, cross, s);
-  else launch_runs<8>(grad_out, w, K, table, f32, r32, D, keys, vals, L, acc, touched, gw, partial, cross, s);
+#define SMLM_RUNS(CPL)                                                                                          \
+  launch_runs<CPL>(grad_out, w, K, table, f32, r32, D, keys, vals, L, acc, touched, gw, partial, gsum, cross, s)
+  if (D <= 128) SMLM_RUNS(2);
+  else if (D <= 256) SMLM_RUNS(4);
+  else if (D <= 384) SMLM_RUNS(6);
+  else SMLM_RUNS(8);
+#undef SMLM_RUNS
   return launch_status("smlm_bag_backward_sorted");
 }
