@@ -137,11 +137,14 @@ def test_bag_backward_rows_index_outside_table(ordered):
 
 
 @pytest.mark.parametrize("N,K,rows,hot", [(256, 128, 1000, 0.5), (1, 5, 10, 0.0), (1, 64, 3, 0.0), (5, 13, 7, 0.9),
-                                          (1, 65, 2, 0.0), (300, 1, 40, 0.0)])
+                                          (1, 65, 2, 0.0), (300, 1, 40, 0.0),
+                                          # one run over ~28 whole 32-chunk groups (added by their group sums)
+                                          (512, 128, 50, 0.9)])
 def test_bag_backward_ordered_is_repeatable_and_matches_oracle(N, K, rows, hot):
     """The ordered bag backward gives the same bits on every call (each accumulator row has one writer, runs across
-    64-lookup chunks add their partial sums in chunk order), matches the oracle, and covers a row read by half of
-    all lookups (its run spans hundreds of chunks), lookups fewer than a chunk, exactly one chunk and one more."""
+    64-lookup chunks add their partial sums in a fixed order), matches the oracle, and covers a row read by half of
+    all lookups (its run spans hundreds of chunks), one read by 90% of 65,536 lookups (whole 32-chunk groups),
+    lookups fewer than a chunk, exactly one chunk and one more."""
     note(f"ordered bag backward N={N} K={K} rows={rows} hot={hot}")
     D = 384
     g = torch.Generator().manual_seed(N * K + rows)
