@@ -656,7 +656,57 @@ def event_time_each_ms(prep, fn, reps):
     return sum(a.elapsed_time(b) for a, b in pairs) / reps
 
 
-def train_kernels(dev, reps):
+def train_cpu_baseline(res):
+    """The reference's torch path of the training side on the host cores (oracle/torch_path.py: the torch branch of
+    the row-sparse bag backward, smlm/sparse_values.py:66-104, and the fp32 torch path of LazyRowAdam, 271-306) at
+    train_kernels' B-1M shape, on a bounded sample: the bag backward over 512 of the micro-batch's 4,096 tokens (all
+    128 uniform lookups each; median of 3), the lazy Adam as the reference steps it, one dense torch.optim.Adam step
+    over the whole 1,048,576 x 384 table with the rows a 32,768-token step reads touched (the first step, which
+    creates the moments, untimed; mean of the next 2).  Each figure sits beside the GPU's in the same unit."""
+    import torch
+    import oracle.torch_path as TP
+    rows, D, Kl, n = 1 << 20, 384, 128, 512
+    g = torch.Generator().manual_seed(5)
+    table = torch.empty(rows, D).normal_(0.0, 0.02, generator=g)
+    acc = torch.zeros(rows, D)
+    touched = torch.zeros(rows, dtype=torch.bool)
+    idx = torch.randint(0, rows, (n, Kl), generator=g)
+    gout = torch.randn(n, D, generator=g)
+    w = torch.softmax(torch.randn(n, 4, 32, generator=g), -1).view(n, Kl)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        TP.bag_backward_rows(gout, idx, w, table, acc, touched)
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    gpu_ms = res["bag_backward_uniform"]["ms"]
+    out = {"bag_backward": {"value": n * Kl / dt, "unit": "lookups/s", "cores": torch.get_num_threads(),
+                            "kind": "port", "gpu_value": 4096 * Kl / gpu_ms * 1e3,
+                            "sample": f"512 tokens x 128 uniform lookups into the 1,048,576 x 384 fp32 table "
+                                      f"({dt * 1e3:.1f} ms; the GPU's 4,096-token micro-batch {gpu_ms:.3f} ms)"}}
+    del idx, gout, w
+    mask = torch.zeros(rows, dtype=torch.bool)
+    mask[torch.randint(0, rows, (8 * 4096 * Kl,), generator=g)] = True
+    hot = int(mask.sum())
+    param = torch.nn.Parameter(table)
+    adam = torch.optim.Adam([param], lr=1e-3, betas=(0.9, 0.95), eps=1e-8)
+    times = []
+    for _ in range(3):
+        acc.fill_(1e-3)
+        touched.copy_(mask)
+        t0 = time.perf_counter()
+        TP.lazy_adam_fp32_step(param, adam, acc, touched)
+        times.append(time.perf_counter() - t0)
+    dt = sum(times[1:]) / 2
+    gpu_ms = res["lazy_adam_fp32"]["ms"]
+    out["lazy_adam_fp32"] = {"value": hot / dt, "unit": "touched rows/s", "cores": torch.get_num_threads(),
+                             "kind": "port", "gpu_value": hot / gpu_ms * 1e3,
+                             "sample": f"the whole step: {hot:,} of 1,048,576 rows touched ({dt * 1e3:.0f} ms per "
+                                       f"step; the GPU's {gpu_ms:.3f} ms)"}
+    return out
+
+
+def train_kernels(dev, reps, cpu=False):
     """The training side of the lookup at the reference's training shape (one micro-batch = 4 x 1024 tokens, 4
     heads x top-32 = 128 lookups per token, B-1M fp32 value table 1,048,576 x 384): the row-sparse bag backward on
     uniform and Zipf(1.1) indices (the ordered form, and the atomic form as ms_atomic), the lazy row Adam (fp32 / bf16 / int8 moments) on the rows a 32,768-token step
@@ -720,6 +770,8 @@ def train_kernels(dev, reps):
     res["select_backward_config2"] = {"ms": ms, "alg_bytes": alg, "alg_GBps": alg / ms / 1e6}
     del idx, wsel, gs, gw
     torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = train_cpu_baseline(res)
     return res
 
 
@@ -1101,10 +1153,10 @@ def main():
                 "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": lk["score_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS}
         line["offload_config3"] = phase("offload", lambda: offload_tiers(model, dev, args.reps),
                                         when=model is not None)
-        tr = phase("train", lambda: train_kernels(dev, args.reps))
+        tr = phase("train", lambda: train_kernels(dev, args.reps, cpu="cpu" in phases))
         if tr is not None:
             for v in tr.values():
-                if isinstance(v, dict):
+                if isinstance(v, dict) and "alg_GBps" in v:
                     v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
         line["train_kernels"] = tr
         line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps))

@@ -8,6 +8,8 @@ reference's key names:
   lm_forward      smlm/model.py:63-118, 156-163, 266-293: RMSNorm, RoPE, causal attention with a dict KV cache,
                   SwiGLU, tied lm_head
   greedy_decode   the decode loop of smlm/train.py:283-301 (prefill, then one token per step, argmax)
+  bag_backward_rows      the torch branch of the row-sparse bag backward, smlm/sparse_values.py:66-104
+  lazy_adam_fp32_step    the fp32 torch path of LazyRowAdam.step, smlm/sparse_values.py:271-306
 Everything runs in the dtype of the given weights (fp32 or fp64).  torch.topk breaks ties in an unspecified
 order, exactly like the reference's torch path; on tie-free scores it selects what pk_select selects.
 """
@@ -135,3 +137,55 @@ def greedy_decode(sd, cfg, prompt, new_tokens):
         nxt = logits[:, -1:].argmax(-1)
         out.append(nxt)
     return torch.cat(out, 1)
+
+
+ACC_CHUNK = 1 << 18     # lookups per accumulation chunk (smlm/sparse_values.py:23)
+
+
+def bag_backward_rows(grad_out, idx, w, table, acc, touched):
+    """The reference's torch branch of the row-sparse bag backward (smlm/sparse_values.py:66-104), in place on acc and
+    touched: the bags' offsets and lookup -> bag map as its forward builds them (76-81), the per-sample-weight
+    gradient by aten's embedding-bag backward (98-99), each lookup's w * g added into acc by index_put_ with
+    accumulation in chunks of 2^18 lookups (100-102), then the rows flagged (103).  grad_out (N, D), idx (N, K)
+    int64, w (N, K), table (rows, D), acc (rows, D), touched (rows,) bool.  Returns gw (N, K)."""
+    n, j = idx.shape
+    flat = idx.reshape(-1).contiguous()
+    wf = w.reshape(-1).to(table.dtype).contiguous()
+    offsets = torch.arange(0, n * j, j)
+    offset2bag = torch.arange(n).repeat_interleave(j)
+    g = grad_out.contiguous().to(acc.dtype)
+    gw = torch.ops.aten._embedding_bag_per_sample_weights_backward(g.to(table.dtype), table, flat, offsets,
+                                                                   offset2bag, 0, -1)
+    for a in range(0, flat.numel(), ACC_CHUNK):
+        contrib = g.index_select(0, offset2bag[a:a + ACC_CHUNK]).mul_(wf[a:a + ACC_CHUNK, None].to(g.dtype))
+        acc.index_put_((flat[a:a + ACC_CHUNK],), contrib, accumulate=True)
+    touched[flat] = True
+    return gw.view(n, j)
+
+
+def lazy_adam_fp32_step(param, adam, acc, touched, grad_scale=1.0):
+    """The fp32 torch path of LazyRowAdam.step (smlm/sparse_values.py:271-306) for one table: param an
+    nn.Parameter, adam its torch.optim.Adam; the unread rows' parameters and moments are kept aside (287-290), the
+    accumulator (scaled) becomes the gradient of one dense Adam step (291-296), the kept rows are put back (297-303)
+    and the accumulator and flags cleared (306, RowStore.reset at 34-41)."""
+    if not bool(touched.any()):
+        return
+    state = adam.state[param]
+    unread = (~touched).nonzero().squeeze(1)
+    keep = [param.data.index_select(0, unread)]
+    if state:
+        keep += [state["exp_avg"].index_select(0, unread), state["exp_avg_sq"].index_select(0, unread)]
+    if grad_scale != 1.0:
+        acc.mul_(grad_scale)
+    param.grad = acc
+    adam.step()
+    param.grad = None
+    param.data.index_put_((unread,), keep[0])
+    if len(keep) == 3:
+        state["exp_avg"].index_put_((unread,), keep[1])
+        state["exp_avg_sq"].index_put_((unread,), keep[2])
+    else:
+        state["exp_avg"].index_fill_(0, unread, 0.0)
+        state["exp_avg_sq"].index_fill_(0, unread, 0.0)
+    acc.zero_()
+    touched.zero_()

@@ -192,3 +192,53 @@ def test_code_division_by_corrected_reciprocal_is_the_ieee_quotient():
     assert np.any(c * (np.float32(1) / np.float32(127)) != c / np.float32(127))
     c = np.arange(0, 256, dtype=np.float32)
     assert np.any(c * (np.float32(1) / np.float32(255)) != c / np.float32(255))
+
+
+def test_torch_path_bag_backward_matches_the_oracle():
+    """oracle/torch_path.bag_backward_rows (the reference's torch branch, bench.py's CPU baseline of the bag backward)
+    against the numpy restatement: the per-sample-weight gradient and the accumulator within fp32 rounding, the flags
+    exact, with rows read several times in a bag and across bags."""
+    import oracle.torch_path as TP
+    g = torch.Generator().manual_seed(3)
+    N, K, D, rows = 64, 16, 48, 200
+    idx = torch.randint(0, rows, (N, K), generator=g)
+    idx[0, :4] = 5
+    idx[-1, 0] = 5
+    w, G = torch.rand(N, K, generator=g), torch.randn(N, D, generator=g)
+    table = torch.randn(rows, D, generator=g)
+    acc0 = torch.randn(rows, D, generator=g) * 0.1
+    t0 = torch.zeros(rows, dtype=torch.bool)
+    t0[rows - 1] = True
+    acc, t = acc0.clone(), t0.clone()
+    gw = TP.bag_backward_rows(G, idx, w, table, acc, t)
+    rgw, racc, rt = T.bag_backward_rows(G.numpy(), idx.numpy(), w.numpy(), table.numpy(), acc0.numpy(), t0.numpy())
+    np.testing.assert_allclose(gw.numpy(), rgw, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(acc.numpy(), racc, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(t.numpy(), rt)
+
+
+def test_torch_path_lazy_adam_fp32_matches_the_oracle():
+    """oracle/torch_path.lazy_adam_fp32_step (the reference's fp32 torch path: one dense torch.optim.Adam step with the
+    unread rows put back, bench.py's CPU baseline of the table optimizer) against the numpy lazy Adam over two steps
+    with different touched rows: touched rows within fp32 rounding, untouched rows unchanged bit for bit."""
+    import oracle.torch_path as TP
+    rng = np.random.default_rng(4)
+    rows, D, lr, b1, b2, eps = 50, 16, 1e-3, 0.9, 0.95, 1e-8
+    p = rng.standard_normal((rows, D)).astype(np.float32)
+    param = torch.nn.Parameter(torch.tensor(p))
+    adam = torch.optim.Adam([param], lr=lr, betas=(b1, b2), eps=eps)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for step in (1, 2):
+        touched = rng.random(rows) < 0.6
+        acc = np.where(touched[:, None], rng.standard_normal((rows, D)), 0).astype(np.float32)
+        before = param.detach().clone()
+        acc_t, t_t = torch.tensor(acc), torch.tensor(touched)
+        TP.lazy_adam_fp32_step(param, adam, acc_t, t_t)
+        p, m, v, _, _ = T.lazy_adam(p, m, v, acc, touched, 1.0, step, lr, b1, b2, eps)
+        got = param.detach().numpy()
+        np.testing.assert_allclose(got[touched], p[touched], rtol=1e-6, atol=1e-7)
+        np.testing.assert_array_equal(got[~touched], before.numpy()[~touched])
+        # torch forms the first moment with lerp_, the oracle as b1 m + (1 - b1) g: equal up to fp32 rounding
+        np.testing.assert_allclose(adam.state[param]["exp_avg"].numpy(), m, rtol=1e-6, atol=1e-7)
+        assert not acc_t.any() and not t_t.any()
