@@ -551,7 +551,45 @@ def offload_tiers(model, dev, reps, staged_steps=32):
     return res
 
 
-def engram_lookup(dev, reps):
+def engram_cpu_baseline(ng, c, res):
+    """The reference's path of the Engram lookup on the host cores over the whole workload: the n-gram hash
+    (oracle/engram_oracle.ngram_rows, the int64 arithmetic of smlm/engram.py:60-73), the fp32 row gather (index_select
+    into the 16 x 524,287 x 24 table) and the row-sparse backward with unit weights (oracle/torch_path.bag_backward_rows,
+    the torch branch of smlm/sparse_values.py:66-104 at K = 1).  Medians of 3, each beside the GPU's time."""
+    import torch
+    import oracle.engram_oracle as EO
+    import oracle.torch_path as TP
+    cc, mult = c.cpu().numpy(), ng.mult.cpu().numpy()
+    g = torch.Generator().manual_seed(11)
+    table = torch.randn(ng.n_lookups * ng.rows, 24, generator=g) * 0.2
+    acc = torch.zeros_like(table)
+    touched = torch.zeros(table.shape[0], dtype=torch.bool)
+
+    def median_s(fn):
+        t = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return sorted(t)[1]
+
+    rows = torch.from_numpy(EO.ngram_rows(cc, mult, ng.orders, ng.heads, ng.rows)).reshape(-1)
+    M = rows.numel()
+    grad = torch.randn(M, 24, generator=g)
+    ones = torch.ones(M, 1)
+    t_hash = median_s(lambda: EO.ngram_rows(cc, mult, ng.orders, ng.heads, ng.rows))
+    t_gather = median_s(lambda: table.index_select(0, rows))
+    t_back = median_s(lambda: TP.bag_backward_rows(grad, rows.view(-1, 1), ones, table, acc, touched))
+    out = {}
+    for name, t, gpu_ms in (("hash", t_hash, res["ms_hash"]), ("gather_fp32", t_gather, res["gather_fp32"]["ms"]),
+                            ("backward_fp32", t_back, res["backward_fp32"]["ms"])):
+        out[name] = {"value": M / t, "unit": "lookups/s", "cores": torch.get_num_threads(), "kind": "port",
+                     "gpu_value": M / gpu_ms * 1e3, "sample": f"the whole workload, {M:,} lookups ({t * 1e3:.2f} ms; "
+                                                            f"the GPU {gpu_ms:.4f} ms)"}
+    return out
+
+
+def engram_lookup(dev, reps, cpu=False):
     """The Engram row lookup at the reference's default shape (orders 2 and 3, 8 heads each = 16 lookups per token,
     524,287 rows per head, head_dim 24) over 8 x 2048 tokens: the hash kernel, the row gather (fp32 and bf16
     tables) and the row-sparse backward (weight 1 per lookup) into an fp32 accumulator."""
@@ -589,6 +627,8 @@ def engram_lookup(dev, reps):
             del acc, touched, grad
         del table
     torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = engram_cpu_baseline(ng, c, res)
     return res
 
 
@@ -1159,7 +1199,7 @@ def main():
                 if isinstance(v, dict) and "alg_GBps" in v:
                     v["hbm_frac"] = v["alg_GBps"] / HBM_PEAK_GBS
         line["train_kernels"] = tr
-        line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps))
+        line["engram_lookup"] = phase("engram", lambda: engram_lookup(dev, args.reps, cpu="cpu" in phases))
     finally:
         if errors:
             line["phase_errors"] = errors

@@ -1,6 +1,7 @@
 """CPU oracle of the Engram n-gram memory -- TEST INFRASTRUCTURE ONLY.
 
-Only tests/ may import this module, as the checker; the product path (smlm_hip) never calls it.
+Only tests/ (as the checker) and bench.py's CPU baseline may import this module; the product path (smlm_hip) never
+calls it.
 
   ngram_rows       smlm/engram.py:60-73    row of every hash head for every position: XOR over the n-gram's
                                             tokens of token x multiplier (int64, wrap-around), x ^= x >> 17
