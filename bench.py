@@ -702,7 +702,8 @@ def train_cpu_baseline(res):
     train_kernels' B-1M shape, on a bounded sample: the bag backward over 512 of the micro-batch's 4,096 tokens (all
     128 uniform lookups each; median of 3), the lazy Adam as the reference steps it, one dense torch.optim.Adam step
     over the whole 1,048,576 x 384 table with the rows a 32,768-token step reads touched (the first step, which
-    creates the moments, untimed; mean of the next 2).  Each figure sits beside the GPU's in the same unit."""
+    creates the moments, untimed; mean of the next 2), and the selection backward (PKSelect.backward, smlm/kernels.py:
+    253-266) on 2,048 of config 2's tokens (median of 3).  Each figure sits beside the GPU's in the same unit."""
     import torch
     import oracle.torch_path as TP
     rows, D, Kl, n = 1 << 20, 384, 128, 512
@@ -743,6 +744,24 @@ def train_cpu_baseline(res):
                              "kind": "port", "gpu_value": hot / gpu_ms * 1e3,
                              "sample": f"the whole step: {hot:,} of 1,048,576 rows touched ({dt * 1e3:.0f} ms per "
                                        f"step; the GPU's {gpu_ms:.3f} ms)"}
+    del param, adam, table, acc, touched, mask
+    # the selection backward at config 2's shape on 2,048 of its 16,384 tokens (PKSelect.backward's torch ops)
+    n, H, NK, knn = 2048, 4, 2048, 32
+    idx = torch.randint(0, NK * NK, (n, H, knn), generator=g)
+    wsel = torch.softmax(torch.randn(n, H, knn, generator=g), -1)
+    gs = torch.randn(n, H, knn, generator=g).to(torch.bfloat16)
+    gwv = torch.randn(n, H, knn, generator=g)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        TP.select_backward(idx, wsel, gs, gwv, NK, torch.bfloat16)
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    gpu_ms = res["select_backward_config2"]["ms"]
+    out["select_backward_config2"] = {"value": n / dt, "unit": "tok/s", "cores": torch.get_num_threads(),
+                                      "kind": "port", "gpu_value": 16384 / gpu_ms * 1e3,
+                                      "sample": f"2,048 of the 16,384 tokens ({dt * 1e3:.1f} ms; the GPU's 16,384 "
+                                                f"{gpu_ms:.3f} ms)"}
     return out
 
 

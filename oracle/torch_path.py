@@ -8,6 +8,7 @@ reference's key names:
   lm_forward      smlm/model.py:63-118, 156-163, 266-293: RMSNorm, RoPE, causal attention with a dict KV cache,
                   SwiGLU, tied lm_head
   greedy_decode   the decode loop of smlm/train.py:283-301 (prefill, then one token per step, argmax)
+  select_backward        PKSelect.backward, smlm/kernels.py:253-266 (torch ops in the reference too)
   bag_backward_rows      the torch branch of the row-sparse bag backward, smlm/sparse_values.py:66-104
   lazy_adam_fp32_step    the fp32 torch path of LazyRowAdam.step, smlm/sparse_values.py:271-306
 Everything runs in the dtype of the given weights (fp32 or fp64).  torch.topk breaks ties in an unspecified
@@ -137,6 +138,23 @@ def greedy_decode(sd, cfg, prompt, new_tokens):
         nxt = logits[:, -1:].argmax(-1)
         out.append(nxt)
     return torch.cat(out, 1)
+
+
+def select_backward(idx, w, g_scores, g_w, nk, dtype):
+    """PKSelect.backward (smlm/kernels.py:253-266): the softmax backward of the knn weights plus the scores' own
+    gradient, rounded to the scores' dtype, scattered (fp32 sums) into dense (N, H, nk) gradients of both halves and
+    rounded once.  idx (N, H, knn) int64, w (N, H, knn) fp32, g_scores of dtype or None, g_w fp32 or None."""
+    dl = torch.zeros_like(w)
+    if g_w is not None:
+        dl = w * (g_w - (w * g_w).sum(-1, keepdim=True))
+    if g_scores is not None:
+        dl = dl + g_scores.float()
+    ds = dl.to(dtype).float()
+    N, H, _ = idx.shape
+    z = torch.zeros(N, H, nk, dtype=torch.float32)
+    ds1 = z.scatter_add(-1, idx // nk, ds).to(dtype)
+    ds2 = z.scatter_add_(-1, idx % nk, ds).to(dtype)
+    return ds1, ds2
 
 
 ACC_CHUNK = 1 << 18     # lookups per accumulation chunk (smlm/sparse_values.py:23)

@@ -242,3 +242,27 @@ def test_torch_path_lazy_adam_fp32_matches_the_oracle():
         # torch forms the first moment with lerp_, the oracle as b1 m + (1 - b1) g: equal up to fp32 rounding
         np.testing.assert_allclose(adam.state[param]["exp_avg"].numpy(), m, rtol=1e-6, atol=1e-7)
         assert not acc_t.any() and not t_t.any()
+
+
+def test_torch_path_select_backward_matches_the_oracle():
+    """oracle/torch_path.select_backward (the reference's PKSelect.backward in torch ops, bench.py's CPU baseline of the
+    selection backward) against the numpy restatement, bf16 and fp32 scores: within one bf16 ulp / fp32 rounding of
+    the per-sub-key sums, unselected sub-keys exactly zero."""
+    import oracle.torch_path as TP
+    g = torch.Generator().manual_seed(8)
+    N, H, NK, knn = 6, 3, 64, 16
+    for dtype in (torch.bfloat16, torch.float32):
+        s1 = torch.randn(N, H, NK, generator=g).to(dtype)
+        s2 = torch.randn(N, H, NK, generator=g).to(dtype)
+        sc, idx = TP.pkm_select_torch(s1.float(), s2.float(), knn)
+        w = torch.softmax(sc, -1)
+        gs = torch.randn(N, H, knn, generator=g).to(dtype)
+        gw = torch.randn(N, H, knn, generator=g)
+        d1, d2 = TP.select_backward(idx, w, gs, gw, NK, dtype)
+        bf16 = dtype == torch.bfloat16
+        r1, r2 = T.select_backward(idx.numpy(), w.numpy(), gs.float().numpy(), gw.numpy(), NK, bf16)
+        for got, ref in ((d1, r1), (d2, r2)):
+            got = got.float().numpy()
+            tol = np.abs(ref) * (2.0 ** -7 if bf16 else 1e-6) + 1e-7
+            assert np.all(np.abs(got - ref) <= tol)
+            assert not got[ref == 0].any()
