@@ -392,8 +392,8 @@ __global__ void __launch_bounds__(kSortThreads)
 // ---------------------------------------------------------------------------------------------------------------
 // state: 0 fp32 moments, 1 bf16 moments, 2 int8 / uint8 codes + fp32 row scales.  Column layout of a row in its
 // wavefront: chunk c, lane l, element i holds column c * 64 * V + l * V + i.  V = 4 (D a multiple of 4) gives each
-// lane 16-byte fp32, 8-byte bf16 and 4-byte int8 accesses; V = 2 (int8 state, 256 < D <= 384: 3 chunks, no idle
-// slots at D = 384) 8-, 4- and 2-byte accesses; V = 1 is the fallback for other widths.
+// lane 16-byte fp32, 8-byte bf16 and 4-byte int8 accesses; V = 2 (fp32 or int8 state, 256 < D <= 384: 3 chunks,
+// no idle slots at D = 384) 8- and 2-byte accesses; V = 1 is the fallback for other widths.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -671,8 +671,8 @@ void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, u
   hipLaunchKernelGGL((lazy_adam_kernel<STATE, V, NC>), grid, block, 0, stream, p, m, v, ms, vs, acc, touched,   \
                      grad_scale, rows, D, step_size, bc2_sqrt, b1, b2, omb1, omb2, eps)
   if (vec && D <= 256) SMLM_ADAM(4, 1);
-  else if (STATE == 2 && vec && D <= 384) {
-    if constexpr (STATE == 2) SMLM_ADAM(2, 3);  // V = 2 only with int8 codes (the bf16 helpers have no V = 2 form)
+  else if (STATE != 1 && vec && D <= 384) {
+    if constexpr (STATE != 1) SMLM_ADAM(2, 3);  // V = 2 with fp32 moments or int8 codes (no bf16 V = 2 form)
   }
   else if (vec) SMLM_ADAM(4, 2);
   else if (D <= 128) SMLM_ADAM(1, 2);
