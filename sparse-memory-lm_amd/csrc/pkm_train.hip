@@ -392,8 +392,8 @@ __global__ void __launch_bounds__(kSortThreads)
 // ---------------------------------------------------------------------------------------------------------------
 // state: 0 fp32 moments, 1 bf16 moments, 2 int8 / uint8 codes + fp32 row scales.  Column layout of a row in its
 // wavefront: chunk c, lane l, element i holds column c * 64 * V + l * V + i.  V = 4 (D a multiple of 4) gives each
-// lane 16-byte fp32, 8-byte bf16 and 4-byte int8 accesses; V = 2 (fp32 or int8 state, 256 < D <= 384: 3 chunks,
-// no idle slots at D = 384) 8- and 2-byte accesses; V = 1 is the fallback for other widths.
+// lane 16-byte fp32, 8-byte bf16 and 4-byte int8 accesses; V = 2 (256 < D <= 384: 3 chunks, no idle slots at
+// D = 384) 8-, 4- and 2-byte accesses; V = 1 is the fallback for other widths.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
@@ -424,6 +424,10 @@ __device__ __forceinline__ void load_bf16v(const uint16_t *q, bool in, float *x)
     const u32x2 t = in ? *(const u32x2 *)q : u32x2{0u, 0u};
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = bf16_bits_to_f32((t[i / 2] >> (16 * (i % 2))) & 0xFFFFu);
+  } else if constexpr (V == 2) {
+    const uint32_t t = in ? *(const uint32_t *)q : 0u;
+    x[0] = bf16_bits_to_f32(t & 0xFFFFu);
+    x[1] = bf16_bits_to_f32(t >> 16);
   } else {
     x[0] = in ? bf16_bits_to_f32(*q) : 0.f;
   }
@@ -433,6 +437,8 @@ __device__ __forceinline__ void store_bf16v(uint16_t *q, const float *x) {
   if constexpr (V == 4) {
     *(u32x2 *)q = u32x2{bf16_bits_rtne(x[0]) | (bf16_bits_rtne(x[1]) << 16),
                         bf16_bits_rtne(x[2]) | (bf16_bits_rtne(x[3]) << 16)};
+  } else if constexpr (V == 2) {
+    *(uint32_t *)q = bf16_bits_rtne(x[0]) | (bf16_bits_rtne(x[1]) << 16);
   } else {
     *q = (uint16_t)bf16_bits_rtne(x[0]);
   }
@@ -671,9 +677,7 @@ void launch_adam(float *p, void *m, void *v, float *ms, float *vs, float *acc, u
   hipLaunchKernelGGL((lazy_adam_kernel<STATE, V, NC>), grid, block, 0, stream, p, m, v, ms, vs, acc, touched,   \
                      grad_scale, rows, D, step_size, bc2_sqrt, b1, b2, omb1, omb2, eps)
   if (vec && D <= 256) SMLM_ADAM(4, 1);
-  else if (STATE != 1 && vec && D <= 384) {
-    if constexpr (STATE != 1) SMLM_ADAM(2, 3);  // V = 2 with fp32 moments or int8 codes (no bf16 V = 2 form)
-  }
+  else if (vec && D <= 384) SMLM_ADAM(2, 3);
   else if (vec) SMLM_ADAM(4, 2);
   else if (D <= 128) SMLM_ADAM(1, 2);
   else if (D <= 256) SMLM_ADAM(1, 4);
