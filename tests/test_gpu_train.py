@@ -237,6 +237,44 @@ def test_bag_backward_without_weight_grad_arguments():
             KR.bag_backward_rows(g, idx, None, acc, acc, touched.bool(), **kw)
 
 
+def test_bag_backward_ordered_hot_run_with_indices_outside_the_table():
+    """A run over whole 32-chunk groups next to lookups whose index is outside the table (they sort after every row,
+    so they share the last chunks with the hot run's end): the valid lookups match the oracle, the others add
+    nothing and get a NaN weight gradient, and two calls give the same bits."""
+    note("ordered bag backward: hot run over chunk groups and indices outside the table")
+    N, K, D, rows = 512, 128, 384, 50
+    g = torch.Generator().manual_seed(21)
+    idx = torch.randint(0, rows, (N, K), generator=g)
+    idx[torch.rand(N, K, generator=g) < 0.9] = rows - 1          # the hot row sorts last among the valid ones
+    bad = torch.rand(N, K, generator=g) < 0.003
+    idx[bad] = rows                                              # outside the table
+    w = torch.rand(N, K, generator=g)
+    table = torch.randn(rows, D, generator=g)
+    G = torch.randn(N, D, generator=g)
+    acc0 = torch.randn(rows, D, generator=g) * 0.1
+    outs = []
+    for _ in range(2):
+        acc, touched = acc0.to(DEV), torch.zeros(rows, dtype=torch.bool, device=DEV)
+        gw = KR.bag_backward_rows(G.to(DEV), idx.to(DEV), w.to(DEV), table.to(DEV), acc, touched)
+        outs.append((gw.cpu(), acc.cpu(), touched.cpu()))
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+    assert torch.equal(torch.isnan(outs[0][0]), bad) and torch.equal(outs[0][0][~bad], outs[1][0][~bad])
+    ok = ~bad
+    rgw, racc, rt = T.bag_backward_rows(G.numpy(), torch.where(ok, idx, 0).numpy(), (w * ok).numpy(), table.numpy(),
+                                        acc0.numpy(), np.zeros(rows, dtype=bool))
+    rt[:] = False
+    rt[idx[ok].numpy()] = True
+    gw, acc, touched = (t.numpy() for t in outs[0])
+    mag_gw = np.abs(G.numpy()) @ np.abs(table.numpy()).T
+    okn = ok.numpy()
+    lim = 1e-5 * np.take_along_axis(mag_gw, torch.where(ok, idx, 0).numpy(), 1) + 1e-6
+    assert np.all(np.abs(gw[okn] - rgw[okn]) < lim[okn])
+    mag = np.zeros((rows, D))
+    np.add.at(mag, idx[ok].numpy(), (np.abs(w.numpy())[..., None] * np.abs(G.numpy())[:, None])[okn])
+    np.testing.assert_array_less(np.abs(acc - racc), 1e-5 * (mag + np.abs(acc0.numpy())) + 1e-7)
+    np.testing.assert_array_equal(touched, rt)
+
+
 def test_bag_backward_sorted_workspace_checks():
     """The workspace query and its use: a too-small or unaligned workspace is refused before any launch."""
     note("ordered bag backward workspace checks")
