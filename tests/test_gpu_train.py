@@ -309,7 +309,7 @@ def _adam_case(rows, D, seed):
 
 
 # D % 4 == 0 takes 4 adjacent columns per lane (one or two chunks of 256); other widths one column per lane
-@pytest.mark.parametrize("rows,D", [(300, 384), (40, 100), (64, 512), (50, 98), (20, 510)])
+@pytest.mark.parametrize("rows,D", [(300, 384), (40, 100), (64, 512), (50, 98), (20, 510), (45, 300)])
 def test_lazy_adam_fp32_bit_exact(rows, D):
     note(f"lazy adam fp32 rows={rows} D={D}")
     rng, p = _adam_case(rows, D, rows + D)
@@ -330,7 +330,7 @@ def test_lazy_adam_fp32_bit_exact(rows, D):
 
 
 @pytest.mark.parametrize("state,rows,D", [("bf16", 200, 384), ("int8", 200, 384), ("int8", 33, 100),
-                                          ("bf16", 30, 130), ("int8", 30, 98), ("int8", 40, 512), ("int8", 50, 300)])
+                                          ("bf16", 30, 130), ("int8", 30, 98), ("int8", 40, 512), ("int8", 50, 300), ("bf16", 45, 300)])
 def test_lazy_adam_lowmem_bit_exact(state, rows, D):
     note(f"lazy adam {state} rows={rows} D={D}")
     rng, p = _adam_case(rows, D, 7 * rows + D)
